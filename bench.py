@@ -1,0 +1,371 @@
+"""Benchmark: BitLinear portion of a batch-32 BitNet b1.58 2B decode step on one MI355X.
+
+A step is the 30-layer chain of the model's BitLinear launches at M = 32
+tokens: per layer the fused RMSNorm->QKV (2560->3840), o_proj (2560->2560,
+attn_sub_norm prologue, residual epilogue), gate||up (2560->2x6912,
+post-attention RMSNorm prologue, relu^2*up epilogue) and down (6912->2560,
+ffn_sub_norm prologue, residual epilogue).  Weights are random-init ternary
+(latents ~N(0, 0.02), absmean-quantised on the device), RMSNorm gains ~N(1,
+0.1), activations ~N(0, 1): synthetic, seeded.  The attention core between
+QKV and o_proj is not part of the BitLinear path; o_proj reads a seeded
+stand-in buffer.  The step is captured once in a HIP graph and replayed.
+
+Printed JSON (one line): value = algorithmic HBM bytes of a step / step time
+(GB/s), ms_per_step = BitLinear ms per decode step, plus the roofline of the
+dominant kernel (the gate||up GEMM) measured with HIP events on the launch
+stream, the prefill MFMA-i8 utilisation, and the CPU oracle timed on the
+host as a reported baseline.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(REPO, "bitnet-tt_amd"), REPO):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=30)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--kernel-reps", type=int, default=10, help="repetitions of the per-kernel event pass")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="approximate CPU-baseline sample length")
+    return ap.parse_args()
+
+
+# --------------------------------------------------------------- kernels ----
+class SplitLauncher:
+    """Launches a BitLinear as its two kernels (activation prologue, GEMM) so
+    the GEMM alone can be bracketed by events on the launch stream."""
+
+    def __init__(self, step, N, torch):
+        self.N, self.torch, self.step = N, torch, step
+        self.L = N.lib()
+        self.dev = step.device
+
+    def prologue(self, x, K, gamma, eps, ws):
+        N = self.N
+        M = x.numel() // K
+        rows = 32 * ((M + 31) // 32)
+        xa = ws["xa"]
+        N.check(self.L.btl_quant_absmax(N.ptr(x), M, K, K, N.ptr(gamma), eps, N.ptr(xa), N.ptr(ws["a_dq"]),
+                                        N.ptr(ws["rowsum"]), None, None, None, N.stream_of(self.dev)),
+                "btl_quant_absmax")
+        return M, rows
+
+    def gemm(self, M, K, w, out, epi, residual, ws):
+        N = self.N
+        sc, en, nseg = N.segments_arrays(w.segment_scales, w.segment_ends)
+        N.check(self.L.btl_gemm_i8t2(N.ptr(ws["xa"]), N.ptr(ws["a_dq"]), N.ptr(ws["rowsum"]), M, K, w.out_features,
+                                     N.ptr(w.data), sc, en, nseg, epi, N.ptr(residual), N.ptr(out), None,
+                                     N.ptr(ws["gemm"]), ws["gemm"].numel(), 0, N.stream_of(self.dev)),
+                "btl_gemm_i8t2")
+
+
+def kernel_event_timing(step, torch, N, reps):
+    """Average duration of each GEMM kind, measured with HIP events on the
+    launch stream.  For every kind the 30 layers' GEMMs (distinct weights,
+    265 MB for gate||up: more than the 256 MB last-level cache) are recorded
+    into a graph; a replay is bracketed by two events and divided by the
+    number of launches."""
+    c = step.config
+    dev = step.device
+    L = N.lib()
+    sl = SplitLauncher(step, N, torch)
+    kinds = {
+        "qkv": (c.hidden_size, lambda w: w.qkv, 0, step.hidden, step.qkv_out, None),
+        "o_proj": (c.num_attention_heads * c.head_dim, lambda w: w.o_proj, 0, step.attn_out, step.hidden, step.hidden),
+        "gate_up": (c.hidden_size, lambda w: w.gate_up, 1, step.hidden, step.ffn_h, None),
+        "down": (c.intermediate_size, lambda w: w.down, 0, step.ffn_h, step.hidden, step.hidden),
+    }
+    res = {}
+    s = torch.cuda.Stream(device=dev)
+    for name, (K, getw, epi, x, out, resid) in kinds.items():
+        w0 = getw(step.layers[0])
+        Nf = w0.out_features
+        ws = {
+            "xa": torch.empty(int(L.btl_act_bytes(32, K)), dtype=torch.uint8, device=dev),
+            "a_dq": torch.empty(32, dtype=torch.float32, device=dev),
+            "rowsum": torch.empty(32, dtype=torch.int32, device=dev),
+            "gemm": torch.zeros(max(int(L.btl_gemm_workspace_bytes(32, K, Nf, epi, 0)), 256), dtype=torch.uint8,
+                                device=dev),
+        }
+        xin = x.clone()
+        o = out.clone()
+        r = o if resid is not None else None
+        sl.prologue(xin, K, None, 0.0, ws)
+        torch.cuda.synchronize()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for lw in step.layers:  # warm the launch path once outside capture
+                sl.gemm(32, K, getw(lw), o, epi, r, ws)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for lw in step.layers:
+                sl.gemm(32, K, getw(lw), o, epi, r, ws)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        times = []
+        with torch.cuda.stream(s):
+            g.replay()
+            for _ in range(reps):
+                e0.record(s)
+                g.replay()
+                e1.record(s)
+                e1.synchronize()
+                times.append(e0.elapsed_time(e1) * 1e3 / len(step.layers))  # us per launch
+        torch.cuda.synchronize()
+        times.sort()
+        res[name] = {"us_per_launch_median": times[len(times) // 2], "us_per_launch_min": times[0], "K": K, "N": Nf}
+        del g
+    return res
+
+
+def gemm_algorithmic_bytes(M, K, N, epi, nseg, residual):
+    n_out = N // 2 if epi == 1 else N
+    b = K * N // 4 + 32 * K + 8 * 32 + 4 * nseg + 2 * M * n_out
+    if residual:
+        b += 2 * M * n_out
+    return b
+
+
+def prefill_mfma(torch, N, dev):
+    """MFMA-i8 utilisation of the prefill GEMM at the configured shapes."""
+    L = N.lib()
+    shapes = [(512, 2560, 3840), (512, 2560, 6912), (512, 2560, 2560), (512, 6912, 2560),
+              (2048, 2560, 3840), (2048, 2560, 6912), (2048, 2560, 2560), (2048, 6912, 2560)]
+    out = []
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(77)
+    for M, K, Nf in shapes:
+        KS = (K + 127) // 128
+        xa = torch.randint(-128, 128, (int(L.btl_act_bytes(M, K)),), generator=gen, device=dev,
+                           dtype=torch.int16).to(torch.int8)
+        a_dq = torch.full((32 * ((M + 31) // 32),), 0.01, device=dev)
+        rowsum = torch.zeros_like(a_dq, dtype=torch.int32)
+        copies = 4
+        wd = [torch.randint(0, 1 << 30, (Nf // 32, KS, 256), generator=gen, device=dev, dtype=torch.int32) & 0x55555555
+              for _ in range(copies)]  # codes 0/1 only: valid ternary offsets
+        o = torch.empty((M, Nf), dtype=torch.bfloat16, device=dev)
+        sc, en, nseg = N.segments_arrays([0.02], [Nf])
+        stream = N.stream_of(dev)
+
+        def launch(i):
+            N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(a_dq), N.ptr(rowsum), M, K, Nf, N.ptr(wd[i % copies]), sc, en,
+                                    nseg, 0, None, N.ptr(o), None, None, 0, 1, stream), "prefill gemm")
+
+        reps = 20
+        s = torch.cuda.Stream(device=dev)
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            stream = N.stream_of(dev)
+            for i in range(3):
+                launch(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            stream = N.stream_of(dev)
+            for i in range(reps):
+                launch(i)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            g.replay()
+            e0.record(s)
+            g.replay()
+            e1.record(s)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        del g
+        tops = 2.0 * M * K * Nf / (us * 1e-6) / 1e12
+        out.append({"M": M, "K": K, "N": Nf, "us": round(us, 2), "tops": round(tops, 1),
+                    "mfma_i8_util": round(tops / MFMA_I8_PEAK_TOPS, 4)})
+    return out
+
+
+# ------------------------------------------------------------ CPU baseline ----
+def cpu_baseline(step, torch, seconds):
+    """Scalar C oracle (one thread) on a bounded sample of the same workload:
+    whole decode layers (4 BitLinears at M = 32), run until `seconds` pass."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    orc.lib()
+    c = step.config
+
+    def wkn(pw):
+        return orc.devlayout_decode(pw.data.cpu().numpy().view(np.uint32), pw.in_features, pw.out_features)
+
+    def bits(t):
+        return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+    eps = step.eps
+    hidden = bits(step.hidden0)
+    attn = bits(step.attn_out)
+    per_layer = step.algorithmic_bytes()["layer"]
+    done, t_total = 0, 0.0
+    for i, w in enumerate(step.layers):
+        mats = (wkn(w.qkv), wkn(w.o_proj), wkn(w.gate_up), wkn(w.down))
+        g = [bits(t) for t in (w.input_layernorm, w.attn_sub_norm, w.post_attention_layernorm, w.ffn_sub_norm)]
+        t0 = time.perf_counter()
+        orc.bitlinear(hidden, mats[0], list(w.qkv.segment_scales), list(w.qkv.segment_ends), gamma_bf16=g[0],
+                      norm_eps=eps)
+        hidden = orc.bitlinear(attn, mats[1], list(w.o_proj.segment_scales), gamma_bf16=g[1], norm_eps=eps,
+                               residual_bf16=hidden)["out"]
+        r = orc.gate_up_relu2(hidden, mats[2], w.gate_up.segment_scales[0], w.gate_up.segment_scales[1],
+                              gamma_bf16=g[2], norm_eps=eps)
+        hidden = orc.bitlinear(r["h"], mats[3], list(w.down.segment_scales), gamma_bf16=g[3], norm_eps=eps,
+                               residual_bf16=hidden)["out"]
+        t_total += time.perf_counter() - t0
+        done += 1
+        if t_total >= seconds:
+            break
+    gbs = per_layer * done / t_total / 1e9
+    ms_step = t_total / done * len(step.layers) * 1e3
+    return {
+        "value": round(gbs, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{done} of {len(step.layers)} decode layers (4 BitLinears each, M=32) through the scalar C "
+                  f"oracle; {t_total:.1f} s; extrapolated {ms_step:.0f} ms per 30-layer step",
+        "ms_per_step_extrapolated": round(ms_step, 1),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: the BitLinear path is measured on a single MI355X "
+              f"(--gpus {args.gpus} is not supported).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from bitnet_tt import _native as N
+    from bitnet_tt.config import BitNet2B4TConfig
+    from bitnet_tt.decode import BitLinearDecodeStep
+
+    N.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = BitNet2B4TConfig()
+    t0 = time.time()
+    step = BitLinearDecodeStep.random_init(cfg, dev, seed=args.seed, num_layers=args.layers).alloc_buffers(seed=1)
+    torch.cuda.synchronize()
+    log(f"[bench] model ready: {args.layers} layers in {time.time() - t0:.1f} s; "
+        f"ternary split +1/0/-1 = {'/'.join(f'{v:.4f}' for v in step.ternary_split)}")
+
+    # warm-up (eager), then capture the step on a side stream
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(max(args.warmup, 1)):
+            step.reset_hidden()
+            step.step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        step.step()
+    with torch.cuda.stream(s):
+        for _ in range(args.warmup):
+            graph.replay()
+    torch.cuda.synchronize()
+    log("[bench] graph captured; timing")
+
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    with torch.cuda.stream(s):
+        for _ in range(args.steps):
+            graph.replay()
+    torch.cuda.synchronize()
+    t_el = time.perf_counter() - t_start
+    ms_per_step = t_el * 1e3 / args.steps
+    nbytes = step.algorithmic_bytes()
+    value = nbytes["step"] / (ms_per_step * 1e-3) / 1e9
+    log(f"[bench] {ms_per_step * 1e3:.1f} us per step, {value:.0f} GB/s")
+
+    kt = kernel_event_timing(step, torch, N, args.kernel_reps)
+    for name, r in kt.items():
+        log(f"[bench] {name}: {r['us_per_launch_median']:.2f} us per GEMM launch (median of {args.kernel_reps})")
+    gu = kt["gate_up"]
+    gu_bytes = gemm_algorithmic_bytes(32, gu["K"], gu["N"], 1, 2, False)
+    achieved = gu_bytes / (gu["us_per_launch_median"] * 1e-6) / 1e9
+    roofline = {
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "kernel": "k_gemm_decode<2,6,relu2> (gate||up 2560->2x6912, M=32)",
+        "bytes_per_launch": gu_bytes,
+        "us_per_launch": round(gu["us_per_launch_median"], 3),
+    }
+    gemm_us = {k: round(v["us_per_launch_median"], 3) for k, v in kt.items()}
+
+    prefill = None
+    if not args.no_prefill:
+        prefill = prefill_mfma(torch, N, dev)
+        for p in prefill:
+            log(f"[bench] prefill M={p['M']} K={p['K']} N={p['N']}: {p['us']} us, {p['tops']} TOPS, "
+                f"MFMA-i8 {100 * p['mfma_i8_util']:.1f}%")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (oracle) ...")
+        cpu = cpu_baseline(step, torch, args.cpu_seconds)
+        log(f"[bench] CPU: {cpu['sample']}")
+
+    line = {
+        "metric": "ternary GEMM HBM GB/s (% roofline) at M=32; BitLinear ms per batch-32 decode step",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8xternary->int32 (bf16 in/out)",
+        "data": "synthetic (seeded random-init ternary weights, N(0,1) activations)",
+        "config": {
+            "workload": f"BitLinear portion of a batch-32 BitNet b1.58 2B decode step ({args.layers} layers x "
+                        "4 fused BitLinear launches: RMSNorm->QKV 2560->3840, o_proj 2560->2560, "
+                        "gate||up 2560->2x6912 relu2, down 6912->2560), HIP-graph replay",
+            "batch": 32,
+            "layers": args.layers,
+            "bytes_per_step": nbytes["step"],
+            "step_roofline_frac": round(value / HBM_PEAK_GBS, 4),
+            "gemm_us_per_launch": gemm_us,
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "prefill_mfma": prefill,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

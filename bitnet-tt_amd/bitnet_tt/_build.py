@@ -1,0 +1,65 @@
+"""Build recipe of libbtl.so (the gfx950 BitLinear library).
+
+``build_native()`` compiles every HIP source under ``csrc/`` with hipcc for
+gfx950 into ``bitnet_tt/_lib/libbtl.so`` (in-tree, so it travels with the
+package).  It runs on a machine without a GPU: hipcc cross-compiles.
+"""
+
+from __future__ import annotations
+
+import glob
+import os
+import subprocess
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+_ROOT = os.path.dirname(_PKG)  # bitnet-tt_amd/
+_REPO = os.path.dirname(_ROOT)
+CSRC = os.path.join(_ROOT, "csrc")
+INCLUDE = os.path.join(_REPO, "include")
+OUT = os.path.join(_PKG, "_lib", "libbtl.so")
+
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # Every float multiply and add is rounded on its own: the kernels' numeric
+    # contract (RMS statistic order, epilogue rounding) depends on it.
+    "-ffp-contract=off",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    # No packed fp32 instructions in device code.
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
+        if cand and (os.path.sep not in cand or os.path.exists(cand)):
+            return cand
+    return "hipcc"
+
+
+def build_native(verbose: bool = False) -> str:
+    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    os.makedirs(os.path.dirname(OUT), exist_ok=True)
+    tmp = OUT + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-o", tmp, *sources]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    errs = "\n".join(ln for ln in proc.stderr.splitlines() if noise not in ln)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{' '.join(cmd)}\n{errs}")
+    if verbose and errs.strip():
+        print(errs)
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build_native(verbose=True))

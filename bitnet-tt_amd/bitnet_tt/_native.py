@@ -1,0 +1,160 @@
+"""ctypes binding of libbtl.so, the gfx950 BitLinear library (include/btl.h).
+
+The library is the only compute path of this package: every device operation
+goes through it, and a missing or stale library raises instead of falling back
+to anything else.  Tensors are passed as raw device pointers together with the
+current HIP stream of the calling thread (``torch.cuda.current_stream()``), so
+calls are stream-ordered and can be recorded into a HIP graph.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_lib", "libbtl.so")
+
+# Status codes and epilogue modes (include/btl.h).
+BTL_OK = 0
+STATUS_NAMES = {
+    1: "BTL_ERR_NULL",
+    2: "BTL_ERR_SHAPE",
+    3: "BTL_ERR_ALIGN",
+    4: "BTL_ERR_WORKSPACE",
+    5: "BTL_ERR_ARG",
+    6: "BTL_ERR_LAUNCH",
+}
+EPI_SCALE = 0
+EPI_RELU2_MUL = 1
+MAX_SEGMENTS = 4
+MAX_K = 16384
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> (argtypes, restype); the exported C ABI, one entry per declaration.
+EXPORTS = {
+    "btl_last_error": ([], ctypes.c_char_p),
+    "btl_version": ([], _I),
+    "btl_packed_tile_count": ([_I64, _I64], _I64),
+    "btl_packed_dram_bytes": ([_I64, _I64], _I64),
+    "btl_devlayout_words": ([_I64, _I64], _I64),
+    "btl_act_bytes": ([_I64, _I64], _I64),
+    "btl_choose_splitk": ([_I64, _I64, _I64, _I], _I),
+    "btl_gemm_workspace_bytes": ([_I64, _I64, _I64, _I, _I], _I64),
+    "btl_fused_workspace_bytes": ([_I64, _I64, _I64, _I, _I], _I64),
+    "btl_weight_quant_scratch_bytes": ([_I64], _I64),
+    "btl_weight_quant_ternary": ([_P, _I64, _F, _P, _P, _P, _SZ, _P], _I),
+    "btl_pack_tiles": ([_P, _I64, _I64, _P, _P], _I),
+    "btl_unpack_tiles": ([_P, _I64, _I64, _P, _P], _I),
+    "btl_repack": ([_P, _I64, _I64, _P, _P], _I),
+    "btl_quant_absmax": ([_P, _I64, _I64, _I64, _P, _F, _P, _P, _P, _P, _P, _P, _P], _I),
+    "btl_rmsnorm": ([_P, _I64, _I64, _I64, _P, _F, _P, _P], _I),
+    "btl_gemm_i8t2": (
+        [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I, _I, _P, _P, _P, _P, _SZ, _I, _P],
+        _I,
+    ),
+    "btl_bitlinear_fused": (
+        [_P, _I64, _I64, _I64, _P, _F, _P, _I64, _P, _P, _I, _I, _P, _P, _P, _P, _P, _SZ, _I, _P],
+        _I,
+    ),
+}
+
+
+class NativeLibraryError(RuntimeError):
+    """libbtl.so is missing or unusable; there is no other compute path."""
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+def lib() -> ctypes.CDLL:
+    """Load libbtl.so once and declare every exported signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise NativeLibraryError(
+                f"{LIB_PATH} is not built; build it with __graft_entry__.build() "
+                "(hipcc --offload-arch=gfx950). The BitLinear path has no other backend."
+            )
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in EXPORTS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    msg = lib().btl_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    if rc != BTL_OK:
+        raise RuntimeError(f"{what} failed with {STATUS_NAMES.get(rc, rc)}: {last_error()}")
+
+
+def ptr(t) -> ctypes.c_void_p | None:
+    """Device pointer of a tensor (None passes NULL)."""
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def require_cuda(t, name: str) -> None:
+    if t is None:
+        return
+    if not t.is_cuda:
+        raise ValueError(
+            f"{name} must be a tensor on a ROCm GPU device; the BitLinear path runs only "
+            "through the gfx950 kernels"
+        )
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def stream_of(device) -> ctypes.c_void_p:
+    import torch
+
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def segments_arrays(scales, ends):
+    """Host arrays for the per-segment epilogue scales."""
+    n = len(scales)
+    if not 1 <= n <= MAX_SEGMENTS:
+        raise ValueError(f"1..{MAX_SEGMENTS} weight-scale segments are supported, got {n}")
+    sc = (ctypes.c_float * n)(*[float(s) for s in scales])
+    en = (ctypes.c_int64 * n)(*[int(e) for e in ends])
+    return sc, en, n
+
+
+# Per (device, stream) workspace.  Calls on one stream are ordered, so they
+# can share it; the activation kernel of every fused call clears the split-K
+# counters it uses.
+_workspaces: dict = {}
+
+
+def workspace(device, nbytes: int):
+    import torch
+
+    stream = torch.cuda.current_stream(device)
+    key = (str(device), stream.cuda_stream)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        size = max(int(nbytes), 1 << 20)
+        buf = torch.zeros(size, dtype=torch.uint8, device=device)
+        _workspaces[key] = buf
+    return buf

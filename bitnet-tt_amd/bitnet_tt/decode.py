@@ -1,0 +1,181 @@
+"""BitLinear portion of a batch-32 BitNet decode step.
+
+Per layer the reference decode loop (src/bitnet_tt/inference/
+generator_batch32.py:713-761) issues four ternary-matmul launches:
+
+    qkv    = ternary_matmul(hidden, W_qkv, norm_weight=input_layernorm)   :721-727
+    hidden = hidden + o_proj(attn_sub_norm(attention(qkv)))               :739-749
+    hidden = hidden + down(ffn_sub_norm(relu(gate)^2 * up))               :752-756
+             with gate||up = BitLinear(post_attention_layernorm(hidden))
+
+Here every BitLinear is one fused launch sequence of libbtl.so and the
+remaining norms and residual adds ride along: attn_sub_norm and
+post_attention_layernorm become RMSNorm prologues, relu^2*up the gate||up
+epilogue, ffn_sub_norm the down prologue, and both residual adds epilogues.
+The attention core (RoPE, KV cache, SDPA) is outside this package: ``step``
+takes its output as an input buffer.
+
+All buffers are allocated once, so :meth:`BitLinearDecodeStep.step` is
+allocation-free and can be captured in a HIP graph.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+from .config import BitNetConfig
+from .ternary_matmul import PackedTernaryWeight, ternary_matmul_into
+
+
+@dataclass
+class LayerWeights:
+    qkv: PackedTernaryWeight
+    o_proj: PackedTernaryWeight
+    gate_up: PackedTernaryWeight
+    down: PackedTernaryWeight
+    input_layernorm: object  # bf16 [hidden]
+    attn_sub_norm: object  # bf16 [q_dim]
+    post_attention_layernorm: object  # bf16 [hidden]
+    ffn_sub_norm: object  # bf16 [ffn]
+
+
+def _quant_pack_device(latents_outin, device, segment_ends=None):
+    """float32 latent rows (out, in) on the device -> ternary -> device layout.
+
+    ``latents_outin`` is a list of (out_i, in) float32 device tensors that are
+    quantised separately (one absmean scale each) and concatenated along out."""
+    import torch
+
+    from .layers.bitlinear import pack_for_device
+    from .utils.quantization import weight_quant_ternary
+
+    qs, scales, ends = [], [], []
+    total = 0
+    for w in latents_outin:
+        q, s = weight_quant_ternary(w)
+        qs.append(q)
+        scales.append(s)
+        total += w.shape[0]
+        ends.append(total)
+    q = qs[0] if len(qs) == 1 else torch.cat(qs, dim=0)
+    return pack_for_device(q, device, tuple(scales), tuple(ends)), q
+
+
+def ternary_split(q) -> tuple[float, float, float]:
+    """Fractions of +1 / 0 / -1 in an int8 ternary tensor."""
+    n = q.numel()
+    pos = int((q == 1).sum().item())
+    neg = int((q == -1).sum().item())
+    return pos / n, (n - pos - neg) / n, neg / n
+
+
+class BitLinearDecodeStep:
+    """All BitLinear weights of a BitNet model plus the decode-step chain."""
+
+    def __init__(self, config: BitNetConfig, device, batch: int = 32):
+        self.config = config
+        self.device = device
+        self.batch = batch
+        self.layers: list[LayerWeights] = []
+        self.eps = config.rms_norm_eps
+        self.ternary_split = None
+
+    # -- weights ---------------------------------------------------------
+    @classmethod
+    def random_init(cls, config: BitNetConfig, device, seed: int = 0, batch: int = 32, latent_std: float = 0.02,
+                    gamma_std: float = 0.1, num_layers: int | None = None):
+        """Random-init weights of the architecture (the reference's demo init,
+        examples/demo.py:199-268, with latents ~N(0, latent_std) and RMSNorm
+        gains ~N(1, gamma_std)), generated and quantised on the device."""
+        import torch
+
+        self = cls(config, device, batch)
+        c = config
+        H, F, qd, kvd = c.hidden_size, c.intermediate_size, c.num_attention_heads * c.head_dim, c.num_kv_heads * c.head_dim
+        gen = torch.Generator(device=device)
+        counts = torch.zeros(3, dtype=torch.float64)
+        n_total = 0
+
+        def latent(rows, cols, tag):
+            gen.manual_seed(seed * 1000003 + tag)
+            return torch.randn((rows, cols), generator=gen, device=device, dtype=torch.float32) * latent_std
+
+        def gamma(n, tag):
+            gen.manual_seed(seed * 1000003 + tag)
+            g = 1.0 + gamma_std * torch.randn((n,), generator=gen, device=device, dtype=torch.float32)
+            return g.to(torch.bfloat16).contiguous()
+
+        L = c.num_layers if num_layers is None else num_layers
+        for i in range(L):
+            t = 100 * (i + 1)
+            qkv, q1 = _quant_pack_device([latent(qd, H, t + 1), latent(kvd, H, t + 2), latent(kvd, H, t + 3)], device)
+            o, q2 = _quant_pack_device([latent(H, qd, t + 4)], device)
+            gu, q3 = _quant_pack_device([latent(F, H, t + 5), latent(F, H, t + 6)], device)
+            dn, q4 = _quant_pack_device([latent(H, F, t + 7)], device)
+            for q in (q1, q2, q3, q4):
+                counts[0] += float((q == 1).sum().item())
+                counts[2] += float((q == -1).sum().item())
+                n_total += q.numel()
+            del q1, q2, q3, q4
+            self.layers.append(
+                LayerWeights(qkv, o, gu, dn, gamma(H, t + 8), gamma(qd, t + 9), gamma(H, t + 10), gamma(F, t + 11))
+            )
+        pos, neg = counts[0].item() / n_total, counts[2].item() / n_total
+        self.ternary_split = (pos, 1.0 - pos - neg, neg)
+        return self
+
+    # -- buffers -----------------------------------------------------------
+    def alloc_buffers(self, seed: int = 1):
+        """hidden [B, H], attention output stand-in [B, q_dim], qkv [B, qkv_dim],
+        FFN intermediate [B, F]; hidden and the attention buffer ~N(0, 1)."""
+        import torch
+
+        c = self.config
+        qd = c.num_attention_heads * c.head_dim
+        gen = torch.Generator(device=self.device)
+        gen.manual_seed(seed)
+        B = self.batch
+        self.hidden0 = torch.randn((B, c.hidden_size), generator=gen, device=self.device).to(torch.bfloat16)
+        self.hidden = self.hidden0.clone()
+        self.attn_out = torch.randn((B, qd), generator=gen, device=self.device).to(torch.bfloat16)
+        self.qkv_out = torch.empty((B, c.qkv_dim), dtype=torch.bfloat16, device=self.device)
+        self.ffn_h = torch.empty((B, c.intermediate_size), dtype=torch.bfloat16, device=self.device)
+        return self
+
+    def reset_hidden(self):
+        self.hidden.copy_(self.hidden0)
+
+    # -- the step ----------------------------------------------------------
+    def layer(self, i: int, hidden, attn_out, qkv_out, ffn_h):
+        """One layer's four BitLinear launch sequences, in place on ``hidden``."""
+        w = self.layers[i]
+        eps = self.eps
+        ternary_matmul_into(hidden, w.qkv, qkv_out, norm_weight=w.input_layernorm, norm_epsilon=eps)
+        ternary_matmul_into(attn_out, w.o_proj, hidden, norm_weight=w.attn_sub_norm, norm_epsilon=eps,
+                            residual=hidden)
+        ternary_matmul_into(hidden, w.gate_up, ffn_h, norm_weight=w.post_attention_layernorm, norm_epsilon=eps,
+                            epilogue="relu2_mul")
+        ternary_matmul_into(ffn_h, w.down, hidden, norm_weight=w.ffn_sub_norm, norm_epsilon=eps, residual=hidden)
+
+    def step(self):
+        for i in range(len(self.layers)):
+            self.layer(i, self.hidden, self.attn_out, self.qkv_out, self.ffn_h)
+        return self.hidden
+
+    # -- accounting ----------------------------------------------------------
+    def algorithmic_bytes(self) -> dict:
+        """Compulsory HBM bytes of one step's BitLinear launches: packed
+        weights, bf16 inputs and outputs, RMSNorm gains, scales (fp32 per
+        token and per weight segment), residual reads."""
+        c = self.config
+        B, H, F = self.batch, c.hidden_size, c.intermediate_size
+        qd = c.num_attention_heads * c.head_dim
+        per = {}
+        per["qkv"] = H * c.qkv_dim // 4 + 2 * B * H + 2 * B * c.qkv_dim + 2 * H + 4 * 3 + 4 * B
+        per["o_proj"] = qd * H // 4 + 2 * B * qd + 2 * B * H * 2 + 2 * qd + 4 + 4 * B
+        per["gate_up"] = H * 2 * F // 4 + 2 * B * H + 2 * B * F + 2 * H + 4 * 2 + 4 * B
+        per["down"] = F * H // 4 + 2 * B * F + 2 * B * H * 2 + 2 * F + 4 + 4 * B
+        per["layer"] = sum(per.values())
+        per["step"] = per["layer"] * len(self.layers)
+        per["weights_step"] = (H * c.qkv_dim + qd * H + H * 2 * F + F * H) // 4 * len(self.layers)
+        return per

@@ -1,0 +1,54 @@
+// Shared helpers of the gfx950 BitLinear library: bf16 conversion, error
+// reporting, argument checks and the quantities that describe the layouts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "btl.h"
+
+namespace btl {
+
+// ---- bf16 (round to nearest even; NaN stays a quiet NaN) --------------
+__host__ __device__ __forceinline__ float bf2f(uint16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+__host__ __device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// ---- errors -------------------------------------------------------------
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+int check_launch(const char* what);
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// ---- layout quantities ----------------------------------------------------
+// Weights: K rows (in_features) x N columns (out_features); the device layout
+// is N/32 column tiles x ceil(K/128) superblocks x 1 KiB.
+inline int64_t ksb(int64_t K) { return (K + 127) / 128; }
+// Activations: ceil(M/32) blocks of 32 rows, each ksb(K) superblocks x 4 KiB.
+inline int64_t mblocks(int64_t M) { return (M + 31) / 32; }
+inline int64_t round_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+// ---- GEMM plan (shared by sizing functions and launches) ----------------
+struct GemmPlan {
+  bool prefill;   // M > 32: tiled kernel over 32-row blocks
+  int tpw;        // decode: column tiles per workgroup (2 for the relu2 pair)
+  int ngroups;    // decode: workgroups along N
+  int splitk;     // decode: workgroups along K
+  int64_t ws_bytes;
+};
+GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req);
+
+// Byte offsets inside the fused workspace.
+struct FusedLayout {
+  int64_t xa, a_dq, rowsum, gemm_ws, total;
+};
+FusedLayout fused_layout(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req);
+
+}  // namespace btl

@@ -1,0 +1,165 @@
+/*
+ * btl.h -- C ABI of the MI355X (gfx950) BitLinear library (libbtl.so).
+ *
+ * The library is the drop-in for bitnet-tt's ternary-matmul path: the op
+ * `ttnn.experimental.ternary_matmul(a, b, use_packed_ternary=True,
+ * norm_weight=..., norm_epsilon=...)` called from
+ * src/bitnet_tt/layers/bitlinear.py:336-341 and
+ * src/bitnet_tt/inference/generator_batch32.py:721-727, its weight packing
+ * (src/bitnet_tt/kernels/pack.py:101-191) and the quantisers of
+ * src/bitnet_tt/utils/quantization.py:15-91.  Every entry point takes plain
+ * device pointers, sizes and a hipStream_t; nothing allocates device memory
+ * and every launch is ordered on the given stream, so the calls can be
+ * recorded into a HIP graph.  A non-zero return is an error code and
+ * btl_last_error() describes it (per calling thread).
+ *
+ * Data types: bf16 tensors are passed as uint16_t bit patterns.
+ */
+#ifndef BTL_H_
+#define BTL_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* btl_stream_t; /* == hipStream_t */
+
+/* ---- status codes ---------------------------------------------------- */
+enum {
+  BTL_OK = 0,
+  BTL_ERR_NULL = 1,      /* a required pointer is NULL                  */
+  BTL_ERR_SHAPE = 2,     /* sizes outside what the kernels support      */
+  BTL_ERR_ALIGN = 3,     /* pointer or leading dimension misaligned     */
+  BTL_ERR_WORKSPACE = 4, /* workspace smaller than btl_*_workspace_bytes */
+  BTL_ERR_ARG = 5,       /* other invalid argument (mode, segments ...)  */
+  BTL_ERR_LAUNCH = 6     /* the HIP runtime rejected a launch           */
+};
+
+/* ---- epilogue modes of the GEMM ------------------------------------- */
+enum {
+  /* out[m,n] = bf16(acc[m,n] * (seg_scale[seg(n)] * a_dq[m]))
+   * [+ residual[m,n] in bf16 when residual != NULL].
+   * Replaces ternary_matmul + Linear's multiply(out, weight_scale)
+   * (src/bitnet_tt/layers/bitlinear.py:336-352). */
+  BTL_EPI_SCALE = 0,
+  /* N = 2F (gate||up, src/bitnet_tt/layers/ffn.py:22-34); with
+   * g = bf16(acc[m,n] * s0 * a_dq[m]), u = bf16(acc[m,F+n] * s1 * a_dq[m]):
+   * out[m,n] = bf16(bf16(relu(g)^2) * u), out is [M, F]
+   * (src/bitnet_tt/layers/ffn.py:140-170). */
+  BTL_EPI_RELU2_MUL = 1
+};
+
+#define BTL_MAX_SEGMENTS 4
+#define BTL_MAX_K 16384
+
+/* Last error message of the calling thread ("" if none). */
+const char* btl_last_error(void);
+/* ABI version (major*100 + minor). */
+int btl_version(void);
+
+/* ---- sizes (host only, never touch the GPU) ---------------------------
+ * btl_packed_tile_count: src/bitnet_tt/kernels/pack.py:194-198.
+ * btl_packed_dram_bytes: src/bitnet_tt/kernels/pack.py:201-203.
+ * btl_devlayout_words:   uint32 words of the device weight layout of a
+ *                        K x N ternary matrix (N % 32 == 0).
+ * btl_act_bytes:         bytes of the quantised-activation buffer (32-row
+ *                        blocks x 128-column superblocks, int8).
+ * btl_gemm_workspace_bytes / btl_fused_workspace_bytes: workspace that
+ *   btl_gemm_i8t2 / btl_bitlinear_fused need for the given shape and
+ *   split-K factor (0 = the library's choice).                            */
+int64_t btl_packed_tile_count(int64_t in_features, int64_t out_features);
+int64_t btl_packed_dram_bytes(int64_t in_features, int64_t out_features);
+int64_t btl_devlayout_words(int64_t K, int64_t N);
+int64_t btl_act_bytes(int64_t M, int64_t K);
+int btl_choose_splitk(int64_t M, int64_t K, int64_t N, int epilogue);
+int64_t btl_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int epilogue, int splitk);
+int64_t btl_fused_workspace_bytes(int64_t M, int64_t K, int64_t N, int epilogue, int splitk);
+
+/* ---- weight preparation (load time) ---------------------------------- */
+
+/* Absmean ternary quantisation of a float32 latent weight with n elements
+ * (src/bitnet_tt/utils/quantization.py:15-57):
+ *   scale = max(mean(|W|), eps) with numpy's float32 summation order,
+ *   q = clip(round_half_even(W / scale), -1, 1).
+ * scratch: >= btl_weight_quant_scratch_bytes(n) bytes of device memory.
+ * scale_out: device pointer to one float.                                  */
+int64_t btl_weight_quant_scratch_bytes(int64_t n);
+int btl_weight_quant_ternary(const float* w, int64_t n, float eps, int8_t* q, float* scale_out,
+                             void* scratch, size_t scratch_bytes, btl_stream_t stream);
+
+/* pack_ternary_tilized (src/bitnet_tt/kernels/pack.py:101-155): quantised
+ * (out_features, in_features) int8 -> 2-bit tiles of the transposed matrix,
+ * tile t = kt*Nt + nt, faces f0..f3, codes {0:00,+1:01,-1:10}, MSB first,
+ * 256 bytes per tile.  packed: btl_packed_dram_bytes(in, out) bytes.     */
+int btl_pack_tiles(const int8_t* w_outin, int64_t out_features, int64_t in_features, uint8_t* packed,
+                   btl_stream_t stream);
+
+/* unpack_ternary_tilized values (src/bitnet_tt/kernels/pack.py:158-191):
+ * packed tiles -> (in_features, out_features) int8 in {-1,0,+1}
+ * (code 0b11 decodes to 0, kernels/device/reader_ternary_in1.cpp:43-56). */
+int btl_unpack_tiles(const uint8_t* packed, int64_t in_features, int64_t out_features, int8_t* w_kn,
+                     btl_stream_t stream);
+
+/* Repack the reference tile layout into the device layout the GEMM streams
+ * (replaces the BFP2 mantissa repack of src/bitnet_tt/layers/bitlinear.py:
+ * 221-248 / 272-297).  K = in_features (K % 32 == 0), N = out_features
+ * (N % 32 == 0).  wdev: btl_devlayout_words(K, N) words.                  */
+int btl_repack(const uint8_t* packed, int64_t K, int64_t N, uint32_t* wdev, btl_stream_t stream);
+
+/* ---- activations ----------------------------------------------------- */
+
+/* Per-token absmax int8 quantisation (src/bitnet_tt/utils/quantization.py:
+ * 60-91), optionally preceded by RMSNorm with gain gamma
+ * (HF BitNetRMSNorm order; src/bitnet_tt/layers/bitlinear.py:433-461):
+ *   y = gamma ? bf16(gamma * bf16(x / sqrt(mean(x^2) + norm_eps))) : x
+ *   a = max(max|y|, 1e-5); q = clip(rne(y * (127/a)), -128, 127)
+ * Outputs: xa (btl_act_bytes(M,K), blocked layout the GEMM reads),
+ * a_dq[32*ceil(M/32)] = a/127, rowsum[32*ceil(M/32)] = sum_k q,
+ * optional act_scale[M] = 127/a (the scale quantization.py returns),
+ * optional xq_rowmajor [M,K] int8 and y_rowmajor [M,K] bf16.
+ * x is [M,K] with row stride ldx elements (ldx % 8 == 0).                */
+int btl_quant_absmax(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint16_t* gamma,
+                     float norm_eps, int8_t* xa, float* a_dq, int32_t* rowsum, float* act_scale,
+                     int8_t* xq_rowmajor, uint16_t* y_rowmajor, btl_stream_t stream);
+
+/* RMSNorm alone (src/bitnet_tt/layers/bitlinear.py:356-461): y [M,K] bf16. */
+int btl_rmsnorm(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint16_t* gamma, float eps,
+                uint16_t* y, btl_stream_t stream);
+
+/* ---- the ternary GEMM ------------------------------------------------ */
+
+/* acc[m,n] = sum_k q[m,k] * w[k,n] in int32 (exact), then the epilogue.
+ * xa/a_dq/rowsum as produced by btl_quant_absmax for the same M, K.
+ * seg_scale/seg_end: host arrays of nseg (1..4) weight scales and exclusive
+ * column ends (multiples of 32, last == N) -- per-projection scales of the
+ * fused QKV / gate||up weights (src/bitnet_tt/layers/attention.py:481-506,
+ * src/bitnet_tt/layers/ffn.py:22-34).  out: [M, N] (SCALE) or [M, N/2]
+ * (RELU2_MUL) bf16; residual: optional [M, N] bf16 (SCALE only; may equal
+ * out).  acc_out: optional [M, N] int32 copy of the exact accumulators.
+ * splitk: 0 = library's choice.  workspace: btl_gemm_workspace_bytes(...)
+ * bytes; its counters must be zero before the first call and are left zero
+ * by every completed call.                                                 */
+int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, const int32_t* rowsum, int64_t M, int64_t K,
+                  int64_t N, const uint32_t* wdev, const float* seg_scale, const int64_t* seg_end, int nseg,
+                  int epilogue, const uint16_t* residual, uint16_t* out, int32_t* acc_out, void* workspace,
+                  size_t workspace_bytes, int splitk, btl_stream_t stream);
+
+/* One BitLinear launch sequence: [RMSNorm(gamma) ->] absmax quant -> ternary
+ * GEMM -> epilogue.  This is ternary_matmul(x, W, norm_weight=gamma,
+ * norm_epsilon=eps) followed by the scale multiply
+ * (src/bitnet_tt/inference/generator_batch32.py:721-727;
+ * src/bitnet_tt/layers/bitlinear.py:309-353).  Arguments as above;
+ * xq_debug [M,K] int8 optional.  workspace: btl_fused_workspace_bytes(...). */
+int btl_bitlinear_fused(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint16_t* gamma,
+                        float norm_eps, const uint32_t* wdev, int64_t N, const float* seg_scale,
+                        const int64_t* seg_end, int nseg, int epilogue, const uint16_t* residual, uint16_t* out,
+                        int32_t* acc_out, int8_t* xq_debug, void* workspace, size_t workspace_bytes, int splitk,
+                        btl_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BTL_H_ */

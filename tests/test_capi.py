@@ -1,0 +1,150 @@
+"""The C ABI of libbtl.so (CPU only: loading, exports, sizes, argument checks).
+
+No call here reaches a kernel launch: the size helpers are host arithmetic and
+every argument-check case is rejected before the library touches HIP.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from bitnet_tt import _native as N
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "btl.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int64_t|int)\s+(btl_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    return N.lib()
+
+
+def test_library_loads_and_exports_every_declaration(L):
+    names = declared_functions()
+    assert len(names) >= 17
+    for name in names:
+        assert hasattr(L, name), f"{name} declared in include/btl.h but not exported"
+        assert name in N.EXPORTS, f"{name} has no ctypes signature"
+    assert set(N.EXPORTS) == set(names)
+    assert L.btl_version() == 100
+
+
+def test_size_helpers(L):
+    assert L.btl_packed_tile_count(2560, 6912) == 80 * 216
+    assert L.btl_packed_dram_bytes(2560, 2560) == 6400 * 256
+    assert L.btl_packed_tile_count(50, 100) == 8
+    assert L.btl_devlayout_words(2560, 3840) == 120 * 20 * 256
+    assert L.btl_devlayout_words(6912, 2560) == 80 * 54 * 256
+    assert L.btl_devlayout_words(96, 64) == 2 * 1 * 256
+    assert L.btl_devlayout_words(64, 33) == 0
+    assert L.btl_act_bytes(32, 2560) == 20 * 4096
+    assert L.btl_act_bytes(33, 2560) == 2 * 20 * 4096
+    assert L.btl_weight_quant_scratch_bytes(8193) == 8
+    # device layout is exactly 2 bits per weight when K % 128 == 0
+    assert L.btl_devlayout_words(2560, 2560) * 4 == L.btl_packed_dram_bytes(2560, 2560)
+
+
+def test_split_k_plans(L):
+    # decode shapes of the 2B model: about one workgroup per CU
+    assert L.btl_choose_splitk(32, 2560, 3840, 0) == 2
+    assert L.btl_choose_splitk(32, 2560, 2560, 0) == 3
+    assert L.btl_choose_splitk(32, 2560, 13824, 1) == 1
+    assert L.btl_choose_splitk(32, 6912, 2560, 0) == 3
+    assert L.btl_choose_splitk(2048, 2560, 6912, 0) == 1  # prefill: no split
+    assert L.btl_gemm_workspace_bytes(32, 2560, 13824, 1, 0) == 0
+    assert L.btl_gemm_workspace_bytes(32, 2560, 3840, 0, 0) > 2 * 120 * 4096
+    assert L.btl_fused_workspace_bytes(32, 2560, 3840, 0, 0) > L.btl_act_bytes(32, 2560)
+    # a split request larger than K allows is capped (one superblock per wave)
+    assert L.btl_choose_splitk(32, 256, 64, 0) == 1
+
+
+FAKE = 0x100000  # never dereferenced: every call below is rejected first
+
+
+def _p(x):
+    return ctypes.c_void_p(x)
+
+
+def call_gemm(L, **kw):
+    a = dict(xa=_p(FAKE), a_dq=_p(FAKE), rowsum=_p(FAKE), M=32, K=256, N=64, wdev=_p(FAKE), nseg=1, epi=0,
+             residual=None, out=_p(FAKE), acc=None, ws=None, ws_bytes=0, splitk=1)
+    a.update(kw)
+    sc = (ctypes.c_float * 4)(1.0, 1.0, 1.0, 1.0)
+    en = (ctypes.c_int64 * 4)(*(kw.get("ends") or (a["N"], a["N"], a["N"], a["N"])))
+    return L.btl_gemm_i8t2(a["xa"], a["a_dq"], a["rowsum"], a["M"], a["K"], a["N"], a["wdev"], sc, en, a["nseg"],
+                           a["epi"], a["residual"], a["out"], a["acc"], a["ws"], a["ws_bytes"], a["splitk"], None)
+
+
+def test_gemm_argument_checks(L):
+    assert call_gemm(L, xa=None) == 1
+    assert call_gemm(L, wdev=None) == 1
+    assert call_gemm(L, K=250) == 2
+    assert call_gemm(L, N=48) == 2
+    assert call_gemm(L, K=32768) == 2
+    assert call_gemm(L, M=0) == 2
+    assert call_gemm(L, epi=7) == 5
+    assert call_gemm(L, epi=1, N=96) == 2  # relu2 needs N = 2F with F % 32 == 0
+    assert call_gemm(L, nseg=0) == 5
+    assert call_gemm(L, nseg=2, N=64, ends=(16, 64, 0, 0)) == 5  # not a multiple of 32
+    assert call_gemm(L, nseg=2, N=64, ends=(32, 96, 0, 0)) == 5  # last end != N
+    assert call_gemm(L, wdev=_p(FAKE + 4)) == 3
+    assert "16-byte" in N.last_error()
+    assert call_gemm(L, xa=_p(FAKE + 8)) == 3
+    assert "misaligned" in N.last_error()
+    # split-K needs a workspace of the advertised size
+    assert call_gemm(L, M=32, K=2560, N=3840, splitk=2, ws=None) == 1
+    assert call_gemm(L, M=32, K=2560, N=3840, splitk=2, ws=_p(FAKE), ws_bytes=16) == 4
+    assert call_gemm(L, splitk=-1) == 5
+    assert "splitk" in N.last_error()
+
+
+def test_fused_and_prep_argument_checks(L):
+    sc = (ctypes.c_float * 1)(1.0)
+    en = (ctypes.c_int64 * 1)(64)
+    f = L.btl_bitlinear_fused
+    args = [_p(FAKE), 32, 256, 256, None, 1e-5, _p(FAKE), 64, sc, en, 1, 0, None, _p(FAKE), None, None, _p(FAKE),
+            1 << 20, 0, None]
+    bad = list(args)
+    bad[0] = None
+    assert f(*bad) == 1
+    bad = list(args)
+    bad[3] = 250  # ldx < K
+    assert f(*bad) == 3
+    bad = list(args)
+    bad[16] = None  # workspace
+    assert f(*bad) == 1
+    bad = list(args)
+    bad[17] = 64  # workspace too small
+    assert f(*bad) == 4
+    bad = list(args)
+    bad[4] = _p(FAKE + 2)  # misaligned gamma
+    assert f(*bad) == 3
+    assert L.btl_quant_absmax(_p(FAKE), 32, 100, 104, None, 0.0, _p(FAKE), _p(FAKE), _p(FAKE), None, None, None,
+                              None) == 2
+    assert L.btl_quant_absmax(_p(FAKE), 32, 256, 256, None, 0.0, None, _p(FAKE), _p(FAKE), None, None, None,
+                              None) == 1
+    assert L.btl_rmsnorm(_p(FAKE), 4, 256, 256, None, 1e-5, None, None) == 1
+    assert L.btl_repack(_p(FAKE), 100, 64, _p(FAKE), None) == 2
+    assert L.btl_repack(_p(FAKE), 128, 64, _p(FAKE + 4), None) == 3
+    assert L.btl_pack_tiles(None, 32, 32, _p(FAKE), None) == 1
+    assert L.btl_unpack_tiles(_p(FAKE), 0, 32, _p(FAKE), None) == 2
+    assert L.btl_weight_quant_ternary(_p(FAKE), 100, 1e-5, _p(FAKE), _p(FAKE), _p(FAKE), 0, None) == 4
+
+
+def test_python_errors_are_loud(L):
+    torch = pytest.importorskip("torch")
+    from bitnet_tt.ternary_matmul import PackedTernaryWeight, ternary_matmul
+
+    w = PackedTernaryWeight(torch.zeros((2, 2, 256), dtype=torch.int32), 256, 64)
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        ternary_matmul(torch.zeros((32, 256), dtype=torch.bfloat16), w)
+    with pytest.raises(RuntimeError, match="BTL_ERR_SHAPE"):
+        N.check(2, "probe")

@@ -1,0 +1,183 @@
+"""GPU parity of the ternary GEMM (btl_gemm_i8t2) and the fused entry point.
+
+int32 accumulators are compared bit for bit with the oracle; bf16 outputs too
+(the epilogue's rounding is specified exactly).  Decode shapes run every
+split-K factor; prefill shapes at full size are checked on sampled rows plus
+row- and column-checksums against the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+import helpers as H
+from bitnet_tt import _native as N
+
+pytestmark = pytest.mark.gpu
+
+
+def device_weight(orc, w_kn):
+    k, n = w_kn.shape
+    dev = orc.devlayout_encode(w_kn)
+    return H.to_dev(dev.view(np.int32))
+
+
+def run_gemm(orc, q, w_kn, scales, ends=None, epi=0, splitk=0, residual_bits=None, wdev=None):
+    """int8 q [m,k] x ternary w [k,n] through btl_gemm_i8t2; a_dq from the
+    oracle's quantiser convention is replaced by a fixed per-row factor."""
+    L = N.lib()
+    d = H.dev()
+    m, k = q.shape
+    n = w_kn.shape[1]
+    rows = 32 * ((m + 31) // 32)
+    rng = np.random.default_rng(m + k + n)
+    a_dq = np.zeros(rows, np.float32)
+    a_dq[:m] = (0.005 + 0.03 * rng.random(m)).astype(np.float32)
+    rowsum = np.zeros(rows, np.int32)
+    rowsum[:m] = q.astype(np.int64).sum(1)
+    xa = H.to_dev(H.rowmajor_to_xa(q))
+    wdev = device_weight(orc, w_kn) if wdev is None else wdev
+    ends = ends or [n]
+    sc, en, nseg = N.segments_arrays(scales, ends)
+    n_out = n // 2 if epi == 1 else n
+    out = torch.empty((m, n_out), dtype=torch.bfloat16, device=d)
+    acc = torch.empty((m, n), dtype=torch.int32, device=d)
+    res = H.to_dev_bf16(residual_bits) if residual_bits is not None else None
+    if res is not None:
+        out.copy_(res)
+        res = out  # in place: out = residual + result
+    ws_bytes = int(L.btl_gemm_workspace_bytes(m, k, n, epi, splitk))
+    ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=d)
+    N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(H.to_dev(a_dq)), N.ptr(H.to_dev(rowsum)), m, k, n, N.ptr(wdev), sc, en,
+                            nseg, epi, N.ptr(res), N.ptr(out), N.ptr(acc), N.ptr(ws), ws.numel(), splitk,
+                            N.stream_of(d)), "btl_gemm_i8t2")
+    torch.cuda.synchronize()
+    counters_clean = ws_bytes == 0 or not ws[: 4 * 2048].cpu().numpy()[: 4 * ((n // 32) or 1)].any()
+    return acc.cpu().numpy(), H.bits_of(out), a_dq[:m], counters_clean
+
+
+def expected_out(orc, acc, a_dq, scales, ends, epi, residual_bits=None):
+    out = orc.scale_bf16(acc, a_dq, scales, ends)
+    if epi == 1:
+        f = acc.shape[1] // 2
+        return orc.relu2_mul_bf16(out[:, :f], out[:, f:])
+    if residual_bits is not None:
+        out = orc.add_bf16(residual_bits, out)
+    return out
+
+
+def test_identity_readback(orc, known):
+    k = known["identity_readback"]
+    w_outin = np.random.default_rng(k["seed"]).choice([-1, 0, 1], size=(k["N"], k["K"])).astype(np.int8)
+    acc, _, _, _ = run_gemm(orc, np.eye(32, 32, dtype=np.int8), np.ascontiguousarray(w_outin.T), [1.0])
+    assert np.array_equal(acc, w_outin.T.astype(np.int32))
+
+
+def test_all_ones_row_sums(orc):
+    rng = np.random.default_rng(2)
+    q = rng.integers(-128, 128, size=(32, 256)).astype(np.int8)
+    acc, _, _, _ = run_gemm(orc, q, np.ones((256, 64), np.int8), [1.0])
+    assert np.all(acc == q.astype(np.int64).sum(1, keepdims=True))
+    acc, _, _, _ = run_gemm(orc, q, -np.ones((256, 64), np.int8), [1.0])
+    assert np.all(acc == -q.astype(np.int64).sum(1, keepdims=True))
+
+
+@pytest.mark.parametrize("m,k,n", [(32, 128, 32), (32, 2560, 256), (7, 640, 96), (1, 2560, 64), (32, 6912, 128),
+                                   (32, 224, 64)])
+@pytest.mark.parametrize("splitk", [1, 2, 3, 0])
+def test_decode_gemm_bit_exact(orc, m, k, n, splitk):
+    print(f"decode gemm m={m} k={k} n={n} splitk={splitk}", flush=True)
+    rng = np.random.default_rng(m * 7 + k + n + splitk)
+    q = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
+    w = H.ternary(k, n, seed=k + n)
+    acc, out, a_dq, clean = run_gemm(orc, q, w, [0.0173], splitk=splitk)
+    ref = orc.gemm_i8t(q, w)
+    assert np.array_equal(acc, ref)
+    assert np.array_equal(out, expected_out(orc, ref, a_dq, [0.0173], [n], 0))
+    assert clean, "split-K counters must be left at zero"
+
+
+def test_extreme_accumulators(orc):
+    # |acc| = 128 * K at its largest: all -128 against all -1 / +1
+    k = 16384
+    q = np.full((32, k), -128, np.int8)
+    w = np.concatenate([np.ones((k, 32), np.int8), -np.ones((k, 32), np.int8)], axis=1)
+    acc, _, _, _ = run_gemm(orc, q, w, [1.0], splitk=4)
+    assert np.all(acc[:, :32] == -128 * k) and np.all(acc[:, 32:] == 128 * k)
+
+
+def test_segments_and_residual(orc):
+    rng = np.random.default_rng(4)
+    m, k, n = 32, 512, 192
+    q = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
+    w = H.ternary(k, n, seed=9)
+    scales, ends = [0.011, 0.023, 0.037], [128, 160, 192]
+    res = orc.f32_to_bf16(rng.standard_normal((m, n)).astype(np.float32))
+    for splitk in (1, 2):
+        acc, out, a_dq, _ = run_gemm(orc, q, w, scales, ends, splitk=splitk, residual_bits=res)
+        assert np.array_equal(out, expected_out(orc, acc, a_dq, scales, ends, 0, res))
+        assert np.array_equal(acc, orc.gemm_i8t(q, w))
+
+
+@pytest.mark.parametrize("m,k,f", [(32, 256, 64), (32, 2560, 512), (5, 640, 96), (100, 256, 128)])
+def test_relu2_epilogue(orc, m, k, f):
+    rng = np.random.default_rng(m + k + f)
+    q = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
+    w = H.ternary(k, 2 * f, seed=f)
+    scales, ends = [0.021, 0.017], [f, 2 * f]
+    acc, out, a_dq, _ = run_gemm(orc, q, w, scales, ends, epi=1)
+    assert np.array_equal(acc, orc.gemm_i8t(q, w))
+    assert np.array_equal(out, expected_out(orc, acc, a_dq, scales, ends, 1))
+
+
+@pytest.mark.parametrize("m,k,n", [(33, 256, 128), (64, 512, 96), (100, 640, 160), (512, 256, 64)])
+def test_prefill_gemm_bit_exact(orc, m, k, n):
+    print(f"prefill gemm m={m} k={k} n={n}", flush=True)
+    rng = np.random.default_rng(m + k + n)
+    q = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
+    w = H.ternary(k, n, seed=n)
+    acc, out, a_dq, _ = run_gemm(orc, q, w, [0.02])
+    ref = orc.gemm_i8t(q, w)
+    assert np.array_equal(acc, ref)
+    assert np.array_equal(out, expected_out(orc, ref, a_dq, [0.02], [n], 0))
+
+
+@pytest.mark.parametrize("m,k,n,epi", [(512, 2560, 3840, 0), (512, 2560, 13824, 1), (2048, 2560, 6912, 0),
+                                       (2048, 6912, 2560, 0), (512, 2560, 2560, 0)])
+def test_prefill_full_size_properties(orc, m, k, n, epi):
+    """Full prefill shapes: sampled rows exact, row/column checksums exact."""
+    print(f"prefill full m={m} k={k} n={n} epi={epi}", flush=True)
+    rng = np.random.default_rng(m + n)
+    q = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
+    w = H.ternary(k, n, seed=k + n)
+    scales = [0.02] if epi == 0 else [0.02, 0.03]
+    ends = [n] if epi == 0 else [n // 2, n]
+    acc, out, a_dq, _ = run_gemm(orc, q, w, scales, ends, epi=epi)
+    rows = np.sort(rng.choice(m, 6, replace=False))
+    ref_rows = orc.gemm_i8t(np.ascontiguousarray(q[rows]), w)
+    assert np.array_equal(acc[rows], ref_rows)
+    q64, w64 = q.astype(np.int64), w.astype(np.int64)
+    assert np.array_equal(acc.astype(np.int64).sum(1), q64 @ w64.sum(1))
+    assert np.array_equal(acc.astype(np.int64).sum(0), q64.sum(0) @ w64)
+    exp_rows = expected_out(orc, ref_rows, a_dq[rows], scales, ends, epi)
+    assert np.array_equal(out[rows], exp_rows)
+
+
+def test_fused_entry_matches_split_path(orc):
+    """btl_bitlinear_fused == btl_quant_absmax + btl_gemm_i8t2, and == oracle."""
+    from bitnet_tt.ternary_matmul import PackedTernaryWeight, ternary_matmul
+
+    m, k, n = 32, 2560, 3840
+    xb = H.activations(orc, m, k, seed=21)
+    gb = H.gamma(orc, k, seed=22)
+    w = H.ternary(k, n, seed=23)
+    pw = PackedTernaryWeight(device_weight(orc, w), k, n, (0.017, 0.019, 0.023), (2560, 3200, 3840))
+    acc = torch.empty((m, n), dtype=torch.int32, device=H.dev())
+    xq = torch.empty((m, k), dtype=torch.int8, device=H.dev())
+    for splitk in (0, 1, 2, 4):
+        out = ternary_matmul(H.to_dev_bf16(xb), pw, norm_weight=H.to_dev_bf16(gb), norm_epsilon=1e-5,
+                             splitk=splitk, acc_out=acc, xq_out=xq)
+        torch.cuda.synchronize()
+        ref = orc.bitlinear(xb, w, [0.017, 0.019, 0.023], [2560, 3200, 3840], gamma_bf16=gb, norm_eps=1e-5)
+        assert np.array_equal(xq.cpu().numpy(), ref["q"])
+        assert np.array_equal(acc.cpu().numpy(), ref["acc"])
+        assert np.array_equal(H.bits_of(out), ref["out"])

@@ -1,0 +1,239 @@
+"""GPU parity of the reference-API layers (Linear, FeedForward, fused QKV) and
+of the decode-step chain, on the BitLinear configurations of the 2B model:
+
+  C1  single BitLinear 2560->2560, x ~N(0,1) with 1 % outlier channels x20,
+      W ~N(0,0.02) absmean-quantised;
+  C2  fused RMSNorm + QKV 2560->3840 (20 Q / 5 KV heads of 128), three scales;
+  C3  FFN block: gate||up 2560->2x6912, relu^2*up, ffn_sub_norm, down 6912->2560;
+  C4  decode-step chain (30 layers at full size: layer 0 exact, the rest by
+      determinism and graph-replay checks; 2 layers of the mini model exact);
+  C5  prefill BitLinear through the layer API (M = 512).
+
+Integer results and bf16 outputs are compared bit for bit with the oracle
+(RMSNorm in its fixed fp32 order); against the float64 reading of the
+reference formula the bf16 output is within 1e-2 relative.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import helpers as H
+from bitnet_tt.config import BitNet2B4TConfig, BitNetMiniConfig
+from bitnet_tt.decode import BitLinearDecodeStep
+from bitnet_tt.layers.attention import QKVProjection
+from bitnet_tt.layers.bitlinear import Linear
+from bitnet_tt.layers.ffn import FeedForward
+from bitnet_tt.ternary_matmul import ternary_matmul
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_err(out_bits, ref64, orc):
+    out = orc.bf16_to_f32(out_bits).astype(np.float64)
+    return np.max(np.abs(out - ref64)) / np.max(np.abs(ref64))
+
+
+def test_c1_single_bitlinear(orc):
+    m, k, n = 32, 2560, 2560
+    xb = H.activations(orc, m, k, seed=101)
+    w = H.latent(n, k, seed=102)
+    lin = Linear(k, n, H.dev())
+    lin.load_weights(w)
+    out = lin(H.to_dev_bf16(xb))
+    q, s = orc.weight_quant_ternary(w)
+    assert lin.weight_scale == float(s)
+    ref = orc.bitlinear(xb, np.ascontiguousarray(q.T), [float(s)])
+    assert np.array_equal(H.bits_of(out), ref["out"])
+    # float64 reading of quant -> matmul -> scale
+    xf = orc.bf16_to_f32(xb).astype(np.float64)
+    a = np.abs(xf).max(1, keepdims=True)
+    ref64 = np.clip(np.round(xf * (127 / a)), -128, 127) @ q.T.astype(np.float64) * float(s) * a / 127
+    assert rel_err(H.bits_of(out), ref64, orc) < 1e-2
+    split = [(q == 1).mean(), (q == 0).mean(), (q == -1).mean()]
+    print(f"C1 ternary split +1/0/-1 = {split[0]:.3f}/{split[1]:.3f}/{split[2]:.3f}")
+
+
+def test_c1_device_weight_load_matches_host(orc):
+    k, n = 2560, 2560
+    w = H.latent(n, k, seed=102)
+    a, b = Linear(k, n, H.dev()), Linear(k, n, H.dev())
+    a.load_weights(w)
+    b.load_weights(H.to_dev(w))
+    assert a.weight_scale == b.weight_scale
+    assert torch.equal(a.weight.data, b.weight.data)
+
+
+def test_c2_fused_rmsnorm_qkv(orc):
+    c = BitNet2B4TConfig()
+    H_, qd, kvd = c.hidden_size, c.num_attention_heads * c.head_dim, c.num_kv_heads * c.head_dim
+    xb = H.activations(orc, 32, H_, seed=201)
+    gb = H.gamma(orc, H_, seed=202)
+    wq, wk, wv = H.latent(qd, H_, 203), H.latent(kvd, H_, 204), H.latent(kvd, H_, 205)
+    proj = QKVProjection(H_, c.num_attention_heads, c.num_kv_heads, c.head_dim, H.dev())
+    proj.load_weights(wq, wk, wv)
+    out = proj(H.to_dev_bf16(xb), norm_weight=H.to_dev_bf16(gb), norm_epsilon=c.rms_norm_eps)
+    qs = [orc.weight_quant_ternary(w) for w in (wq, wk, wv)]
+    w_kn = np.ascontiguousarray(np.concatenate([q for q, _ in qs]).T)
+    ends = [qd, qd + kvd, qd + 2 * kvd]
+    ref = orc.bitlinear(xb, w_kn, [float(s) for _, s in qs], ends, gamma_bf16=gb, norm_eps=c.rms_norm_eps)
+    assert out.shape == (32, 3840)
+    assert np.array_equal(H.bits_of(out), ref["out"])
+    # RMSNorm in double precision (reference formula) -> output within 1e-2
+    ref0 = orc.bitlinear(xb, w_kn, [float(s) for _, s in qs], ends, gamma_bf16=gb, norm_eps=c.rms_norm_eps, order=0)
+    assert rel_err(H.bits_of(out), orc.bf16_to_f32(ref0["out"]).astype(np.float64), orc) < 1e-2
+
+
+def test_c2_rope_permutation_and_unscaled(orc):
+    hd, nh, nkv, hid = 16, 4, 2, 64
+    rng_w = [H.latent(nh * hd, hid, 1), H.latent(nkv * hd, hid, 2), H.latent(nkv * hd, hid, 3)]
+    xb = H.activations(orc, 8, hid, seed=4, outliers=False)
+    gb = H.gamma(orc, hid, seed=5)
+    proj = QKVProjection(hid, nh, nkv, hd, H.dev(), use_fused_rope=True)
+    proj.load_weights(*rng_w, apply_scales=False)
+    out = proj(H.to_dev_bf16(xb), norm_weight=H.to_dev_bf16(gb), norm_epsilon=1e-5)
+    qs = [orc.weight_quant_ternary(w) for w in rng_w]
+    qt = orc.permute_halfsplit_to_adjacent(np.ascontiguousarray(qs[0][0].T), nh, hd)
+    kt = orc.permute_halfsplit_to_adjacent(np.ascontiguousarray(qs[1][0].T), nkv, hd)
+    w_kn = np.ascontiguousarray(np.concatenate([qt, kt, qs[2][0].T], axis=1))
+    ref = orc.bitlinear(xb, w_kn, [1.0, 1.0, 1.0], [64, 96, 128], gamma_bf16=gb, norm_eps=1e-5)
+    assert np.array_equal(H.bits_of(out), ref["out"])
+
+
+def test_c3_ffn_block(orc):
+    c = BitNet2B4TConfig()
+    Hh, F = c.hidden_size, c.intermediate_size
+    xb = H.activations(orc, 32, Hh, seed=301)
+    g_post = H.gamma(orc, Hh, seed=302)
+    sub = orc.bf16_to_f32(H.gamma(orc, F, seed=303))
+    gate, up, down = H.latent(F, Hh, 304), H.latent(F, Hh, 305), H.latent(Hh, F, 306)
+    ffn = FeedForward(Hh, F, H.dev(), eps=c.rms_norm_eps)
+    ffn.load_weights(gate, up, down, sub)
+    res = orc.f32_to_bf16(np.random.default_rng(307).standard_normal((32, Hh)).astype(np.float32))
+    y = ffn(H.to_dev_bf16(xb), mode="decode", norm_weight=H.to_dev_bf16(g_post), norm_epsilon=c.rms_norm_eps,
+            residual=H.to_dev_bf16(res))
+    gq, gs = orc.weight_quant_ternary(gate)
+    uq, us = orc.weight_quant_ternary(up)
+    dq, ds = orc.weight_quant_ternary(down)
+    r1 = orc.gate_up_relu2(xb, np.ascontiguousarray(np.concatenate([gq, uq]).T), float(gs), float(us),
+                           gamma_bf16=g_post, norm_eps=c.rms_norm_eps)
+    r2 = orc.bitlinear(r1["h"], np.ascontiguousarray(dq.T), [float(ds)], gamma_bf16=orc.f32_to_bf16(sub),
+                       norm_eps=c.rms_norm_eps, residual_bf16=res)
+    assert np.array_equal(H.bits_of(y), r2["out"])
+
+
+def test_c5_prefill_linear(orc):
+    m, k, n = 512, 2560, 2560
+    xb = H.activations(orc, m, k, seed=501)
+    gb = H.gamma(orc, k, seed=502)
+    w = H.latent(n, k, seed=503)
+    lin = Linear(k, n, H.dev())
+    lin.load_weights(w)
+    out = H.bits_of(lin(H.to_dev_bf16(xb), norm_weight=H.to_dev_bf16(gb), norm_epsilon=1e-5))
+    q, s = orc.weight_quant_ternary(w)
+    rows = [0, 1, 77, 255, 256, 511]
+    ref = orc.bitlinear(np.ascontiguousarray(xb[rows]), np.ascontiguousarray(q.T), [float(s)], gamma_bf16=gb,
+                        norm_eps=1e-5)
+    assert np.array_equal(out[rows], ref["out"])
+
+
+def test_ternary_matmul_op_signature(orc):
+    """The reference call form: ternary_matmul(x, W, use_packed_ternary=True,
+    norm_weight=..., norm_epsilon=...) with [1, 1, M, K] activations."""
+    k, n = 256, 96
+    xb = H.activations(orc, 32, k, seed=601).reshape(1, 1, 32, k)
+    gb = H.gamma(orc, k, seed=602)
+    w = H.latent(n, k, seed=603)
+    lin = Linear(k, n, H.dev())
+    lin.load_weights(w)
+    out = ternary_matmul(H.to_dev_bf16(xb), lin.weight, use_packed_ternary=True,
+                         norm_weight=H.to_dev_bf16(gb).reshape(1, 1, 1, k), norm_epsilon=1e-5)
+    assert out.shape == (1, 1, 32, n)
+    q, s = orc.weight_quant_ternary(w)
+    ref = orc.bitlinear(xb.reshape(32, k), np.ascontiguousarray(q.T), [float(s)], gamma_bf16=gb, norm_eps=1e-5)
+    assert np.array_equal(H.bits_of(out).reshape(32, n), ref["out"])
+    with pytest.raises(RuntimeError, match="Weights not loaded"):
+        Linear(k, n, H.dev())(H.to_dev_bf16(xb))
+
+
+def oracle_layer(orc, step, i, hidden, attn):
+    """One decode layer of the chain on the CPU, from the device weights."""
+    w = step.layers[i]
+    eps = step.eps
+    c = step.config
+
+    def wkn(pw):
+        dev = pw.data.cpu().numpy().view(np.uint32)
+        return orc.devlayout_decode(dev, pw.in_features, pw.out_features)
+
+    g = lambda t: H.bits_of(t)  # noqa: E731
+    qkv = orc.bitlinear(hidden, wkn(w.qkv), list(w.qkv.segment_scales), list(w.qkv.segment_ends),
+                        gamma_bf16=g(w.input_layernorm), norm_eps=eps)["out"]
+    hidden = orc.bitlinear(attn, wkn(w.o_proj), list(w.o_proj.segment_scales), gamma_bf16=g(w.attn_sub_norm),
+                           norm_eps=eps, residual_bf16=hidden)["out"]
+    r = orc.gate_up_relu2(hidden, wkn(w.gate_up), w.gate_up.segment_scales[0], w.gate_up.segment_scales[1],
+                          gamma_bf16=g(w.post_attention_layernorm), norm_eps=eps)
+    hidden = orc.bitlinear(r["h"], wkn(w.down), list(w.down.segment_scales), gamma_bf16=g(w.ffn_sub_norm),
+                           norm_eps=eps, residual_bf16=hidden)["out"]
+    assert c.qkv_dim == qkv.shape[1]
+    return hidden, qkv
+
+
+def test_c4_mini_decode_chain_exact(orc):
+    cfg = BitNetMiniConfig(num_layers=2)
+    step = BitLinearDecodeStep.random_init(cfg, H.dev(), seed=7).alloc_buffers(seed=8)
+    hid, attn = H.bits_of(step.hidden), H.bits_of(step.attn_out)
+    step.step()
+    torch.cuda.synchronize()
+    for i in range(2):
+        hid, qkv = oracle_layer(orc, step, i, hid, attn)
+    assert np.array_equal(H.bits_of(step.hidden), hid)
+    assert np.array_equal(H.bits_of(step.qkv_out), qkv)
+
+
+def test_c4_graph_replay_matches_eager(orc):
+    cfg = BitNetMiniConfig(num_layers=3)
+    step = BitLinearDecodeStep.random_init(cfg, H.dev(), seed=9).alloc_buffers(seed=10)
+    step.step()  # warm-up: workspaces exist before capture
+    step.reset_hidden()
+    step.step()
+    torch.cuda.synchronize()
+    eager = H.bits_of(step.hidden)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step.reset_hidden()
+        step.step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step.step()
+    for rep in range(4):
+        step.reset_hidden()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(H.bits_of(step.hidden), eager), f"replay {rep} differs"
+        _ = torch.ones(1024, device=H.dev()).sum().item()  # eager work between replays
+
+
+def test_c4_full_model_layer0_exact_and_deterministic(orc):
+    cfg = BitNet2B4TConfig()
+    step = BitLinearDecodeStep.random_init(cfg, H.dev(), seed=11).alloc_buffers(seed=12)
+    assert len(step.layers) == 30
+    pos, zero, neg = step.ternary_split
+    print(f"C4 ternary split +1/0/-1 = {pos:.4f}/{zero:.4f}/{neg:.4f}")
+    assert abs(zero - 0.31) < 0.01
+    hid0, attn = H.bits_of(step.hidden), H.bits_of(step.attn_out)
+    step.layer(0, step.hidden, step.attn_out, step.qkv_out, step.ffn_h)
+    torch.cuda.synchronize()
+    ref_h, ref_qkv = oracle_layer(orc, step, 0, hid0, attn)
+    assert np.array_equal(H.bits_of(step.qkv_out), ref_qkv)
+    assert np.array_equal(H.bits_of(step.hidden), ref_h)
+    step.reset_hidden()
+    a = step.step().clone()
+    step.reset_hidden()
+    b = step.step().clone()
+    torch.cuda.synchronize()
+    assert torch.isfinite(a.float()).all()
+    assert torch.equal(a, b)
