@@ -68,14 +68,14 @@ class SplitLauncher:
         rows = 32 * ((M + 31) // 32)
         xa = ws["xa"]
         N.check(self.L.btl_quant_absmax(N.ptr(x), M, K, K, N.ptr(gamma), eps, N.ptr(xa), N.ptr(ws["a_dq"]),
-                                        N.ptr(ws["rowsum"]), None, None, None, N.stream_of(self.dev)),
+                                        None, None, None, None, N.stream_of(self.dev)),
                 "btl_quant_absmax")
         return M, rows
 
     def gemm(self, M, K, w, out, epi, residual, ws):
         N = self.N
         sc, en, nseg = N.segments_arrays(w.segment_scales, w.segment_ends)
-        N.check(self.L.btl_gemm_i8t2(N.ptr(ws["xa"]), N.ptr(ws["a_dq"]), N.ptr(ws["rowsum"]), M, K, w.out_features,
+        N.check(self.L.btl_gemm_i8t2(N.ptr(ws["xa"]), N.ptr(ws["a_dq"]), M, K, w.out_features,
                                      N.ptr(w.data), sc, en, nseg, epi, N.ptr(residual), N.ptr(out), None,
                                      N.ptr(ws["gemm"]), ws["gemm"].numel(), 0, N.stream_of(self.dev)),
                 "btl_gemm_i8t2")
@@ -105,7 +105,6 @@ def kernel_event_timing(step, torch, N, reps):
         ws = {
             "xa": torch.empty(int(L.btl_act_bytes(32, K)), dtype=torch.uint8, device=dev),
             "a_dq": torch.empty(32, dtype=torch.float32, device=dev),
-            "rowsum": torch.empty(32, dtype=torch.int32, device=dev),
             "gemm": torch.zeros(max(int(L.btl_gemm_workspace_bytes(32, K, Nf, epi, 0)), 256), dtype=torch.uint8,
                                 device=dev),
         }
@@ -162,7 +161,6 @@ def prefill_mfma(torch, N, dev):
         xa = torch.randint(-128, 128, (int(L.btl_act_bytes(M, K)),), generator=gen, device=dev,
                            dtype=torch.int16).to(torch.int8)
         a_dq = torch.full((32 * ((M + 31) // 32),), 0.01, device=dev)
-        rowsum = torch.zeros_like(a_dq, dtype=torch.int32)
         copies = 4
         wd = [torch.randint(0, 1 << 30, (Nf // 32, KS, 256), generator=gen, device=dev, dtype=torch.int32) & 0x55555555
               for _ in range(copies)]  # codes 0/1 only: valid ternary offsets
@@ -171,7 +169,7 @@ def prefill_mfma(torch, N, dev):
         stream = N.stream_of(dev)
 
         def launch(i):
-            N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(a_dq), N.ptr(rowsum), M, K, Nf, N.ptr(wd[i % copies]), sc, en,
+            N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(a_dq), M, K, Nf, N.ptr(wd[i % copies]), sc, en,
                                     nseg, 0, None, N.ptr(o), None, None, 0, 1, stream), "prefill gemm")
 
         reps = 20

@@ -48,6 +48,7 @@ EXPORTS = {
     "btl_choose_splitk": ([_I64, _I64, _I64, _I], _I),
     "btl_gemm_workspace_bytes": ([_I64, _I64, _I64, _I, _I], _I64),
     "btl_fused_workspace_bytes": ([_I64, _I64, _I64, _I, _I], _I64),
+    "btl_fused_error_offset": ([], _I64),
     "btl_weight_quant_scratch_bytes": ([_I64], _I64),
     "btl_weight_quant_ternary": ([_P, _I64, _F, _P, _P, _P, _SZ, _P], _I),
     "btl_pack_tiles": ([_P, _I64, _I64, _P, _P], _I),
@@ -56,7 +57,7 @@ EXPORTS = {
     "btl_quant_absmax": ([_P, _I64, _I64, _I64, _P, _F, _P, _P, _P, _P, _P, _P, _P], _I),
     "btl_rmsnorm": ([_P, _I64, _I64, _I64, _P, _F, _P, _P], _I),
     "btl_gemm_i8t2": (
-        [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I, _I, _P, _P, _P, _P, _SZ, _I, _P],
+        [_P, _P, _I64, _I64, _I64, _P, _P, _P, _I, _I, _P, _P, _P, _P, _SZ, _I, _P],
         _I,
     ),
     "btl_bitlinear_fused": (

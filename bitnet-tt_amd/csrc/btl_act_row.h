@@ -1,0 +1,282 @@
+// Activation prologue of a BitLinear for one token row: optional RMSNorm,
+// per-token absmax int8 quantisation, and the blocked operand layout the
+// ternary GEMM consumes.  Shared by the standalone activation kernel and the
+// fused decode BitLinear kernel.
+//
+//   RMSNorm  (HF BitNetRMSNorm order; src/bitnet_tt/layers/bitlinear.py:433-461,
+//            fused into the QKV launch at inference/generator_batch32.py:721-727):
+//            r = 1/sqrt(sum(x^2)/K + eps); y = bf16(gamma * bf16(x * r))
+//   quant    (src/bitnet_tt/utils/quantization.py:60-91):
+//            a = max(max|y|, 1e-5); q = clip(rne(y * (127/a)), -128, 127)
+//
+// 256 threads (4 waves) work on a row.  The sum of squares follows a fixed
+// order so the statistic is reproducible bit for bit: thread t accumulates
+// x^2 over the 8-element chunks t, t+256, ... in order, the 64 lanes of a wave
+// combine by an xor butterfly (offsets 32..1), and the four wave sums combine
+// as (w0+w1)+(w2+w3).  Multiplies and adds are separately rounded (built with
+// -ffp-contract=off); division and sqrt are correctly rounded.
+//
+// Quantised output layout (per 32-row block mb, 128-column superblock ks):
+// byte (((mb*KS + ks)*4 + q)*64 + lane)*16 + p holds q[mb*32 + (lane & 31)]
+// [ks*128 + q*32 + (lane >> 5)*16 + p] -- exactly the 16 bytes lane `lane`
+// feeds to v_mfma_i32_32x32x32_i8 for k-step q, so one 1 KiB load per wave
+// and k-step brings a whole A operand.  Rows >= M and columns >= K are zero.
+#pragma once
+
+#include <math.h>
+
+#include "btl_common.h"
+
+namespace btl {
+
+constexpr int kActThreads = 256;
+constexpr int kActMaxChunks = BTL_MAX_K / 8 / kActThreads;  // 8 chunks of 8 per thread
+
+// Chunks of 8 elements per thread for a row of K (1, 2, 4 or 8): the row code
+// is instantiated per bucket so a thread's loops cover only chunks it can own.
+inline int act_cpt(int64_t K) {
+  const int64_t c = (K / 8 + kActThreads - 1) / kActThreads;
+  return c <= 1 ? 1 : c <= 2 ? 2 : c <= 4 ? 4 : 8;
+}
+
+struct ActArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  int M, K, KS;
+  const uint16_t* gamma;
+  float norm_eps;
+  float act_eps;
+  int8_t* xa;
+  float* a_dq;
+  int32_t* rowsum;       // optional [rows] sum_k q (the GEMM recomputes it)
+  float* act_scale;      // optional [M] 127/a
+  int8_t* xq_rm;         // optional [M, K] int8
+  uint16_t* y_rm;        // optional [M, K] bf16 (the normalised y)
+  uint32_t* zero_words;  // optional words cleared by row 0 (GEMM counters)
+  int n_zero_words;
+};
+
+// Memory operations every workgroup of the device observes without an L2
+// write-back: agent-scope relaxed atomics bypass the per-XCD L2.  Data is
+// published as "coherent stores, wait for their acknowledgement, bump a
+// counter"; a __threadfence() would instead write back every XCD's whole L2.
+__device__ __forceinline__ void st_coherent(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t ld_coherent(const int32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_coherent(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float* p) {
+  return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT));
+}
+// Waits until every memory operation this thread issued has completed.
+__device__ __forceinline__ void wait_memory() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+__device__ __forceinline__ int64_t xa_offset(int m, int k0, int KS) {
+  const int mb = m >> 5, mr = m & 31;
+  const int ks = k0 >> 7, qs = (k0 >> 5) & 3, h = (k0 >> 4) & 1, p0 = k0 & 15;
+  return ((((int64_t)mb * KS + ks) * 4 + qs) * 64 + (h * 32 + mr)) * 16 + p0;
+}
+
+template <bool COHERENT>
+__device__ __forceinline__ void store8(int8_t* p, uint32_t lo, uint32_t hi) {
+  if (COHERENT)
+    st_coherent(reinterpret_cast<uint64_t*>(p), (uint64_t)lo | ((uint64_t)hi << 32));
+  else
+    *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
+}
+
+// Row m of the activation prologue.  Threads 0..255 do the work; any further
+// threads of the block only take part in the barriers.  With COHERENT the
+// quantised row and a_dq are written with coherent stores (for a consumer in
+// the same launch).
+template <bool NORM, bool QUANT, bool COHERENT, int CPT>
+__device__ void act_row(const ActArgs& p, int m, int tid) {
+  static_assert(CPT >= 1 && CPT <= kActMaxChunks, "chunks per thread");
+  const bool active = tid < kActThreads;
+  const int lane = tid & 63, wv = tid >> 6;
+  __shared__ float s_sum[4];
+  __shared__ float s_max[4];
+  __shared__ int s_int[4];
+
+  if (p.zero_words && m == 0 && active)
+    for (int i = tid; i < p.n_zero_words; i += kActThreads) {
+      if (COHERENT)
+        st_coherent(p.zero_words + i, 0u);
+      else
+        p.zero_words[i] = 0u;
+    }
+
+  const int nch = p.K >> 3;    // 8-element chunks holding data
+  const int nchp = p.KS * 16;  // chunks up to the 128-column padding
+  if (m >= p.M) {              // padding row of the last 32-row block
+    if (QUANT && active) {
+      for (int c = tid; c < nchp; c += kActThreads) store8<COHERENT>(p.xa + xa_offset(m, 8 * c, p.KS), 0u, 0u);
+      if (tid == 0) {
+        if (COHERENT)
+          st_coherent(p.a_dq + m, 0.0f);
+        else
+          p.a_dq[m] = 0.0f;
+        if (p.rowsum) p.rowsum[m] = 0;
+      }
+    }
+    return;
+  }
+
+  const uint16_t* xr = p.x + (int64_t)m * p.ldx;
+  float v[CPT][8];
+  // gamma travels with x: both loads are in flight before the first barrier.
+  uint4 graw[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = tid + kActThreads * i;
+    graw[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (NORM && p.gamma && active && c < nch) graw[i] = *reinterpret_cast<const uint4*>(p.gamma + 8 * c);
+  }
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = tid + kActThreads * i;
+    if (active && c < nch) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(xr + 8 * c);
+      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[i][2 * j] = bf2f((uint16_t)(w4[j] & 0xffffu));
+        v[i][2 * j + 1] = bf2f((uint16_t)(w4[j] >> 16));
+      }
+    }
+  }
+
+  if (NORM) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i)
+      if (active && tid + kActThreads * i < nch) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float sq = v[i][j] * v[i][j];
+          s = s + sq;
+        }
+      }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_xor(s, off, 64);
+    if (active && lane == 0) s_sum[wv] = s;
+    __syncthreads();
+    const float ss = (s_sum[0] + s_sum[1]) + (s_sum[2] + s_sum[3]);
+    const float var = ss / (float)p.K;
+    const float r = 1.0f / sqrtf(var + p.norm_eps);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + kActThreads * i;
+      if (active && c < nch) {
+        const uint32_t g4[4] = {graw[i].x, graw[i].y, graw[i].z, graw[i].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float t = bf2f(f2bf(v[i][j] * r));
+          if (p.gamma) {
+            const float g = bf2f((uint16_t)((j & 1) ? (g4[j >> 1] >> 16) : (g4[j >> 1] & 0xffffu)));
+            v[i][j] = bf2f(f2bf(g * t));
+          } else {
+            v[i][j] = t;
+          }
+        }
+      }
+    }
+  }
+
+  if (!QUANT || p.y_rm) {
+    uint16_t* yr = p.y_rm + (int64_t)m * p.K;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + kActThreads * i;
+      if (active && c < nch) {
+        uint4 o;
+        o.x = (uint32_t)f2bf(v[i][0]) | ((uint32_t)f2bf(v[i][1]) << 16);
+        o.y = (uint32_t)f2bf(v[i][2]) | ((uint32_t)f2bf(v[i][3]) << 16);
+        o.z = (uint32_t)f2bf(v[i][4]) | ((uint32_t)f2bf(v[i][5]) << 16);
+        o.w = (uint32_t)f2bf(v[i][6]) | ((uint32_t)f2bf(v[i][7]) << 16);
+        *reinterpret_cast<uint4*>(yr + 8 * c) = o;
+      }
+    }
+  }
+  if (!QUANT) return;
+
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i)
+    if (active && tid + kActThreads * i < nch) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[i][j]));
+    }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  if (active && lane == 0) s_max[wv] = amax;
+  __syncthreads();
+  float a = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+  a = a > p.act_eps ? a : p.act_eps;
+  const float scale = 127.0f / a;
+  if (tid == 0) {
+    if (COHERENT)
+      st_coherent(p.a_dq + m, a / 127.0f);
+    else
+      p.a_dq[m] = a / 127.0f;
+    if (p.act_scale) p.act_scale[m] = scale;
+  }
+
+  int rs = 0;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = tid + kActThreads * i;
+    if (active && c < nch) {
+      uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float t = rintf(v[i][j] * scale);
+        t = fminf(fmaxf(t, -128.0f), 127.0f);
+        const int qi = (int)t;
+        rs += qi;
+        const uint32_t b = (uint32_t)(qi & 0xff);
+        if (j < 4)
+          lo |= b << (8 * j);
+        else
+          hi |= b << (8 * (j - 4));
+      }
+      store8<COHERENT>(p.xa + xa_offset(m, 8 * c, p.KS), lo, hi);
+      if (p.xq_rm) *reinterpret_cast<uint2*>(p.xq_rm + (int64_t)m * p.K + 8 * c) = make_uint2(lo, hi);
+    }
+  }
+  if (active)
+    for (int c = nch + tid; c < nchp; c += kActThreads) store8<COHERENT>(p.xa + xa_offset(m, 8 * c, p.KS), 0u, 0u);
+
+  if (!p.rowsum) return;  // the GEMM derives row sums from its operand
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) rs += __shfl_xor(rs, off, 64);
+  if (active && lane == 0) s_int[wv] = rs;
+  __syncthreads();
+  if (tid == 0) {
+    const int32_t total = s_int[0] + s_int[1] + s_int[2] + s_int[3];
+    if (COHERENT)
+      st_coherent(p.rowsum + m, total);
+    else
+      p.rowsum[m] = total;
+  }
+}
+
+}  // namespace btl

@@ -14,10 +14,15 @@ __host__ __device__ __forceinline__ float bf2f(uint16_t h) {
   return __uint_as_float(((uint32_t)h) << 16);
 }
 __host__ __device__ __forceinline__ uint16_t f2bf(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  // v_cvt_pk_bf16_f32: round to nearest even in one instruction.
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+#else
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
   u += 0x7fffu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
+#endif
 }
 
 // ---- errors -------------------------------------------------------------
@@ -38,16 +43,20 @@ inline int64_t round_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 // ---- GEMM plan (shared by sizing functions and launches) ----------------
 struct GemmPlan {
   bool prefill;   // M > 32: tiled kernel over 32-row blocks
+  bool fused;     // decode: activation prologue and GEMM in one launch
   int tpw;        // decode: column tiles per workgroup (2 for the relu2 pair)
+  int waves;      // decode: waves per workgroup (4 or 8), splitting the slice's K
   int ngroups;    // decode: workgroups along N
   int splitk;     // decode: workgroups along K
   int64_t ws_bytes;
 };
 GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req);
 
-// Byte offsets inside the fused workspace.
+// Byte offsets inside the fused workspace (the first 256 bytes hold the
+// producer/consumer words of the fused decode kernel; byte 128 is its error
+// word).
 struct FusedLayout {
-  int64_t xa, a_dq, rowsum, gemm_ws, total;
+  int64_t xa, a_dq, gemm_ws, total;
 };
 FusedLayout fused_layout(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req);
 

@@ -6,23 +6,32 @@
 // in MFMA operand order, so unpacking a dword of 16 codes into the four B
 // operand dwords is one shift and one AND each.  The int8 MFMA then computes
 // sum_k q*u, and the exact accumulator is recovered as
-//   acc = sum_k q*u - sum_k q      (the row sum comes with the quantiser).
+//   acc = sum_k q*u - sum_k q
+// with the row sum taken from the A operand in the same pass (v_dot4 of the
+// operand bytes with 0x01010101; each K slice subtracts its own part).
 // |acc| <= 128*2*16384 < 2^31, so every step is exact.
 //
 // Decode (M <= 32): the whole activation block is one 32-row MFMA operand.
-// A workgroup (4 waves) owns TPW column tiles of 32 and a slice of the K
-// superblocks; each wave takes a quarter of that slice, issues all of its
-// weight and activation loads up front (1 KiB per wave per load: fully
-// coalesced), then runs the MFMAs.  The four wave partials meet in LDS.
-// When K is split across workgroups (split-K), each writes its partial tile
-// to the workspace and the last to arrive (atomic counter) sums them in a
-// fixed order and runs the epilogue -- no spinning, no float atomics, the
-// result is deterministic.
+// A workgroup (4 or 8 waves) owns TPW column tiles of 32 and a slice of the K
+// superblocks; each wave takes its share of that slice, issues its weight
+// loads and then its activation loads (1 KiB per wave per load: fully
+// coalesced) before the first MFMA.  The wave partials meet in LDS.  When K
+// is split across workgroups (split-K), each publishes its partial tile with
+// coherent stores and the last to arrive (atomic counter) sums them and runs
+// the epilogue -- no spinning, no float atomics, a deterministic result.
+//
+// Fused decode BitLinear (one launch): workgroups 0..31 run the activation
+// prologue of one token row each (btl_act_row.h) and publish the quantised
+// rows with coherent stores and a counter; the GEMM workgroups issue their
+// weight loads first, then wait for the counter (bounded spin), so weight
+// streaming overlaps the prologue and a launch is saved.
 //
 // Prefill (M > 32): 128x128 output tiles, one 64x64 quadrant per wave, A and
 // B fragments loaded straight into registers (both operands are stored in
 // MFMA order), the next superblock prefetched while the current one runs.
-#include "btl_common.h"
+#include <stdlib.h>
+
+#include "btl_act_row.h"
 
 namespace btl {
 
@@ -37,10 +46,10 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 struct GemmArgs {
   const int8_t* xa;
   const float* a_dq;
-  const int32_t* rowsum;
   const uint32_t* wdev;
   int M, KS, NT, N, n_out, Mb;
   int splitk, ngroups;
+  int xa_bytes;
   float seg_scale[BTL_MAX_SEGMENTS];
   int seg_end[BTL_MAX_SEGMENTS];
   int nseg;
@@ -50,6 +59,26 @@ struct GemmArgs {
   int32_t* ws_part;
   uint32_t* ws_cnt;
 };
+
+// Producer/consumer handshake of the fused decode kernel (each word on its
+// own 128-byte line):
+//   ready: activation block m sets flag m once its row is published; a GEMM
+//          block polls the 32 flags with 32 lanes of one wave.
+//   pass:  a GEMM block bumps its group counter (8 groups) once it has passed
+//          the wait, and checks the result only when it exits; the last of a
+//          group bumps the top counter, and the block completing the top
+//          counter clears the flags and counters for the next call.
+struct FusedSync {
+  uint32_t* words;  // handshake words, 32 words apart
+  int nact;         // activation workgroups (32)
+  int ngemm;        // GEMM workgroups
+  unsigned spin_limit;
+  int pre_sleep;    // s_sleep(8) rounds before the weight loads (row loads first)
+};
+constexpr int kSyncGroups = 8;
+constexpr int kSyncStride = 32;  // words: 128 bytes
+enum { kReadyFlag = 0, kPassGrp = 32, kPassTop = 40, kErrorWord = 41 };
+__device__ __forceinline__ uint32_t* sync_word(const FusedSync& fs, int w) { return fs.words + w * kSyncStride; }
 
 __device__ __forceinline__ v4i unpack_b(uint32_t d) {
   const int m = 0x03030303;
@@ -63,6 +92,11 @@ __device__ __forceinline__ v4i unpack_b(uint32_t d) {
 
 __device__ __forceinline__ v4i ld128(const void* p) { return *reinterpret_cast<const v4i*>(p); }
 
+// 16-byte load that bypasses the per-XCD L2 (data published in this launch).
+__device__ __forceinline__ v4i ld128_coherent(__amdgpu_buffer_rsrc_t rsrc, int offset) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 16 /* sc1 */);
+}
+
 __device__ __forceinline__ float seg_scale_of(const GemmArgs& p, int n) {
   float s = p.seg_scale[0];
 #pragma unroll
@@ -74,20 +108,21 @@ __device__ __forceinline__ float seg_scale_of(const GemmArgs& p, int n) {
 // Row of element r (0..15) of a lane's 32x32 MFMA accumulator.
 __device__ __forceinline__ int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
-// Epilogue for one accumulator element (acc already row-sum corrected).
-__device__ __forceinline__ void epi_scale(const GemmArgs& p, int i, int n, int32_t acc) {
+// Epilogue for one accumulator element (acc already row-sum corrected);
+// ad = a_dq of the row.
+__device__ __forceinline__ void epi_scale(const GemmArgs& p, int i, int n, int32_t acc, float ad) {
   if (p.acc_out) p.acc_out[(int64_t)i * p.N + n] = acc;
-  const float f = seg_scale_of(p, n) * p.a_dq[i];
+  const float f = seg_scale_of(p, n) * ad;
   uint16_t o = f2bf((float)acc * f);
   if (p.residual) o = f2bf(bf2f(p.residual[(int64_t)i * p.n_out + n]) + bf2f(o));
   p.out[(int64_t)i * p.n_out + n] = o;
 }
-__device__ __forceinline__ void epi_relu2(const GemmArgs& p, int i, int ng, int nu, int32_t ag, int32_t au) {
+__device__ __forceinline__ void epi_relu2(const GemmArgs& p, int i, int ng, int nu, int32_t ag, int32_t au,
+                                          float ad) {
   if (p.acc_out) {
     p.acc_out[(int64_t)i * p.N + ng] = ag;
     p.acc_out[(int64_t)i * p.N + nu] = au;
   }
-  const float ad = p.a_dq[i];
   const float g = bf2f(f2bf((float)ag * (seg_scale_of(p, ng) * ad)));
   const float u = bf2f(f2bf((float)au * (seg_scale_of(p, nu) * ad)));
   const float gr = g > 0.0f ? g : 0.0f;
@@ -98,14 +133,19 @@ __device__ __forceinline__ void epi_relu2(const GemmArgs& p, int i, int ng, int 
 enum { EPI_SCALE = BTL_EPI_SCALE, EPI_RELU2 = BTL_EPI_RELU2_MUL };
 
 // ------------------------------------------------------------- decode ----
-template <int TPW, int NSB, int EPI>
-__global__ __launch_bounds__(256) void k_gemm_decode(GemmArgs p) {
+// GEMM workgroup of the decode path.  With FUSED the activations come from
+// workgroups of the same launch: wait for them after the weight loads of the
+// first pass are in flight, and read activations and scales coherently.
+template <int TPW, int NSB, int EPI, int WAVES, bool FUSED>
+__device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) {
   static_assert(EPI != EPI_RELU2 || TPW == 2, "relu2 pairs a gate tile with its up tile");
-  __shared__ int32_t red[4][TPW][16][64];
+  static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
+  constexpr int RR = 16 / WAVES;  // accumulator rows finished per thread and tile
+  __shared__ int32_t red[WAVES][TPW][16][64];
   __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int g = blockIdx.x % p.ngroups;
-  const int s = blockIdx.x / p.ngroups;
+  const int g = bid % p.ngroups;
+  const int s = bid / p.ngroups;
 
   int tile[TPW];
 #pragma unroll
@@ -113,29 +153,79 @@ __global__ __launch_bounds__(256) void k_gemm_decode(GemmArgs p) {
 
   const int sb0 = (s * p.KS) / p.splitk, sb1 = ((s + 1) * p.KS) / p.splitk;
   const int nsb = sb1 - sb0;
-  const int wb = sb0 + (wv * nsb) / 4, we = sb0 + ((wv + 1) * nsb) / 4;
+  const int wb = sb0 + (wv * nsb) / WAVES, we = sb0 + ((wv + 1) * nsb) / WAVES;
+
+  __amdgpu_buffer_rsrc_t xa_rsrc;
+  if (FUSED) xa_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)p.xa, 0, p.xa_bytes, 0x00020000);
 
   v16i acc[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) acc[t] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-  for (int base = wb; base < we; base += NSB) {
-    const int cnt = (we - base) < NSB ? (we - base) : NSB;
-    v4i b[TPW][NSB];
-    v4i a[NSB][4];
-    // Loads for the whole pass go out before any MFMA; a slot past `cnt`
-    // re-reads the pass's last superblock (valid address, cache hit).
+  // A slot past a pass's count re-reads the pass's last superblock (valid
+  // address, cache hit); only the first `cnt` slots feed MFMAs.
+  v4i b[TPW][NSB];
+  auto load_b = [&](int base, int cnt) {
 #pragma unroll
     for (int i = 0; i < NSB; ++i) {
       const int sb = base + (i < cnt ? i : cnt - 1);
 #pragma unroll
       for (int t = 0; t < TPW; ++t) b[t][i] = ld128(p.wdev + (((int64_t)tile[t] * p.KS + sb) * 64 + lane) * 4);
     }
+  };
+
+  if (FUSED)
+    for (int i = 0; i < fs.pre_sleep; ++i) __builtin_amdgcn_s_sleep(8);
+  if (wb < we) load_b(wb, (we - wb) < NSB ? (we - wb) : NSB);
+  // pass accounting of the fused handshake: issued after the wait, settled
+  // when the block exits (its latency hides behind the GEMM).
+  uint32_t pass_prev = 0;
+  const int pass_grp = bid % kSyncGroups;
+  auto settle_pass = [&]() {
+    if (!FUSED || tid != 0) return;
+    const int grp_size = fs.ngemm / kSyncGroups + (pass_grp < fs.ngemm % kSyncGroups ? 1 : 0);
+    if (pass_prev + 1 != (uint32_t)grp_size) return;
+    const int ngrp = fs.ngemm < kSyncGroups ? fs.ngemm : kSyncGroups;
+    if (atomicAdd(sync_word(fs, kPassTop), 1u) + 1 != (uint32_t)ngrp) return;
+    for (int i = 0; i < fs.nact; ++i) st_coherent(sync_word(fs, kReadyFlag + i), 0u);  // all GEMM blocks are past the wait
+    for (int i = 0; i < kSyncGroups; ++i) st_coherent(sync_word(fs, kPassGrp + i), 0u);
+    st_coherent(sync_word(fs, kPassTop), 0u);
+  };
+  float ad_pre[RR];
+  if (FUSED) {
+    // Every thread of the workgroup reaches this barrier, with or without work.
+    if (wv == 0) {
+      unsigned n = 0;
+      for (;;) {
+        const bool mine = lane >= fs.nact || ld_coherent(sync_word(fs, kReadyFlag + lane)) != 0u;
+        if (__all(mine)) break;
+        if (++n > fs.spin_limit) {
+          if (lane == 0) st_coherent(sync_word(fs, kErrorWord), 1u);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    __syncthreads();
+    if (tid == 0) pass_prev = atomicAdd(sync_word(fs, kPassGrp + pass_grp), 1u);
+    // Scales of the rows this thread finishes, loaded with the activations.
+#pragma unroll
+    for (int rr = 0; rr < RR; ++rr) ad_pre[rr] = ld_coherent(p.a_dq + acc_row(wv + WAVES * rr, lane));
+  }
+
+  int32_t rs_lane = 0;  // sum of this lane's A bytes (row lane & 31, half lane >> 5)
+  for (int base = wb; base < we; base += NSB) {
+    const int cnt = (we - base) < NSB ? (we - base) : NSB;
+    if (base != wb) load_b(base, cnt);
+    v4i a[NSB][4];
 #pragma unroll
     for (int i = 0; i < NSB; ++i) {
       const int sb = base + (i < cnt ? i : cnt - 1);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) a[i][q] = ld128(p.xa + (((int64_t)sb * 4 + q) * 64 + lane) * 16);
+      for (int q = 0; q < 4; ++q) {
+        const int off = ((sb * 4 + q) * 64 + lane) * 16;
+        a[i][q] = FUSED ? ld128_coherent(xa_rsrc, off) : ld128(p.xa + off);
+      }
     }
 #pragma unroll
     for (int i = 0; i < NSB; ++i) {
@@ -147,9 +237,18 @@ __global__ __launch_bounds__(256) void k_gemm_decode(GemmArgs p) {
             const uint32_t d = (uint32_t)b[t][i][q];
             acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][q], unpack_b(d), acc[t], 0, 0, 0);
           }
+          rs_lane = __builtin_amdgcn_sdot4(a[i][q].x, 0x01010101, rs_lane, false);
+          rs_lane = __builtin_amdgcn_sdot4(a[i][q].y, 0x01010101, rs_lane, false);
+          rs_lane = __builtin_amdgcn_sdot4(a[i][q].z, 0x01010101, rs_lane, false);
+          rs_lane = __builtin_amdgcn_sdot4(a[i][q].w, 0x01010101, rs_lane, false);
         }
       }
     }
+  }
+  __shared__ int32_t red_rs[WAVES][32];
+  {
+    const int32_t rs_row = rs_lane + __shfl_xor(rs_lane, 32, 64);
+    if (lane < 32) red_rs[wv][lane] = rs_row;
   }
 
 #pragma unroll
@@ -158,60 +257,92 @@ __global__ __launch_bounds__(256) void k_gemm_decode(GemmArgs p) {
     for (int r = 0; r < 16; ++r) red[wv][t][r][lane] = acc[t][r];
   __syncthreads();
 
-  // Thread (wv, lane) finishes accumulator rows r = wv + 4*rr of every tile.
-  int32_t v[TPW][4];
+  // Thread (wv, lane) finishes accumulator rows r = wv + WAVES*rr of every
+  // tile, minus this K slice's part of the row sum.
+  int32_t v[TPW][RR];
 #pragma unroll
-  for (int t = 0; t < TPW; ++t)
+  for (int rr = 0; rr < RR; ++rr) {
+    const int r = wv + WAVES * rr;
+    const int i = acc_row(r, lane);
+    int32_t rs = 0;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int r = wv + 4 * rr;
-      v[t][rr] = red[0][t][r][lane] + red[1][t][r][lane] + red[2][t][r][lane] + red[3][t][r][lane];
+    for (int w = 0; w < WAVES; ++w) rs += red_rs[w][i];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      int32_t sum = -rs;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) sum += red[w][t][r][lane];
+      v[t][rr] = sum;
     }
+  }
 
   if (p.splitk > 1) {
+    // Publish this slice's partial tile; the last slice to arrive sums all
+    // of them (integers: any order gives the same result) and finishes.
     int32_t* part = p.ws_part + ((int64_t)(g * p.splitk + s) * TPW) * 1024;
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        __hip_atomic_store(part + t * 1024 + (wv + 4 * rr) * 64 + lane, v[t][rr], __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    __threadfence();
+      for (int rr = 0; rr < RR; ++rr) st_coherent(part + t * 1024 + (wv + WAVES * rr) * 64 + lane, v[t][rr]);
+    wait_memory();
     __syncthreads();
     if (tid == 0) {
       const unsigned prev = atomicAdd(p.ws_cnt + g, 1u);
       s_last = (prev == (unsigned)(p.splitk - 1));
     }
     __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+    if (!s_last) {
+      settle_pass();
+      return;
+    }
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        int32_t sum = 0;
+      for (int rr = 0; rr < RR; ++rr) {
+        int32_t sum = v[t][rr];
         for (int ss = 0; ss < p.splitk; ++ss)
-          sum += __hip_atomic_load(p.ws_part + ((int64_t)(g * p.splitk + ss) * TPW + t) * 1024 +
-                                       (wv + 4 * rr) * 64 + lane,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (ss != s)
+            sum += ld_coherent(p.ws_part + ((int64_t)(g * p.splitk + ss) * TPW + t) * 1024 +
+                               (wv + WAVES * rr) * 64 + lane);
         v[t][rr] = sum;
       }
-    if (tid == 0) __hip_atomic_store(p.ws_cnt + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) st_coherent(p.ws_cnt + g, 0u);
   }
 
   const int j = lane & 31;
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int i = acc_row(wv + 4 * rr, lane);
+  for (int rr = 0; rr < RR; ++rr) {
+    const int i = acc_row(wv + WAVES * rr, lane);
     if (i >= p.M) continue;
-    const int32_t rs = p.rowsum[i];
+    const float ad = FUSED ? ad_pre[rr] : p.a_dq[i];
     if (EPI == EPI_RELU2) {
-      epi_relu2(p, i, tile[0] * 32 + j, tile[1] * 32 + j, v[0][rr] - rs, v[1][rr] - rs);
+      epi_relu2(p, i, tile[0] * 32 + j, tile[1] * 32 + j, v[0][rr], v[1][rr], ad);
     } else {
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) epi_scale(p, i, tile[t] * 32 + j, v[t][rr] - rs);
+      for (int t = 0; t < TPW; ++t) epi_scale(p, i, tile[t] * 32 + j, v[t][rr], ad);
     }
   }
+  settle_pass();
+}
+
+template <int TPW, int NSB, int EPI, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_gemm_decode(GemmArgs p) {
+  gemm_decode_wg<TPW, NSB, EPI, WAVES, false>(p, blockIdx.x, FusedSync{});
+}
+
+// One launch per decode BitLinear: blocks [0, nact) quantise the token rows,
+// blocks [nact, nact + ngemm) run the GEMM.  Activation blocks come first in
+// dispatch order, so they never wait behind GEMM blocks.
+template <int TPW, int NSB, int EPI, bool NORM, int CPT>
+__global__ __launch_bounds__(512) void k_bitlinear_decode(GemmArgs p, ActArgs a, FusedSync fs) {
+  if ((int)blockIdx.x < fs.nact) {
+    act_row<NORM, true, true, CPT>(a, blockIdx.x, threadIdx.x);
+    wait_memory();
+    __syncthreads();
+    if (threadIdx.x == 0) st_coherent(sync_word(fs, kReadyFlag + (int)blockIdx.x), 1u);
+    return;
+  }
+  gemm_decode_wg<TPW, NSB, EPI, 8, true>(p, blockIdx.x - fs.nact, fs);
 }
 
 // ------------------------------------------------------------ prefill ----
@@ -257,6 +388,7 @@ __global__ __launch_bounds__(256) void k_gemm_prefill(GemmArgs p) {
     for (int y = 0; y < 2; ++y) acc[x][y] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
   const int KS = p.KS;
+  int32_t rs_lane[2] = {0, 0};  // A-operand byte sums of the two row blocks
   v4i a[2][4], b[2], an[2][4], bn[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
@@ -281,6 +413,10 @@ __global__ __launch_bounds__(256) void k_gemm_prefill(GemmArgs p) {
       for (int x = 0; x < 2; ++x) {
         acc[x][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[x][q], b0, acc[x][0], 0, 0, 0);
         acc[x][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[x][q], b1, acc[x][1], 0, 0, 0);
+        rs_lane[x] = __builtin_amdgcn_sdot4(a[x][q].x, 0x01010101, rs_lane[x], false);
+        rs_lane[x] = __builtin_amdgcn_sdot4(a[x][q].y, 0x01010101, rs_lane[x], false);
+        rs_lane[x] = __builtin_amdgcn_sdot4(a[x][q].z, 0x01010101, rs_lane[x], false);
+        rs_lane[x] = __builtin_amdgcn_sdot4(a[x][q].w, 0x01010101, rs_lane[x], false);
       }
     }
 #pragma unroll
@@ -294,24 +430,56 @@ __global__ __launch_bounds__(256) void k_gemm_prefill(GemmArgs p) {
   const int j = lane & 31;
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
+    // lanes l and l+32 hold the two halves of row l & 31
+    const int32_t rs_row = rs_lane[x] + __shfl_xor(rs_lane[x], 32, 64);
     if (!mok[x]) continue;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
+      const int32_t rs = __shfl(rs_row, acc_row(r, lane), 64);
       const int i = mblk[x] * 32 + acc_row(r, lane);
       if (i >= p.M) continue;
-      const int32_t rs = p.rowsum[i];
+      const float ad = p.a_dq[i];
       if (EPI == EPI_RELU2) {
-        if (tok[0]) epi_relu2(p, i, tile[0] * 32 + j, tile[1] * 32 + j, acc[x][0][r] - rs, acc[x][1][r] - rs);
+        if (tok[0]) epi_relu2(p, i, tile[0] * 32 + j, tile[1] * 32 + j, acc[x][0][r] - rs, acc[x][1][r] - rs, ad);
       } else {
 #pragma unroll
         for (int u = 0; u < 2; ++u)
-          if (tok[u]) epi_scale(p, i, tile[u] * 32 + j, acc[x][u][r] - rs);
+          if (tok[u]) epi_scale(p, i, tile[u] * 32 + j, acc[x][u][r] - rs, ad);
       }
     }
   }
 }
 
 // ------------------------------------------------------------- planning --
+// Waves per standalone decode workgroup: 8 (two per SIMD) unless
+// BTL_DECODE_WAVES=4.  The fused kernel always runs 8.
+static int decode_waves() {
+  static const int w = [] {
+    const char* e = getenv("BTL_DECODE_WAVES");
+    return (e && atoi(e) == 4) ? 4 : 8;
+  }();
+  return w;
+}
+
+// Compute units of the current device (256 on MI355X), cached per device.
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+      (void)hipGetLastError();
+      cus = 256;
+    }
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
 static int nsb_bucket(int per_wave) {
   if (per_wave <= 2) return 2;
   if (per_wave <= 4) return 4;
@@ -319,28 +487,36 @@ static int nsb_bucket(int per_wave) {
   return 8;
 }
 
-GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req) {
+constexpr int kFusedActBlocks = 32;
+constexpr int64_t kSyncBytes = 8192;  // handshake words of the fused decode kernel
+
+// Delay of the GEMM blocks' weight loads in the fused kernel (rounds of
+// s_sleep 8, about 0.2 us each) so the row loads of the activation blocks are
+// not queued behind the weight stream; BTL_FUSED_DELAY overrides it.
+static int fused_pre_sleep() {
+  static const int v = [] {
+    const char* e = getenv("BTL_FUSED_DELAY");
+    return e ? atoi(e) : 0;
+  }();
+  return v;
+}
+
+// max_wgs: cap on workgroups (the fused kernel keeps every block resident).
+static GemmPlan plan_decode(int64_t K, int64_t N, int epilogue, int splitk_req, int waves, int max_wgs) {
   GemmPlan pl = {};
   const int64_t KS = ksb(K), NT = N / 32;
-  if (M > 32) {
-    pl.prefill = true;
-    pl.tpw = 0;
-    pl.ngroups = 0;
-    pl.splitk = 1;
-    pl.ws_bytes = 0;
-    return pl;
-  }
   pl.prefill = false;
+  pl.waves = waves;
   pl.tpw = 2;
-  if (epilogue == BTL_EPI_SCALE && NT % 2) pl.tpw = 1;
-  if (epilogue == BTL_EPI_SCALE && NT <= 160) pl.tpw = 1;  // small N: spread tiles over more CUs
+  if (epilogue == BTL_EPI_SCALE && (NT % 2 || NT <= 160)) pl.tpw = 1;  // small N: spread tiles over more CUs
   pl.ngroups = (int)((epilogue == BTL_EPI_RELU2_MUL) ? NT / 2 : NT / pl.tpw);
   int sk = splitk_req;
   if (sk <= 0) {
-    // Aim for about one workgroup per CU (256 CUs) without making a wave's
-    // share of K smaller than one superblock.
-    sk = (int)((256 + pl.ngroups / 2) / pl.ngroups);
+    // About one workgroup per CU, without making a wave's share of K
+    // smaller than one superblock.
+    sk = (int)((max_wgs + pl.ngroups / 2) / pl.ngroups);
     if (sk < 1) sk = 1;
+    while (sk > 1 && (int64_t)sk * pl.ngroups > max_wgs) --sk;
   }
   const int max_sk = (int)(KS / 4 > 1 ? KS / 4 : 1);
   if (sk > max_sk) sk = max_sk;
@@ -354,25 +530,74 @@ GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req
   return pl;
 }
 
+GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req) {
+  if (M > 32) {
+    GemmPlan pl = {};
+    pl.prefill = true;
+    pl.splitk = 1;
+    return pl;
+  }
+  return plan_decode(K, N, epilogue, splitk_req, decode_waves(), device_cus());
+}
+
+// Fused plan: the GEMM blocks plus the activation blocks fit on the device
+// at once.  fused = false when the shape needs more GEMM blocks than that.
+static GemmPlan plan_fused(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req) {
+  if (M > 32) return plan_gemm(M, K, N, epilogue, splitk_req);
+  const int max_wgs = device_cus() - kFusedActBlocks;
+  GemmPlan pl = plan_decode(K, N, epilogue, splitk_req, 8, max_wgs);
+  pl.fused = (int64_t)pl.ngroups * pl.splitk <= max_wgs && act_cpt(K) <= 4;
+  return pl;
+}
+
 FusedLayout fused_layout(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req) {
   FusedLayout L;
   const int64_t rows = mblocks(M) * 32;
-  L.xa = 0;
-  L.a_dq = round_up(btl_act_bytes(M, K), 256);
-  L.rowsum = L.a_dq + round_up(rows * 4, 256);
-  L.gemm_ws = L.rowsum + round_up(rows * 4, 256);
-  L.total = L.gemm_ws + plan_gemm(M, K, N, epilogue, splitk_req).ws_bytes;
+  L.xa = kSyncBytes;
+  L.a_dq = L.xa + round_up(btl_act_bytes(M, K), 256);
+  L.gemm_ws = L.a_dq + round_up(rows * 4, 256);
+  const GemmPlan pf = plan_fused(M, K, N, epilogue, splitk_req);
+  const GemmPlan pg = plan_gemm(M, K, N, epilogue, splitk_req);
+  L.total = L.gemm_ws + (pf.ws_bytes > pg.ws_bytes ? pf.ws_bytes : pg.ws_bytes);
   return L;
 }
 
-template <int TPW, int EPI>
+template <int TPW, int EPI, int WAVES>
 static void launch_decode_nsb(int nsb, dim3 grid, hipStream_t s, const GemmArgs& a) {
+  const dim3 block(64 * WAVES);
   switch (nsb) {
-    case 2: hipLaunchKernelGGL((k_gemm_decode<TPW, 2, EPI>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((k_gemm_decode<TPW, 4, EPI>), grid, dim3(256), 0, s, a); break;
-    case 6: hipLaunchKernelGGL((k_gemm_decode<TPW, 6, EPI>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((k_gemm_decode<TPW, 8, EPI>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_gemm_decode<TPW, 2, EPI, WAVES>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_gemm_decode<TPW, 4, EPI, WAVES>), grid, block, 0, s, a); break;
+    case 6: hipLaunchKernelGGL((k_gemm_decode<TPW, 6, EPI, WAVES>), grid, block, 0, s, a); break;
+    default:  // 8 superblocks a pass (6 where 8 would spill, see decode_nsb)
+      hipLaunchKernelGGL((k_gemm_decode<TPW, (WAVES == 8 && TPW == 2) ? 6 : 8, EPI, WAVES>), grid, block, 0, s, a);
+      break;
   }
+}
+
+template <int TPW, int EPI, bool NORM, int CPT>
+static void launch_fused_nsb(int nsb, dim3 grid, hipStream_t s, const GemmArgs& g, const ActArgs& a,
+                             const FusedSync& fs) {
+  const dim3 block(512);
+  switch (nsb) {
+    case 2: hipLaunchKernelGGL((k_bitlinear_decode<TPW, 2, EPI, NORM, CPT>), grid, block, 0, s, g, a, fs); break;
+    case 4: hipLaunchKernelGGL((k_bitlinear_decode<TPW, 4, EPI, NORM, CPT>), grid, block, 0, s, g, a, fs); break;
+    case 6: hipLaunchKernelGGL((k_bitlinear_decode<TPW, 6, EPI, NORM, CPT>), grid, block, 0, s, g, a, fs); break;
+    default:
+      hipLaunchKernelGGL((k_bitlinear_decode<TPW, TPW == 2 ? 6 : 8, EPI, NORM, CPT>), grid, block, 0, s, g, a, fs);
+      break;
+  }
+}
+
+// Superblocks per pass: the slice's share per wave, bucketed.  Two waves per
+// SIMD leave 256 registers a wave: 2 tiles x 8 superblocks would spill, so
+// such slices run as passes of 6.
+static int decode_nsb(const GemmPlan& pl, int64_t KS, int epilogue) {
+  const int per_wg = (int)((KS + pl.splitk - 1) / pl.splitk);
+  const int per_wave = (per_wg + pl.waves - 1) / pl.waves;
+  int nsb = nsb_bucket(per_wave);
+  if (pl.waves == 8 && (pl.tpw == 2 || epilogue == BTL_EPI_RELU2_MUL) && nsb > 6) nsb = 6;
+  return nsb;
 }
 
 static int check_gemm_args(const char* who, int64_t M, int64_t K, int64_t N, const uint32_t* wdev,
@@ -408,14 +633,13 @@ static int check_gemm_args(const char* who, int64_t M, int64_t K, int64_t N, con
   return BTL_OK;
 }
 
-static int launch_gemm(const int8_t* xa, const float* a_dq, const int32_t* rowsum, int64_t M, int64_t K, int64_t N,
-                       const uint32_t* wdev, const float* seg_scale, const int64_t* seg_end, int nseg, int epilogue,
-                       const uint16_t* residual, uint16_t* out, int32_t* acc_out, char* ws, const GemmPlan& pl,
-                       hipStream_t s) {
+static GemmArgs gemm_args(const int8_t* xa, const float* a_dq, int64_t M, int64_t K,
+                          int64_t N, const uint32_t* wdev, const float* seg_scale, const int64_t* seg_end, int nseg,
+                          int epilogue, const uint16_t* residual, uint16_t* out, int32_t* acc_out, char* ws,
+                          const GemmPlan& pl) {
   GemmArgs a = {};
   a.xa = xa;
   a.a_dq = a_dq;
-  a.rowsum = rowsum;
   a.wdev = wdev;
   a.M = (int)M;
   a.KS = (int)ksb(K);
@@ -423,6 +647,7 @@ static int launch_gemm(const int8_t* xa, const float* a_dq, const int32_t* rowsu
   a.N = (int)N;
   a.n_out = (int)(epilogue == BTL_EPI_RELU2_MUL ? N / 2 : N);
   a.Mb = (int)mblocks(M);
+  a.xa_bytes = (int)btl_act_bytes(M, K);
   a.nseg = nseg;
   for (int i = 0; i < BTL_MAX_SEGMENTS; ++i) {
     a.seg_scale[i] = i < nseg ? seg_scale[i] : 0.0f;
@@ -431,6 +656,16 @@ static int launch_gemm(const int8_t* xa, const float* a_dq, const int32_t* rowsu
   a.residual = residual;
   a.out = out;
   a.acc_out = acc_out;
+  a.splitk = pl.splitk;
+  a.ngroups = pl.ngroups;
+  if (!pl.prefill && pl.splitk > 1) {
+    a.ws_cnt = reinterpret_cast<uint32_t*>(ws);
+    a.ws_part = reinterpret_cast<int32_t*>(ws + round_up((int64_t)pl.ngroups * 4, 256));
+  }
+  return a;
+}
+
+static int launch_gemm(const GemmArgs& a, int epilogue, const GemmPlan& pl, hipStream_t s) {
   if (pl.prefill) {
     const int ngn = (epilogue == BTL_EPI_RELU2_MUL) ? (int)((a.NT / 2 + 1) / 2) : (a.NT + 3) / 4;
     dim3 grid((unsigned)ngn, (unsigned)((a.Mb + 3) / 4));
@@ -440,23 +675,45 @@ static int launch_gemm(const int8_t* xa, const float* a_dq, const int32_t* rowsu
       hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE>), grid, dim3(256), 0, s, a);
     return check_launch("ternary gemm (prefill)");
   }
-  a.splitk = pl.splitk;
-  a.ngroups = pl.ngroups;
-  if (pl.splitk > 1) {
-    a.ws_cnt = reinterpret_cast<uint32_t*>(ws);
-    a.ws_part = reinterpret_cast<int32_t*>(ws + round_up((int64_t)pl.ngroups * 4, 256));
-  }
-  const int per_wg = (int)((a.KS + pl.splitk - 1) / pl.splitk);
-  const int per_wave = (per_wg + 3) / 4;
-  const int nsb = nsb_bucket(per_wave);
+  const int nsb = decode_nsb(pl, a.KS, epilogue);
   dim3 grid((unsigned)(pl.ngroups * pl.splitk));
-  if (epilogue == BTL_EPI_RELU2_MUL)
-    launch_decode_nsb<2, EPI_RELU2>(nsb, grid, s, a);
-  else if (pl.tpw == 2)
-    launch_decode_nsb<2, EPI_SCALE>(nsb, grid, s, a);
-  else
-    launch_decode_nsb<1, EPI_SCALE>(nsb, grid, s, a);
+  if (pl.waves == 8) {
+    if (epilogue == BTL_EPI_RELU2_MUL)
+      launch_decode_nsb<2, EPI_RELU2, 8>(nsb, grid, s, a);
+    else if (pl.tpw == 2)
+      launch_decode_nsb<2, EPI_SCALE, 8>(nsb, grid, s, a);
+    else
+      launch_decode_nsb<1, EPI_SCALE, 8>(nsb, grid, s, a);
+  } else {
+    if (epilogue == BTL_EPI_RELU2_MUL)
+      launch_decode_nsb<2, EPI_RELU2, 4>(nsb, grid, s, a);
+    else if (pl.tpw == 2)
+      launch_decode_nsb<2, EPI_SCALE, 4>(nsb, grid, s, a);
+    else
+      launch_decode_nsb<1, EPI_SCALE, 4>(nsb, grid, s, a);
+  }
   return check_launch("ternary gemm (decode)");
+}
+
+template <bool NORM, int CPT>
+static void launch_fused_epi(int epilogue, const GemmPlan& pl, int nsb, dim3 grid, hipStream_t s, const GemmArgs& g,
+                             const ActArgs& a, const FusedSync& fs) {
+  if (epilogue == BTL_EPI_RELU2_MUL)
+    launch_fused_nsb<2, EPI_RELU2, NORM, CPT>(nsb, grid, s, g, a, fs);
+  else if (pl.tpw == 2)
+    launch_fused_nsb<2, EPI_SCALE, NORM, CPT>(nsb, grid, s, g, a, fs);
+  else
+    launch_fused_nsb<1, EPI_SCALE, NORM, CPT>(nsb, grid, s, g, a, fs);
+}
+
+// Rows of up to 4 chunks of 8 per thread (K <= 8192) run fused.
+template <bool NORM>
+static void launch_fused(int cpt, int epilogue, const GemmPlan& pl, int nsb, dim3 grid, hipStream_t s,
+                         const GemmArgs& g, const ActArgs& a, const FusedSync& fs) {
+  if (cpt <= 2)
+    launch_fused_epi<NORM, 2>(epilogue, pl, nsb, grid, s, g, a, fs);
+  else
+    launch_fused_epi<NORM, 4>(epilogue, pl, nsb, grid, s, g, a, fs);
 }
 
 }  // namespace btl
@@ -475,20 +732,22 @@ int64_t btl_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int epilogue, 
   return plan_gemm(M, K, N, epilogue, splitk).ws_bytes;
 }
 
+int64_t btl_fused_error_offset(void) { return (int64_t)kErrorWord * kSyncStride * 4; }
+
 int64_t btl_fused_workspace_bytes(int64_t M, int64_t K, int64_t N, int epilogue, int splitk) {
   if (M <= 0 || K <= 0 || N <= 0 || N % 32) return 0;
   return fused_layout(M, K, N, epilogue, splitk).total;
 }
 
-int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, const int32_t* rowsum, int64_t M, int64_t K, int64_t N,
+int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, int64_t M, int64_t K, int64_t N,
                   const uint32_t* wdev, const float* seg_scale, const int64_t* seg_end, int nseg, int epilogue,
                   const uint16_t* residual, uint16_t* out, int32_t* acc_out, void* workspace, size_t workspace_bytes,
                   int splitk, btl_stream_t stream) {
   clear_error();
   int rc = check_gemm_args("btl_gemm_i8t2", M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out);
   if (rc) return rc;
-  if (!xa || !a_dq || !rowsum) return set_error(BTL_ERR_NULL, "btl_gemm_i8t2: activation pointer is NULL");
-  if (!aligned(xa, 16) || !aligned(a_dq, 4) || !aligned(rowsum, 4) || (acc_out && !aligned(acc_out, 4)))
+  if (!xa || !a_dq) return set_error(BTL_ERR_NULL, "btl_gemm_i8t2: activation pointer is NULL");
+  if (!aligned(xa, 16) || !aligned(a_dq, 4) || (acc_out && !aligned(acc_out, 4)))
     return set_error(BTL_ERR_ALIGN, "btl_gemm_i8t2: misaligned activation or acc_out buffer");
   if (splitk < 0) return set_error(BTL_ERR_ARG, "btl_gemm_i8t2: splitk=%d", splitk);
   const GemmPlan pl = plan_gemm(M, K, N, epilogue, splitk);
@@ -499,8 +758,9 @@ int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, const int32_t* rowsum, in
                        (long long)pl.ws_bytes);
     if (!aligned(workspace, 256)) return set_error(BTL_ERR_ALIGN, "btl_gemm_i8t2: workspace must be 256-byte aligned");
   }
-  return launch_gemm(xa, a_dq, rowsum, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out, acc_out,
-                     (char*)workspace, pl, (hipStream_t)stream);
+  const GemmArgs a = gemm_args(xa, a_dq, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out,
+                               acc_out, (char*)workspace, pl);
+  return launch_gemm(a, epilogue, pl, (hipStream_t)stream);
 }
 
 int btl_bitlinear_fused(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint16_t* gamma, float norm_eps,
@@ -521,17 +781,55 @@ int btl_bitlinear_fused(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, co
   if ((int64_t)workspace_bytes < L.total)
     return set_error(BTL_ERR_WORKSPACE, "btl_bitlinear_fused: workspace %zu < %lld bytes", workspace_bytes,
                      (long long)L.total);
-  const GemmPlan pl = plan_gemm(M, K, N, epilogue, splitk);
   char* ws = (char*)workspace;
   hipStream_t s = (hipStream_t)stream;
-  // The activation kernel also clears the split-K counters, so a workspace
-  // left dirty by an interrupted call is repaired by the next one.
-  rc = launch_act(x, M, K, ldx, gamma, norm_eps, (int8_t*)(ws + L.xa), (float*)(ws + L.a_dq),
-                  (int32_t*)(ws + L.rowsum), nullptr, xq_debug, nullptr, pl.splitk > 1 ? (uint32_t*)(ws + L.gemm_ws) : nullptr,
-                  pl.splitk > 1 ? pl.ngroups : 0, s);
+  int8_t* xa = (int8_t*)(ws + L.xa);
+  float* a_dq = (float*)(ws + L.a_dq);
+
+  const GemmPlan pf = plan_fused(M, K, N, epilogue, splitk);
+  if (pf.fused) {
+    ActArgs a = {};
+    a.x = x;
+    a.ldx = ldx;
+    a.M = (int)M;
+    a.K = (int)K;
+    a.KS = (int)ksb(K);
+    a.gamma = gamma;
+    a.norm_eps = norm_eps;
+    a.act_eps = 1e-5f;
+    a.xa = xa;
+    a.a_dq = a_dq;
+    a.rowsum = nullptr;
+    a.xq_rm = xq_debug;
+    // Row 0 also clears the split-K counters, so a workspace left dirty by an
+    // interrupted call is repaired by the next one.
+    a.zero_words = pf.splitk > 1 ? (uint32_t*)(ws + L.gemm_ws) : nullptr;
+    a.n_zero_words = pf.splitk > 1 ? pf.ngroups : 0;
+    const GemmArgs g = gemm_args(xa, a_dq, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out,
+                                 acc_out, ws + L.gemm_ws, pf);
+    FusedSync fs;
+    fs.words = (uint32_t*)ws;
+    fs.nact = kFusedActBlocks;
+    fs.ngemm = pf.ngroups * pf.splitk;
+    fs.spin_limit = 1u << 20;
+    fs.pre_sleep = fused_pre_sleep();
+    const int nsb = decode_nsb(pf, ksb(K), epilogue);
+    const dim3 grid((unsigned)(kFusedActBlocks + fs.ngemm));
+    const int cpt = act_cpt(K);
+    if (gamma)
+      launch_fused<true>(cpt, epilogue, pf, nsb, grid, s, g, a, fs);
+    else
+      launch_fused<false>(cpt, epilogue, pf, nsb, grid, s, g, a, fs);
+    return check_launch("fused decode BitLinear");
+  }
+
+  const GemmPlan pl = plan_gemm(M, K, N, epilogue, splitk);
+  rc = launch_act(x, M, K, ldx, gamma, norm_eps, xa, a_dq, nullptr, nullptr, xq_debug, nullptr,
+                  pl.splitk > 1 ? (uint32_t*)(ws + L.gemm_ws) : nullptr, pl.splitk > 1 ? pl.ngroups : 0, s);
   if (rc) return rc;
-  return launch_gemm((const int8_t*)(ws + L.xa), (const float*)(ws + L.a_dq), (const int32_t*)(ws + L.rowsum), M, K,
-                     N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out, acc_out, ws + L.gemm_ws, pl, s);
+  const GemmArgs g = gemm_args(xa, a_dq, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out,
+                               acc_out, ws + L.gemm_ws, pl);
+  return launch_gemm(g, epilogue, pl, s);
 }
 
 }  // extern "C"

@@ -117,7 +117,7 @@ int btl_repack(const uint8_t* packed, int64_t K, int64_t N, uint32_t* wdev, btl_
  *   y = gamma ? bf16(gamma * bf16(x / sqrt(mean(x^2) + norm_eps))) : x
  *   a = max(max|y|, 1e-5); q = clip(rne(y * (127/a)), -128, 127)
  * Outputs: xa (btl_act_bytes(M,K), blocked layout the GEMM reads),
- * a_dq[32*ceil(M/32)] = a/127, rowsum[32*ceil(M/32)] = sum_k q,
+ * a_dq[32*ceil(M/32)] = a/127, optional rowsum[32*ceil(M/32)] = sum_k q,
  * optional act_scale[M] = 127/a (the scale quantization.py returns),
  * optional xq_rowmajor [M,K] int8 and y_rowmajor [M,K] bf16.
  * x is [M,K] with row stride ldx elements (ldx % 8 == 0).                */
@@ -132,7 +132,7 @@ int btl_rmsnorm(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint
 /* ---- the ternary GEMM ------------------------------------------------ */
 
 /* acc[m,n] = sum_k q[m,k] * w[k,n] in int32 (exact), then the epilogue.
- * xa/a_dq/rowsum as produced by btl_quant_absmax for the same M, K.
+ * xa/a_dq as produced by btl_quant_absmax for the same M, K.
  * seg_scale/seg_end: host arrays of nseg (1..4) weight scales and exclusive
  * column ends (multiples of 32, last == N) -- per-projection scales of the
  * fused QKV / gate||up weights (src/bitnet_tt/layers/attention.py:481-506,
@@ -142,17 +142,26 @@ int btl_rmsnorm(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint
  * splitk: 0 = library's choice.  workspace: btl_gemm_workspace_bytes(...)
  * bytes; its counters must be zero before the first call and are left zero
  * by every completed call.                                                 */
-int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, const int32_t* rowsum, int64_t M, int64_t K,
-                  int64_t N, const uint32_t* wdev, const float* seg_scale, const int64_t* seg_end, int nseg,
-                  int epilogue, const uint16_t* residual, uint16_t* out, int32_t* acc_out, void* workspace,
+int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, int64_t M, int64_t K, int64_t N, const uint32_t* wdev,
+                  const float* seg_scale, const int64_t* seg_end, int nseg, int epilogue, const uint16_t* residual, uint16_t* out, int32_t* acc_out, void* workspace,
                   size_t workspace_bytes, int splitk, btl_stream_t stream);
+
+/* Byte offset, inside a btl_bitlinear_fused workspace, of the 32-bit word
+ * that is non-zero when a bounded wait of the single-launch decode kernel
+ * ran out (the outputs of that call are then invalid).  The first 8192 bytes
+ * of the workspace hold that kernel's handshake words; they must be zero
+ * before the first call and every completed call leaves them zero. */
+int64_t btl_fused_error_offset(void);
 
 /* One BitLinear launch sequence: [RMSNorm(gamma) ->] absmax quant -> ternary
  * GEMM -> epilogue.  This is ternary_matmul(x, W, norm_weight=gamma,
  * norm_epsilon=eps) followed by the scale multiply
  * (src/bitnet_tt/inference/generator_batch32.py:721-727;
  * src/bitnet_tt/layers/bitlinear.py:309-353).  Arguments as above;
- * xq_debug [M,K] int8 optional.  workspace: btl_fused_workspace_bytes(...). */
+ * xq_debug [M,K] int8 optional.  workspace: btl_fused_workspace_bytes(...),
+ * zero-filled once before first use.  For M <= 32 (decode) the whole
+ * sequence is one launch: 32 workgroups quantise the token rows while the
+ * GEMM workgroups already stream their weights. */
 int btl_bitlinear_fused(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint16_t* gamma,
                         float norm_eps, const uint32_t* wdev, int64_t N, const float* seg_scale,
                         const int64_t* seg_end, int nseg, int epilogue, const uint16_t* residual, uint16_t* out,

@@ -35,6 +35,7 @@ def test_library_loads_and_exports_every_declaration(L):
         assert name in N.EXPORTS, f"{name} has no ctypes signature"
     assert set(N.EXPORTS) == set(names)
     assert L.btl_version() == 100
+    assert L.btl_fused_error_offset() % 4 == 0 and 0 < L.btl_fused_error_offset() < 8192
 
 
 def test_size_helpers(L):
@@ -74,12 +75,12 @@ def _p(x):
 
 
 def call_gemm(L, **kw):
-    a = dict(xa=_p(FAKE), a_dq=_p(FAKE), rowsum=_p(FAKE), M=32, K=256, N=64, wdev=_p(FAKE), nseg=1, epi=0,
+    a = dict(xa=_p(FAKE), a_dq=_p(FAKE), M=32, K=256, N=64, wdev=_p(FAKE), nseg=1, epi=0,
              residual=None, out=_p(FAKE), acc=None, ws=None, ws_bytes=0, splitk=1)
     a.update(kw)
     sc = (ctypes.c_float * 4)(1.0, 1.0, 1.0, 1.0)
     en = (ctypes.c_int64 * 4)(*(kw.get("ends") or (a["N"], a["N"], a["N"], a["N"])))
-    return L.btl_gemm_i8t2(a["xa"], a["a_dq"], a["rowsum"], a["M"], a["K"], a["N"], a["wdev"], sc, en, a["nseg"],
+    return L.btl_gemm_i8t2(a["xa"], a["a_dq"], a["M"], a["K"], a["N"], a["wdev"], sc, en, a["nseg"],
                            a["epi"], a["residual"], a["out"], a["acc"], a["ws"], a["ws_bytes"], a["splitk"], None)
 
 

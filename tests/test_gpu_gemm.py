@@ -22,8 +22,8 @@ def device_weight(orc, w_kn):
 
 
 def run_gemm(orc, q, w_kn, scales, ends=None, epi=0, splitk=0, residual_bits=None, wdev=None):
-    """int8 q [m,k] x ternary w [k,n] through btl_gemm_i8t2; a_dq from the
-    oracle's quantiser convention is replaced by a fixed per-row factor."""
+    """int8 q [m,k] x ternary w [k,n] through btl_gemm_i8t2 with a random
+    per-row dequantisation factor a_dq (the row sums come from the operand)."""
     L = N.lib()
     d = H.dev()
     m, k = q.shape
@@ -32,8 +32,6 @@ def run_gemm(orc, q, w_kn, scales, ends=None, epi=0, splitk=0, residual_bits=Non
     rng = np.random.default_rng(m + k + n)
     a_dq = np.zeros(rows, np.float32)
     a_dq[:m] = (0.005 + 0.03 * rng.random(m)).astype(np.float32)
-    rowsum = np.zeros(rows, np.int32)
-    rowsum[:m] = q.astype(np.int64).sum(1)
     xa = H.to_dev(H.rowmajor_to_xa(q))
     wdev = device_weight(orc, w_kn) if wdev is None else wdev
     ends = ends or [n]
@@ -47,7 +45,8 @@ def run_gemm(orc, q, w_kn, scales, ends=None, epi=0, splitk=0, residual_bits=Non
         res = out  # in place: out = residual + result
     ws_bytes = int(L.btl_gemm_workspace_bytes(m, k, n, epi, splitk))
     ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=d)
-    N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(H.to_dev(a_dq)), N.ptr(H.to_dev(rowsum)), m, k, n, N.ptr(wdev), sc, en,
+    a_dq_d = H.to_dev(a_dq)  # keep the tensor alive across the launch
+    N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(a_dq_d), m, k, n, N.ptr(wdev), sc, en,
                             nseg, epi, N.ptr(res), N.ptr(out), N.ptr(acc), N.ptr(ws), ws.numel(), splitk,
                             N.stream_of(d)), "btl_gemm_i8t2")
     torch.cuda.synchronize()
@@ -181,3 +180,26 @@ def test_fused_entry_matches_split_path(orc):
         assert np.array_equal(xq.cpu().numpy(), ref["q"])
         assert np.array_equal(acc.cpu().numpy(), ref["acc"])
         assert np.array_equal(H.bits_of(out), ref["out"])
+
+
+def test_fused_decode_handshake_clean(orc):
+    """The single-launch decode path (activation blocks + GEMM blocks) leaves its
+    producer/consumer words at zero and never reports a timed-out wait."""
+    from bitnet_tt.ternary_matmul import PackedTernaryWeight, ternary_matmul
+
+    for m, k, n, epi in [(32, 2560, 3840, "none"), (5, 6912, 2560, "none"), (32, 2560, 1024, "relu2_mul")]:
+        xb = H.activations(orc, m, k, seed=m + k)
+        w = H.ternary(k, n, seed=n)
+        ends = (n // 2, n) if epi == "relu2_mul" else (n,)
+        pw = PackedTernaryWeight(device_weight(orc, w), k, n, (0.02,) * len(ends), ends)
+        for _ in range(3):
+            out = ternary_matmul(H.to_dev_bf16(xb), pw, epilogue=epi)
+        torch.cuda.synchronize()
+        ref = orc.bitlinear(xb, w, [0.02] * len(ends), list(ends))
+        exp = ref["out"] if epi == "none" else orc.relu2_mul_bf16(ref["out"][:, : n // 2], ref["out"][:, n // 2:])
+        assert np.array_equal(H.bits_of(out), exp)
+    err = int(N.lib().btl_fused_error_offset())
+    for ws in N._workspaces.values():
+        words = ws[:8192].view(torch.int32).cpu().numpy()
+        assert words[err // 4] == 0, "a bounded wait ran out"
+        assert not words.any(), "handshake counters must be reset after every call"
