@@ -12,9 +12,10 @@ stand-in buffer.  The step is captured once in a HIP graph and replayed.
 
 Printed JSON (one line): value = algorithmic HBM bytes of a step / step time
 (GB/s), ms_per_step = BitLinear ms per decode step, plus the roofline of the
-dominant kernel (the gate||up GEMM) measured with HIP events on the launch
-stream, the prefill MFMA-i8 utilisation, and the CPU oracle timed on the
-host as a reported baseline.
+dominant kernel (the BitLinear kind with the longest launch) measured with HIP
+events on the launch stream, the prefill MFMA-i8 utilisation, and the CPU
+oracle timed on the host as a reported baseline.  ``--pmc-pass`` runs only
+the workload of the rocprofv3 --pmc traffic measurement.
 """
 
 from __future__ import annotations
@@ -49,95 +50,123 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="approximate CPU-baseline sample length")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="run only the workload of the rocprofv3 --pmc traffic runs and exit")
     return ap.parse_args()
 
 
 # --------------------------------------------------------------- kernels ----
-class SplitLauncher:
-    """Launches a BitLinear as its two kernels (activation prologue, GEMM) so
-    the GEMM alone can be bracketed by events on the launch stream."""
-
-    def __init__(self, step, N, torch):
-        self.N, self.torch, self.step = N, torch, step
-        self.L = N.lib()
-        self.dev = step.device
-
-    def prologue(self, x, K, gamma, eps, ws):
-        N = self.N
-        M = x.numel() // K
-        rows = 32 * ((M + 31) // 32)
-        xa = ws["xa"]
-        N.check(self.L.btl_quant_absmax(N.ptr(x), M, K, K, N.ptr(gamma), eps, N.ptr(xa), N.ptr(ws["a_dq"]),
-                                        None, None, None, None, N.stream_of(self.dev)),
-                "btl_quant_absmax")
-        return M, rows
-
-    def gemm(self, M, K, w, out, epi, residual, ws):
-        N = self.N
-        sc, en, nseg = N.segments_arrays(w.segment_scales, w.segment_ends)
-        N.check(self.L.btl_gemm_i8t2(N.ptr(ws["xa"]), N.ptr(ws["a_dq"]), M, K, w.out_features,
-                                     N.ptr(w.data), sc, en, nseg, epi, N.ptr(residual), N.ptr(out), None,
-                                     N.ptr(ws["gemm"]), ws["gemm"].numel(), 0, N.stream_of(self.dev)),
-                "btl_gemm_i8t2")
+KINDS = ("qkv", "o_proj", "gate_up", "down")
 
 
-def kernel_event_timing(step, torch, N, reps):
-    """Average duration of each GEMM kind, measured with HIP events on the
-    launch stream.  For every kind the 30 layers' GEMMs (distinct weights,
-    265 MB for gate||up: more than the 256 MB last-level cache) are recorded
-    into a graph; a replay is bracketed by two events and divided by the
-    number of launches."""
-    c = step.config
+def kind_launcher(step, kind):
+    """(launch(layer_index), description) of one BitLinear kind of the step,
+    with exactly the arguments the step's own chain passes."""
+    from bitnet_tt.ternary_matmul import ternary_matmul_into
+
+    eps = step.eps
+    if kind == "qkv":
+        def launch(i):
+            w = step.layers[i]
+            ternary_matmul_into(step.hidden, w.qkv, step.qkv_out, norm_weight=w.input_layernorm, norm_epsilon=eps)
+    elif kind == "o_proj":
+        def launch(i):
+            w = step.layers[i]
+            ternary_matmul_into(step.attn_out, w.o_proj, step.hidden, norm_weight=w.attn_sub_norm,
+                                norm_epsilon=eps, residual=step.hidden)
+    elif kind == "gate_up":
+        def launch(i):
+            w = step.layers[i]
+            ternary_matmul_into(step.hidden, w.gate_up, step.ffn_h, norm_weight=w.post_attention_layernorm,
+                                norm_epsilon=eps, epilogue="relu2_mul")
+    else:
+        def launch(i):
+            w = step.layers[i]
+            ternary_matmul_into(step.ffn_h, w.down, step.hidden, norm_weight=w.ffn_sub_norm, norm_epsilon=eps,
+                                residual=step.hidden)
+    return launch
+
+
+def kernel_event_timing(step, torch, reps):
+    """Average duration of each BitLinear kind's single-launch decode kernel,
+    measured with HIP events on the launch stream.  For every kind the 30
+    layers' launches (distinct weights: 265 MB for gate||up, more than the
+    256 MB last-level cache) are recorded into a graph; a replay is bracketed
+    by two events on that stream and divided by the number of launches."""
     dev = step.device
-    L = N.lib()
-    sl = SplitLauncher(step, N, torch)
-    kinds = {
-        "qkv": (c.hidden_size, lambda w: w.qkv, 0, step.hidden, step.qkv_out, None),
-        "o_proj": (c.num_attention_heads * c.head_dim, lambda w: w.o_proj, 0, step.attn_out, step.hidden, step.hidden),
-        "gate_up": (c.hidden_size, lambda w: w.gate_up, 1, step.hidden, step.ffn_h, None),
-        "down": (c.intermediate_size, lambda w: w.down, 0, step.ffn_h, step.hidden, step.hidden),
-    }
     res = {}
     s = torch.cuda.Stream(device=dev)
-    for name, (K, getw, epi, x, out, resid) in kinds.items():
-        w0 = getw(step.layers[0])
-        Nf = w0.out_features
-        ws = {
-            "xa": torch.empty(int(L.btl_act_bytes(32, K)), dtype=torch.uint8, device=dev),
-            "a_dq": torch.empty(32, dtype=torch.float32, device=dev),
-            "gemm": torch.zeros(max(int(L.btl_gemm_workspace_bytes(32, K, Nf, epi, 0)), 256), dtype=torch.uint8,
-                                device=dev),
-        }
-        xin = x.clone()
-        o = out.clone()
-        r = o if resid is not None else None
-        sl.prologue(xin, K, None, 0.0, ws)
+    n = len(step.layers)
+    for kind in KINDS:
+        launch = kind_launcher(step, kind)
+        step.reset_hidden()
         torch.cuda.synchronize()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
-            for lw in step.layers:  # warm the launch path once outside capture
-                sl.gemm(32, K, getw(lw), o, epi, r, ws)
+            for i in range(n):  # eager pass: workspace allocation happens outside capture
+                launch(i)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=s):
-            for lw in step.layers:
-                sl.gemm(32, K, getw(lw), o, epi, r, ws)
+            for i in range(n):
+                launch(i)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         times = []
         with torch.cuda.stream(s):
             g.replay()
             for _ in range(reps):
+                step.reset_hidden()
                 e0.record(s)
                 g.replay()
                 e1.record(s)
                 e1.synchronize()
-                times.append(e0.elapsed_time(e1) * 1e3 / len(step.layers))  # us per launch
+                times.append(e0.elapsed_time(e1) * 1e3 / n)  # us per launch
         torch.cuda.synchronize()
         times.sort()
-        res[name] = {"us_per_launch_median": times[len(times) // 2], "us_per_launch_min": times[0], "K": K, "N": Nf}
+        res[kind] = {"us_per_launch_median": times[len(times) // 2], "us_per_launch_min": times[0]}
         del g
+    step.reset_hidden()
+    torch.cuda.synchronize()
     return res
+
+
+def pmc_pass(step, torch):
+    """Workload for the rocprofv3 --pmc traffic runs: a plain 256 MiB device
+    copy (the counter calibration: it reads and writes exactly 256 MiB), then
+    two eager passes of each BitLinear kind over all layers."""
+    dev = step.device
+    a = torch.empty(128 << 20, dtype=torch.int16, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
+    for kind in KINDS:
+        launch = kind_launcher(step, kind)
+        for _ in range(2):
+            step.reset_hidden()
+            for i in range(len(step.layers)):
+                launch(i)
+        torch.cuda.synchronize()
+        log(f"[bench] pmc pass: {kind} done")
+
+
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "bitlinear_decode_b32_traffic.md")
+
+
+def committed_traffic(kind):
+    """HBM bytes per launch of a kind from the committed rocprofv3 --pmc
+    summary (lines 'traffic_bytes_per_launch <kind> <bytes>'), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.strip().strip("`").split()
+                if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kind:
+                    return int(parts[2])
+    except OSError:
+        return None
+    return None
 
 
 def gemm_algorithmic_bytes(M, K, N, epi, nseg, residual):
@@ -274,6 +303,10 @@ def main():
     log(f"[bench] model ready: {args.layers} layers in {time.time() - t0:.1f} s; "
         f"ternary split +1/0/-1 = {'/'.join(f'{v:.4f}' for v in step.ternary_split)}")
 
+    if args.pmc_pass:
+        pmc_pass(step, torch)
+        return
+
     # warm-up (eager), then capture the step on a side stream
     s = torch.cuda.Stream(device=dev)
     s.wait_stream(torch.cuda.current_stream())
@@ -303,24 +336,32 @@ def main():
     value = nbytes["step"] / (ms_per_step * 1e-3) / 1e9
     log(f"[bench] {ms_per_step * 1e3:.1f} us per step, {value:.0f} GB/s")
 
-    kt = kernel_event_timing(step, torch, N, args.kernel_reps)
+    kt = kernel_event_timing(step, torch, args.kernel_reps)
     for name, r in kt.items():
-        log(f"[bench] {name}: {r['us_per_launch_median']:.2f} us per GEMM launch (median of {args.kernel_reps})")
-    gu = kt["gate_up"]
-    gu_bytes = gemm_algorithmic_bytes(32, gu["K"], gu["N"], 1, 2, False)
-    achieved = gu_bytes / (gu["us_per_launch_median"] * 1e-6) / 1e9
+        log(f"[bench] {name}: {r['us_per_launch_median']:.2f} us per launch (median of {args.kernel_reps})")
+    # dominant kernel: the kind with the largest share of the step
+    dom = max(KINDS, key=lambda k: kt[k]["us_per_launch_median"])
+    dom_bytes = nbytes[dom]
+    dom_us = kt[dom]["us_per_launch_median"]
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    traffic = committed_traffic(dom)
     roofline = {
         "bound": "hbm",
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": None,
-        "kernel": "k_gemm_decode<2,6,relu2> (gate||up 2560->2x6912, M=32)",
-        "bytes_per_launch": gu_bytes,
-        "us_per_launch": round(gu["us_per_launch_median"], 3),
+        "traffic": traffic,
+        "kernel": f"k_bitlinear_decode ({dom}: " + {
+            "qkv": "RMSNorm->QKV 2560->3840", "o_proj": "attn_sub_norm->o_proj 2560->2560 +residual",
+            "gate_up": "RMSNorm->gate||up 2560->2x6912, relu2*up", "down": "ffn_sub_norm->down 6912->2560 +residual",
+        }[dom] + ", M=32)",
+        "bytes_per_launch": dom_bytes,
+        "us_per_launch": round(dom_us, 3),
     }
-    gemm_us = {k: round(v["us_per_launch_median"], 3) for k, v in kt.items()}
+    kernel_us = {k: round(v["us_per_launch_median"], 3) for k, v in kt.items()}
+    kernel_frac = {k: round(nbytes[k] / (kt[k]["us_per_launch_median"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+                   for k in KINDS}
 
     prefill = None
     if not args.no_prefill:
@@ -356,7 +397,8 @@ def main():
             "layers": args.layers,
             "bytes_per_step": nbytes["step"],
             "step_roofline_frac": round(value / HBM_PEAK_GBS, 4),
-            "gemm_us_per_launch": gemm_us,
+            "us_per_launch": kernel_us,
+            "roofline_frac_per_launch": kernel_frac,
         },
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -22,9 +22,9 @@
 //
 // Fused decode BitLinear (one launch): workgroups 0..31 run the activation
 // prologue of one token row each (btl_act_row.h) and publish the quantised
-// rows with coherent stores and a counter; the GEMM workgroups issue their
-// weight loads first, then wait for the counter (bounded spin), so weight
-// streaming overlaps the prologue and a launch is saved.
+// rows with coherent stores and one ready flag per row; the GEMM workgroups
+// issue their weight loads first, then wait for the 32 flags (bounded spin),
+// so weight streaming overlaps the prologue and a launch is saved.
 //
 // Prefill (M > 32): 128x128 output tiles, one 64x64 quadrant per wave, A and
 // B fragments loaded straight into registers (both operands are stored in
