@@ -336,6 +336,27 @@ def main():
     value = nbytes["step"] / (ms_per_step * 1e-3) / 1e9
     log(f"[bench] {ms_per_step * 1e3:.1f} us per step, {value:.0f} GB/s")
 
+    # the same step as persistent per-layer launches (btl_decode_layer)
+    with torch.cuda.stream(s):
+        step.reset_hidden()
+        step.step_layers()
+    torch.cuda.synchronize()
+    graph_l = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph_l, stream=s):
+        step.step_layers()
+    with torch.cuda.stream(s):
+        for _ in range(args.warmup):
+            graph_l.replay()
+    torch.cuda.synchronize()
+    t_l = time.perf_counter()
+    with torch.cuda.stream(s):
+        for _ in range(args.steps):
+            graph_l.replay()
+    torch.cuda.synchronize()
+    us_layers = (time.perf_counter() - t_l) * 1e6 / args.steps
+    del graph_l
+    log(f"[bench] persistent per-layer launches: {us_layers:.1f} us per step")
+
     kt = kernel_event_timing(step, torch, args.kernel_reps)
     for name, r in kt.items():
         log(f"[bench] {name}: {r['us_per_launch_median']:.2f} us per launch (median of {args.kernel_reps})")
@@ -397,6 +418,7 @@ def main():
             "layers": args.layers,
             "bytes_per_step": nbytes["step"],
             "step_roofline_frac": round(value / HBM_PEAK_GBS, 4),
+            "us_per_step_layer_launches": round(us_layers, 1),
             "us_per_launch": kernel_us,
             "roofline_frac_per_launch": kernel_frac,
         },

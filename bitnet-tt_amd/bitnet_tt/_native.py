@@ -37,6 +37,37 @@ _I = ctypes.c_int
 _F = ctypes.c_float
 _SZ = ctypes.c_size_t
 
+
+
+class LayerWeight(ctypes.Structure):
+    """btl_layer_weight_t: one BitLinear of a btl_decode_layer launch."""
+
+    _fields_ = [
+        ("wdev", ctypes.c_void_p),
+        ("seg_scale", ctypes.c_float * MAX_SEGMENTS),
+        ("seg_end", ctypes.c_int64 * MAX_SEGMENTS),
+        ("nseg", ctypes.c_int),
+        ("gamma", ctypes.c_void_p),
+    ]
+
+
+def layer_weight(w, gamma) -> LayerWeight:
+    """LayerWeight of a PackedTernaryWeight and the RMSNorm gain of its input."""
+    n = len(w.segment_scales)
+    if not 1 <= n <= MAX_SEGMENTS:
+        raise ValueError(f"1..{MAX_SEGMENTS} weight-scale segments are supported, got {n}")
+    lw = LayerWeight()
+    lw.wdev = w.data.data_ptr()
+    for i in range(MAX_SEGMENTS):
+        lw.seg_scale[i] = float(w.segment_scales[i]) if i < n else 0.0
+        lw.seg_end[i] = int(w.segment_ends[i]) if i < n else 0
+    lw.nseg = n
+    lw.gamma = gamma.data_ptr()
+    return lw
+
+
+_LWP = ctypes.POINTER(LayerWeight)
+
 # name -> (argtypes, restype); the exported C ABI, one entry per declaration.
 EXPORTS = {
     "btl_last_error": ([], ctypes.c_char_p),
@@ -62,6 +93,12 @@ EXPORTS = {
     ),
     "btl_bitlinear_fused": (
         [_P, _I64, _I64, _I64, _P, _F, _P, _I64, _P, _P, _I, _I, _P, _P, _P, _P, _P, _SZ, _I, _P],
+        _I,
+    ),
+    "btl_decode_layer_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64], _I64),
+    "btl_decode_layer_error_offset": ([], _I64),
+    "btl_decode_layer": (
+        [_I64, _I64, _I64, _I64, _I64, _LWP, _LWP, _LWP, _LWP, _F, _P, _P, _P, _P, _P, _SZ, _P],
         _I,
     ),
 }
@@ -148,11 +185,25 @@ def segments_arrays(scales, ends):
 _workspaces: dict = {}
 
 
-def workspace(device, nbytes: int):
+def has_workspace(device, nbytes: int, kind: str = "bitlinear") -> bool:
+    """True when the current stream already owns a workspace of nbytes."""
+    import torch
+
+    buf = _workspaces.get((kind, str(device), torch.cuda.current_stream(device).cuda_stream))
+    return buf is not None and buf.numel() >= nbytes
+
+
+def workspace(device, nbytes: int, kind: str = "bitlinear"):
+    """Zero-filled device workspace of at least nbytes for the current stream.
+
+    kind separates workspaces whose layouts differ ("bitlinear" for
+    btl_bitlinear_fused / btl_gemm_i8t2, "layer" for btl_decode_layer).  A
+    workspace that grows is replaced by a fresh zero-filled one; the old one
+    is released in stream order, after the calls that used it."""
     import torch
 
     stream = torch.cuda.current_stream(device)
-    key = (str(device), stream.cuda_stream)
+    key = (kind, str(device), stream.cuda_stream)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
         size = max(int(nbytes), 1 << 20)

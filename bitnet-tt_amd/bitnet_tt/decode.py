@@ -8,11 +8,21 @@ generator_batch32.py:713-761) issues four ternary-matmul launches:
     hidden = hidden + down(ffn_sub_norm(relu(gate)^2 * up))               :752-756
              with gate||up = BitLinear(post_attention_layernorm(hidden))
 
-Here every BitLinear is one fused launch sequence of libbtl.so and the
-remaining norms and residual adds ride along: attn_sub_norm and
-post_attention_layernorm become RMSNorm prologues, relu^2*up the gate||up
-epilogue, ffn_sub_norm the down prologue, and both residual adds epilogues.
-The attention core (RoPE, KV cache, SDPA) is outside this package: ``step``
+Here the remaining norms and residual adds ride along with the BitLinears:
+attn_sub_norm and post_attention_layernorm become RMSNorm prologues, relu^2*up
+the gate||up epilogue, ffn_sub_norm the down prologue, and both residual adds
+epilogues.  Two launch structures compute the same bits:
+
+* ``step_per_call`` (the default ``step``): one ``btl_bitlinear_fused``
+  launch per BitLinear (120 per 30-layer step);
+* ``step_layers``: layer 0's QKV as one such launch, then one
+  ``btl_decode_layer`` launch per layer covering o_proj, gate||up, down and
+  the next layer's QKV -- the BitLinear work between two attentions (31
+  launches per step).  On MI355X it measures within a few percent of the
+  per-call chain: the in-kernel hand-offs cost about what kernel boundaries
+  cost, so the default stays with the per-call launches.
+
+The attention core (RoPE, KV cache, SDPA) is outside this package: the step
 takes its output as an input buffer.
 
 All buffers are allocated once, so :meth:`BitLinearDecodeStep.step` is
@@ -23,6 +33,7 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+from . import _native as N
 from .config import BitNetConfig
 from .ternary_matmul import PackedTernaryWeight, ternary_matmul_into
 
@@ -157,10 +168,72 @@ class BitLinearDecodeStep:
                             epilogue="relu2_mul")
         ternary_matmul_into(ffn_h, w.down, hidden, norm_weight=w.ffn_sub_norm, norm_epsilon=eps, residual=hidden)
 
-    def step(self):
+    def step_per_call(self):
         for i in range(len(self.layers)):
             self.layer(i, self.hidden, self.attn_out, self.qkv_out, self.ffn_h)
         return self.hidden
+
+    # -- persistent layer launches ------------------------------------------
+    def _layer_structs(self):
+        """btl_layer_weight_t of every BitLinear (kept alive with the step)."""
+        if getattr(self, "_lw", None) is None:
+            lw = []
+            for w in self.layers:
+                lw.append((N.layer_weight(w.o_proj, w.attn_sub_norm),
+                           N.layer_weight(w.gate_up, w.post_attention_layernorm),
+                           N.layer_weight(w.down, w.ffn_sub_norm),
+                           N.layer_weight(w.qkv, w.input_layernorm)))
+            self._lw = lw
+        return self._lw
+
+    def decode_layer(self, i: int, hidden, attn_out, qkv_out, ffn_h):
+        """Layer i's o_proj, gate||up and down plus layer i+1's QKV (when
+        there is one) as one btl_decode_layer launch, in place on hidden."""
+        import ctypes
+
+        import torch
+
+        c = self.config
+        lw = self._layer_structs()
+        B = hidden.shape[0]
+        H, F, qd = c.hidden_size, c.intermediate_size, c.num_attention_heads * c.head_dim
+        nxt = lw[i + 1][3] if i + 1 < len(lw) else None
+        for t, name in ((hidden, "hidden"), (attn_out, "attn_out"), (qkv_out, "qkv_out"), (ffn_h, "ffn_h")):
+            N.require_cuda(t, name)
+        L = N.lib()
+        nbytes = int(L.btl_decode_layer_workspace_bytes(B, H, qd, F, c.qkv_dim))
+        if torch.cuda.is_current_stream_capturing() and not N.has_workspace(hidden.device, nbytes, "layer"):
+            # a workspace made inside a capture would be re-zeroed by every
+            # replay, resetting the launch counters the kernel's flags rely on
+            raise RuntimeError("run one eager decode step on this stream before capturing it in a graph")
+        ws = N.workspace(hidden.device, nbytes, kind="layer")
+        N.check(
+            L.btl_decode_layer(B, H, qd, F, c.qkv_dim, ctypes.byref(lw[i][0]), ctypes.byref(lw[i][1]),
+                               ctypes.byref(lw[i][2]), ctypes.byref(nxt) if nxt is not None else None,
+                               float(self.eps), N.ptr(attn_out), N.ptr(hidden), N.ptr(ffn_h), N.ptr(qkv_out),
+                               N.ptr(ws), ws.numel(), N.stream_of(hidden.device)),
+            "btl_decode_layer",
+        )
+
+    def layer_error_word(self) -> int:
+        """Error word of this stream's decode-layer workspace (0: no bounded
+        wait ran out)."""
+        import torch
+
+        L = N.lib()
+        ws = N.workspace(self.device, 0, kind="layer")
+        off = int(L.btl_decode_layer_error_offset())
+        return int(ws[off:off + 4].view(torch.int32).item())
+
+    def step_layers(self):
+        w0 = self.layers[0]
+        ternary_matmul_into(self.hidden, w0.qkv, self.qkv_out, norm_weight=w0.input_layernorm, norm_epsilon=self.eps)
+        for i in range(len(self.layers)):
+            self.decode_layer(i, self.hidden, self.attn_out, self.qkv_out, self.ffn_h)
+        return self.hidden
+
+    def step(self):
+        return self.step_per_call()
 
     # -- accounting ----------------------------------------------------------
     def algorithmic_bytes(self) -> dict:

@@ -78,6 +78,9 @@ __device__ __forceinline__ int32_t ld_coherent(const int32_t* p) {
 __device__ __forceinline__ uint32_t ld_coherent(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ uint64_t ld_coherent(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ float ld_coherent(const float* p) {
   return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT));
@@ -101,6 +104,98 @@ __device__ __forceinline__ void store8(int8_t* p, uint32_t lo, uint32_t hi) {
     st_coherent(reinterpret_cast<uint64_t*>(p), (uint64_t)lo | ((uint64_t)hi << 32));
   else
     *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
+}
+
+// ---- pieces of the row prologue shared by every kernel that runs it -------
+// A row lives in registers as v[i][0..7] = elements 8c..8c+7 of chunk
+// c = tid + 256*i; only chunks c < nch hold data.  Threads >= 256 of a block
+// hold nothing and only join the barriers.
+
+// 1/sqrt(sum(v^2)/K + eps) in the fixed order described above (one barrier).
+template <int CPT>
+__device__ __forceinline__ float row_rms_inv(const float (&v)[CPT][8], int nch, int K, float eps, int tid,
+                                             float* s_sum) {
+  const bool active = tid < kActThreads;
+  const int lane = tid & 63, wv = tid >> 6;
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i)
+    if (active && tid + kActThreads * i < nch) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float sq = v[i][j] * v[i][j];
+        s = s + sq;
+      }
+    }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_xor(s, off, 64);
+  if (active && lane == 0) s_sum[wv] = s;
+  __syncthreads();
+  const float ss = (s_sum[0] + s_sum[1]) + (s_sum[2] + s_sum[3]);
+  const float var = ss / (float)K;
+  return 1.0f / sqrtf(var + eps);
+}
+
+// y = bf16(gamma * bf16(x * r)) (or bf16(x * r) without gamma), in place.
+template <int CPT>
+__device__ __forceinline__ void row_apply_norm(float (&v)[CPT][8], const uint4 (&graw)[CPT], bool has_gamma,
+                                               float r, int nch, int tid) {
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = tid + kActThreads * i;
+    if (tid < kActThreads && c < nch) {
+      const uint32_t g4[4] = {graw[i].x, graw[i].y, graw[i].z, graw[i].w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float t = bf2f(f2bf(v[i][j] * r));
+        if (has_gamma) {
+          const float g = bf2f((uint16_t)((j & 1) ? (g4[j >> 1] >> 16) : (g4[j >> 1] & 0xffffu)));
+          v[i][j] = bf2f(f2bf(g * t));
+        } else {
+          v[i][j] = t;
+        }
+      }
+    }
+  }
+}
+
+// a = max(max|v|, act_eps) over the row (one barrier).
+template <int CPT>
+__device__ __forceinline__ float row_absmax(const float (&v)[CPT][8], int nch, float act_eps, int tid,
+                                            float* s_max) {
+  const bool active = tid < kActThreads;
+  const int lane = tid & 63, wv = tid >> 6;
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i)
+    if (active && tid + kActThreads * i < nch) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[i][j]));
+    }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  if (active && lane == 0) s_max[wv] = amax;
+  __syncthreads();
+  const float a = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+  return a > act_eps ? a : act_eps;
+}
+
+// Eight quantised values packed little-endian into two words; rs += their sum.
+__device__ __forceinline__ void quant8(const float (&v)[8], float scale, uint32_t& lo, uint32_t& hi, int& rs) {
+  lo = 0u;
+  hi = 0u;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float t = rintf(v[j] * scale);
+    t = fminf(fmaxf(t, -128.0f), 127.0f);
+    const int qi = (int)t;
+    rs += qi;
+    const uint32_t b = (uint32_t)(qi & 0xff);
+    if (j < 4)
+      lo |= b << (8 * j);
+    else
+      hi |= b << (8 * (j - 4));
+  }
 }
 
 // Row m of the activation prologue.  Threads 0..255 do the work; any further
@@ -150,55 +245,27 @@ __device__ void act_row(const ActArgs& p, int m, int tid) {
     graw[i] = make_uint4(0u, 0u, 0u, 0u);
     if (NORM && p.gamma && active && c < nch) graw[i] = *reinterpret_cast<const uint4*>(p.gamma + 8 * c);
   }
+  // all loads are issued before the first conversion waits for one
+  uint4 raw[CPT];
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int c = tid + kActThreads * i;
-    if (active && c < nch) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(xr + 8 * c);
-      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+    raw[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (active && c < nch) raw[i] = *reinterpret_cast<const uint4*>(xr + 8 * c);
+  }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[i][2 * j] = bf2f((uint16_t)(w4[j] & 0xffffu));
-        v[i][2 * j + 1] = bf2f((uint16_t)(w4[j] >> 16));
-      }
+  for (int i = 0; i < CPT; ++i) {
+    const uint32_t w4[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[i][2 * j] = bf2f((uint16_t)(w4[j] & 0xffffu));
+      v[i][2 * j + 1] = bf2f((uint16_t)(w4[j] >> 16));
     }
   }
 
   if (NORM) {
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < CPT; ++i)
-      if (active && tid + kActThreads * i < nch) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float sq = v[i][j] * v[i][j];
-          s = s + sq;
-        }
-      }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_xor(s, off, 64);
-    if (active && lane == 0) s_sum[wv] = s;
-    __syncthreads();
-    const float ss = (s_sum[0] + s_sum[1]) + (s_sum[2] + s_sum[3]);
-    const float var = ss / (float)p.K;
-    const float r = 1.0f / sqrtf(var + p.norm_eps);
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + kActThreads * i;
-      if (active && c < nch) {
-        const uint32_t g4[4] = {graw[i].x, graw[i].y, graw[i].z, graw[i].w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float t = bf2f(f2bf(v[i][j] * r));
-          if (p.gamma) {
-            const float g = bf2f((uint16_t)((j & 1) ? (g4[j >> 1] >> 16) : (g4[j >> 1] & 0xffffu)));
-            v[i][j] = bf2f(f2bf(g * t));
-          } else {
-            v[i][j] = t;
-          }
-        }
-      }
-    }
+    const float r = row_rms_inv<CPT>(v, nch, p.K, p.norm_eps, tid, s_sum);
+    row_apply_norm<CPT>(v, graw, p.gamma != nullptr, r, nch, tid);
   }
 
   if (!QUANT || p.y_rm) {
@@ -218,19 +285,7 @@ __device__ void act_row(const ActArgs& p, int m, int tid) {
   }
   if (!QUANT) return;
 
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < CPT; ++i)
-    if (active && tid + kActThreads * i < nch) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[i][j]));
-    }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-  if (active && lane == 0) s_max[wv] = amax;
-  __syncthreads();
-  float a = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
-  a = a > p.act_eps ? a : p.act_eps;
+  const float a = row_absmax<CPT>(v, nch, p.act_eps, tid, s_max);
   const float scale = 127.0f / a;
   if (tid == 0) {
     if (COHERENT)
@@ -245,19 +300,8 @@ __device__ void act_row(const ActArgs& p, int m, int tid) {
   for (int i = 0; i < CPT; ++i) {
     const int c = tid + kActThreads * i;
     if (active && c < nch) {
-      uint32_t lo = 0u, hi = 0u;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float t = rintf(v[i][j] * scale);
-        t = fminf(fmaxf(t, -128.0f), 127.0f);
-        const int qi = (int)t;
-        rs += qi;
-        const uint32_t b = (uint32_t)(qi & 0xff);
-        if (j < 4)
-          lo |= b << (8 * j);
-        else
-          hi |= b << (8 * (j - 4));
-      }
+      uint32_t lo, hi;
+      quant8(v[i], scale, lo, hi, rs);
       store8<COHERENT>(p.xa + xa_offset(m, 8 * c, p.KS), lo, hi);
       if (p.xq_rm) *reinterpret_cast<uint2*>(p.xq_rm + (int64_t)m * p.K + 8 * c) = make_uint2(lo, hi);
     }

@@ -52,9 +52,9 @@ struct GemmPlan {
 };
 GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req);
 
-// Byte offsets inside the fused workspace (the first 256 bytes hold the
-// producer/consumer words of the fused decode kernel; byte 128 is its error
-// word).
+// Byte offsets inside the fused workspace (the first kSyncBytes hold the
+// handshake words of the single-launch decode kernel, its error word among
+// them).
 struct FusedLayout {
   int64_t xa, a_dq, gemm_ws, total;
 };

@@ -32,6 +32,7 @@
 #include <stdlib.h>
 
 #include "btl_act_row.h"
+#include "btl_mfma.h"
 
 namespace btl {
 
@@ -39,9 +40,6 @@ int launch_act(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint1
                int8_t* xa, float* a_dq, int32_t* rowsum, float* act_scale, int8_t* xq_rm, uint16_t* y_rm,
                uint32_t* zero_words, int n_zero_words, hipStream_t stream);
 int check_act_args(const char* who, const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint16_t* gamma);
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
 
 struct GemmArgs {
   const int8_t* xa;
@@ -80,18 +78,6 @@ constexpr int kSyncStride = 32;  // words: 128 bytes
 enum { kReadyFlag = 0, kPassGrp = 32, kPassTop = 40, kErrorWord = 41 };
 __device__ __forceinline__ uint32_t* sync_word(const FusedSync& fs, int w) { return fs.words + w * kSyncStride; }
 
-__device__ __forceinline__ v4i unpack_b(uint32_t d) {
-  const int m = 0x03030303;
-  v4i b;
-  b.x = (int)(d & m);
-  b.y = (int)((d >> 2) & m);
-  b.z = (int)((d >> 4) & m);
-  b.w = (int)((d >> 6) & m);
-  return b;
-}
-
-__device__ __forceinline__ v4i ld128(const void* p) { return *reinterpret_cast<const v4i*>(p); }
-
 // 16-byte load that bypasses the per-XCD L2 (data published in this launch).
 __device__ __forceinline__ v4i ld128_coherent(__amdgpu_buffer_rsrc_t rsrc, int offset) {
   return __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 16 /* sc1 */);
@@ -104,9 +90,6 @@ __device__ __forceinline__ float seg_scale_of(const GemmArgs& p, int n) {
     if (i + 1 < p.nseg && n >= p.seg_end[i]) s = p.seg_scale[i + 1];
   return s;
 }
-
-// Row of element r (0..15) of a lane's 32x32 MFMA accumulator.
-__device__ __forceinline__ int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
 // Epilogue for one accumulator element (acc already row-sum corrected);
 // ad = a_dq of the row.

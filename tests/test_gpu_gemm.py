@@ -199,7 +199,9 @@ def test_fused_decode_handshake_clean(orc):
         exp = ref["out"] if epi == "none" else orc.relu2_mul_bf16(ref["out"][:, : n // 2], ref["out"][:, n // 2:])
         assert np.array_equal(H.bits_of(out), exp)
     err = int(N.lib().btl_fused_error_offset())
-    for ws in N._workspaces.values():
+    for key, ws in N._workspaces.items():
+        if key[0] != "bitlinear":
+            continue  # decode-layer workspaces keep launch counters
         words = ws[:8192].view(torch.int32).cpu().numpy()
         assert words[err // 4] == 0, "a bounded wait ran out"
         assert not words.any(), "handshake counters must be reset after every call"

@@ -206,7 +206,7 @@ def test_c4_graph_replay_matches_eager(orc):
         step.step()
     torch.cuda.current_stream().wait_stream(s)
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):  # the stream whose workspaces the warm-up made
         step.step()
     for rep in range(4):
         step.reset_hidden()
