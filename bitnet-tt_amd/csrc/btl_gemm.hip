@@ -26,9 +26,8 @@
 // issue their weight loads first, then wait for the 32 flags (bounded spin),
 // so weight streaming overlaps the prologue and a launch is saved.
 //
-// Prefill (M > 32): 128x128 output tiles, one 64x64 quadrant per wave, A and
-// B fragments loaded straight into registers (both operands are stored in
-// MFMA order), the next superblock prefetched while the current one runs.
+// Prefill (M > 32): 128x256 output tiles, operands staged through LDS once
+// per superblock and shared by the four waves (64x128 each).
 #include <stdlib.h>
 
 #include "btl_act_row.h"
@@ -92,13 +91,22 @@ __device__ __forceinline__ float seg_scale_of(const GemmArgs& p, int n) {
 }
 
 // Epilogue for one accumulator element (acc already row-sum corrected);
-// ad = a_dq of the row.
-__device__ __forceinline__ void epi_scale(const GemmArgs& p, int i, int n, int32_t acc, float ad) {
+// ad = a_dq of the row, res = the residual element (used when p.residual).
+// Callers load ad and res ahead: a load inside the store loop would cost a
+// memory round trip per element.
+__device__ __forceinline__ void epi_scale(const GemmArgs& p, int i, int n, int32_t acc, float ad, uint16_t res) {
   if (p.acc_out) p.acc_out[(int64_t)i * p.N + n] = acc;
   const float f = seg_scale_of(p, n) * ad;
   uint16_t o = f2bf((float)acc * f);
-  if (p.residual) o = f2bf(bf2f(p.residual[(int64_t)i * p.n_out + n]) + bf2f(o));
+  if (p.residual) o = f2bf(bf2f(res) + bf2f(o));
   p.out[(int64_t)i * p.n_out + n] = o;
+}
+// Residual element (i, n) with the row clamped into range (for loads issued
+// before the row check).
+__device__ __forceinline__ uint16_t residual_at(const GemmArgs& p, int i, int n) {
+  if (!p.residual) return 0;
+  const int ic = i < p.M ? i : p.M - 1;
+  return p.residual[(int64_t)ic * p.n_out + n];
 }
 __device__ __forceinline__ void epi_relu2(const GemmArgs& p, int i, int ng, int nu, int32_t ag, int32_t au,
                                           float ad) {
@@ -160,6 +168,13 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
   if (FUSED)
     for (int i = 0; i < fs.pre_sleep; ++i) __builtin_amdgcn_s_sleep(8);
   if (wb < we) load_b(wb, (we - wb) < NSB ? (we - wb) : NSB);
+  // The residual is an input of the launch: fetch it now, behind the weights.
+  uint16_t res_pre[TPW][RR];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int rr = 0; rr < RR; ++rr)
+      res_pre[t][rr] = EPI == EPI_SCALE ? residual_at(p, acc_row(wv + WAVES * rr, lane), tile[t] * 32 + (lane & 31)) : 0;
   // pass accounting of the fused handshake: issued after the wait, settled
   // when the block exits (its latency hides behind the GEMM).
   uint32_t pass_prev = 0;
@@ -293,16 +308,19 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
   }
 
   const int j = lane & 31;
+  float ad_row[RR];
+#pragma unroll
+  for (int rr = 0; rr < RR; ++rr) ad_row[rr] = FUSED ? ad_pre[rr] : p.a_dq[acc_row(wv + WAVES * rr, lane)];
 #pragma unroll
   for (int rr = 0; rr < RR; ++rr) {
     const int i = acc_row(wv + WAVES * rr, lane);
     if (i >= p.M) continue;
-    const float ad = FUSED ? ad_pre[rr] : p.a_dq[i];
+    const float ad = ad_row[rr];
     if (EPI == EPI_RELU2) {
       epi_relu2(p, i, tile[0] * 32 + j, tile[1] * 32 + j, v[0][rr], v[1][rr], ad);
     } else {
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) epi_scale(p, i, tile[t] * 32 + j, v[t][rr], ad);
+      for (int t = 0; t < TPW; ++t) epi_scale(p, i, tile[t] * 32 + j, v[t][rr], ad, res_pre[t][rr]);
     }
   }
   settle_pass();
@@ -329,107 +347,262 @@ __global__ __launch_bounds__(512) void k_bitlinear_decode(GemmArgs p, ActArgs a,
 }
 
 // ------------------------------------------------------------ prefill ----
-// Workgroup tile: 4 row blocks x 4 column tiles (scale) or 2 gate tiles plus
-// their 2 up tiles (relu2).  Wave (wm, wn) = (wv & 1, wv >> 1) owns row
-// blocks 2*wm, 2*wm+1 and column slots 2*wn, 2*wn+1 (relu2: slot 0 = gate,
-// slot 1 = matching up tile).
+// Workgroup tile: 4 row blocks (128 rows) x 8 column tiles (256 columns); for
+// relu2 the 8 slots are 4 gate tiles and their 4 up tiles, so the workgroup
+// finishes 128 columns of relu(g)^2*u.  Each superblock (128 of K) of the
+// activation tile (16 KiB: 4 row blocks x 4 k-steps) and of the packed
+// weights (8 KiB: 8 tiles) is staged in LDS as 24 chunks of 1 KiB, six per
+// wave, each one global_load_lds_dwordx4 (lane i's 16 bytes land at chunk +
+// 16i), so staging costs no registers.  kPfStages superblocks are in flight:
+// a stage is waited for (vmcnt of the wave's own loads, then a barrier), its
+// MFMAs run, and after a second barrier the freed buffer is refilled with the
+// superblock kPfStages ahead.  Wave (wm, wn) = (wv & 1, wv >> 1) computes row
+// blocks 2wm, 2wm+1 against four slots: 4wn..4wn+3 (scale) or gate slots 2wn,
+// 2wn+1 with up slots 4+2wn, 5+2wn (relu2).
+//
+// Tile order is XCD-aware: workgroup b runs on XCD b % 8, so tiles are
+// numbered in groups of kPfGroupRows row tiles (column tiles inner) and XCD x
+// takes the contiguous range [x*per, (x+1)*per) of that order -- a compact
+// block of about kPfGroupRows row tiles x per/kPfGroupRows column tiles whose
+// operands (a few MB) stay in that XCD's L2.
+constexpr int kPfXcds = 8;
+constexpr int kPfGroupRows = 4;
+constexpr int kPfRB = 4;                              // row blocks of 32 per workgroup
+constexpr int kPfCT = 8;                              // column tiles of 32 per workgroup
+constexpr int kPfChunks = kPfRB * 4 + kPfCT;          // 1 KiB chunks per stage
+constexpr int kPfChunksPerWave = kPfChunks / 4;
+constexpr int kPfStages = 3;
+
 template <int EPI>
-__global__ __launch_bounds__(256) void k_gemm_prefill(GemmArgs p) {
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int wm = wv & 1, wn = wv >> 1;
-  const int gm = blockIdx.y, gn = blockIdx.x;
-  int mblk[2];
-  bool mok[2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    mblk[u] = gm * 4 + 2 * wm + u;
-    mok[u] = mblk[u] < p.Mb;
-    if (!mok[u]) mblk[u] = p.Mb - 1;
-  }
-  int tile[2];
-  bool tok[2];
+__device__ __forceinline__ int pf_tile(const GemmArgs& p, int gn, int slot) {
   if (EPI == EPI_RELU2) {
     const int half = p.NT >> 1;
-    int gt = gn * 2 + wn;
-    tok[0] = tok[1] = gt < half;
-    if (gt >= half) gt = half - 1;
-    tile[0] = gt;
-    tile[1] = gt + half;
-  } else {
+    const int g = gn * 4 + (slot & 3);
+    return (slot < 4 ? 0 : half) + (g < half ? g : half - 1);
+  }
+  const int t = gn * kPfCT + slot;
+  return t < p.NT ? t : p.NT - 1;
+}
+
+// s_waitcnt with only the vector-memory count constrained (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+#define BTL_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+// Workgroup barrier without the memory fence of __syncthreads (whose release
+// part would wait for every load in flight, the LDS-direct ones included);
+// the compiler fences keep LDS accesses on their side of it.
+__device__ __forceinline__ void barrier_only() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, int ngn) {
+  // One LDS object: the stage buffers, then a_dq and the row sums of the
+  // tile's rows.
+  __shared__ __attribute__((aligned(16))) int8_t lds[kPfStages * kPfChunks * 1024 + kPfRB * 32 * 8];
+  int8_t (*stage)[kPfChunks * 1024] = reinterpret_cast<int8_t (*)[kPfChunks * 1024]>(lds);
+  float* s_adq = reinterpret_cast<float*>(lds + kPfStages * kPfChunks * 1024);
+  int32_t* s_rs = reinterpret_cast<int32_t*>(lds + kPfStages * kPfChunks * 1024 + kPfRB * 32 * 4);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wm = wv & 1, wn = wv >> 1;
+  const int ntiles = ngm * ngn;
+  const int per = (ntiles + kPfXcds - 1) / kPfXcds;
+  const int t = (int)(blockIdx.x % kPfXcds) * per + (int)(blockIdx.x / kPfXcds);
+  if (t >= ntiles) return;
+  const int grp = t / (kPfGroupRows * ngn);            // group of kPfGroupRows row tiles
+  const int rows_in = min(kPfGroupRows, ngm - grp * kPfGroupRows);
+  const int r = t - grp * kPfGroupRows * ngn;
+  const int gm = grp * kPfGroupRows + r % rows_in;
+  const int gn = r / rows_in;
+  const int KS = p.KS;
+
+  // Global source of this wave's chunks at superblock 0; a superblock
+  // advances activation chunks by 4 KiB and weight chunks by 1 KiB.
+  const int8_t* src[kPfChunksPerWave];
+  int step[kPfChunksPerWave];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      tile[u] = gn * 4 + 2 * wn + u;
-      tok[u] = tile[u] < p.NT;
-      if (!tok[u]) tile[u] = p.NT - 1;
+  for (int i = 0; i < kPfChunksPerWave; ++i) {
+    const int c = wv * kPfChunksPerWave + i;
+    if (c < kPfRB * 4) {
+      int mb = gm * kPfRB + (c >> 2);
+      mb = mb < p.Mb ? mb : p.Mb - 1;
+      src[i] = p.xa + ((((int64_t)mb * KS) * 4 + (c & 3)) * 64 + lane) * 16;
+      step[i] = 4096;
+    } else {
+      const int tile = pf_tile<EPI>(p, gn, c - kPfRB * 4);
+      src[i] = reinterpret_cast<const int8_t*>(p.wdev) + (((int64_t)tile * KS) * 64 + lane) * 16;
+      step[i] = 1024;
     }
   }
+  auto issue = [&](int ks) {
+    int8_t* dst = &stage[ks % kPfStages][wv * kPfChunksPerWave * 1024];
+#pragma unroll
+    for (int i = 0; i < kPfChunksPerWave; ++i)
+      __builtin_amdgcn_global_load_lds(src[i] + (int64_t)ks * step[i], dst + i * 1024, 16, 0, 0);
+  };
 
-  v16i acc[2][2];
+  int slot[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) slot[u] = (EPI == EPI_RELU2) ? ((u < 2 ? 0 : 4) + 2 * wn + (u & 1)) : (4 * wn + u);
+
+  v16i acc[2][4];
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
-    for (int y = 0; y < 2; ++y) acc[x][y] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    for (int u = 0; u < 4; ++u) acc[x][u] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  // Row sums: wave (wm, wn) sums the bytes of its row block 2wm + wn only
+  // (the other wave of the pair takes the other block).
+  int32_t rs_lane = 0;
 
-  const int KS = p.KS;
-  int32_t rs_lane[2] = {0, 0};  // A-operand byte sums of the two row blocks
-  v4i a[2][4], b[2], an[2][4], bn[2];
+  const float adq_mine = p.a_dq[min(gm * kPfRB * 32 + (tid & (kPfRB * 32 - 1)), p.Mb * 32 - 1)];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    b[u] = ld128(p.wdev + (((int64_t)tile[u] * KS) * 64 + lane) * 4);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) a[u][q] = ld128(p.xa + ((((int64_t)mblk[u] * KS) * 4 + q) * 64 + lane) * 16);
-  }
+  for (int k = 0; k < kPfStages; ++k)
+    if (k < KS) issue(k);
   for (int ks = 0; ks < KS; ++ks) {
-    const int kn = (ks + 1 < KS) ? ks + 1 : ks;
+    // this wave's loads of superblock ks are done once at most the loads of
+    // the (up to kPfStages - 1) later superblocks are outstanding
+    const int later = KS - 1 - ks;
+    if (later >= 2)
+      BTL_WAIT_VMCNT(2 * kPfChunksPerWave);
+    else if (later == 1)
+      BTL_WAIT_VMCNT(kPfChunksPerWave);
+    else
+      BTL_WAIT_VMCNT(0);
+    barrier_only();
+    const int8_t* buf = stage[ks % kPfStages];
+    v4i bw[4];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      bn[u] = ld128(p.wdev + (((int64_t)tile[u] * KS + kn) * 64 + lane) * 4);
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        an[u][q] = ld128(p.xa + ((((int64_t)mblk[u] * KS + kn) * 4 + q) * 64 + lane) * 16);
-    }
+    for (int u = 0; u < 4; ++u) bw[u] = *reinterpret_cast<const v4i*>(buf + (kPfRB * 4 + slot[u]) * 1024 + lane * 16);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const v4i b0 = unpack_b((uint32_t)b[0][q]);
-      const v4i b1 = unpack_b((uint32_t)b[1][q]);
+      v4i a[2];
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        acc[x][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[x][q], b0, acc[x][0], 0, 0, 0);
-        acc[x][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[x][q], b1, acc[x][1], 0, 0, 0);
-        rs_lane[x] = __builtin_amdgcn_sdot4(a[x][q].x, 0x01010101, rs_lane[x], false);
-        rs_lane[x] = __builtin_amdgcn_sdot4(a[x][q].y, 0x01010101, rs_lane[x], false);
-        rs_lane[x] = __builtin_amdgcn_sdot4(a[x][q].z, 0x01010101, rs_lane[x], false);
-        rs_lane[x] = __builtin_amdgcn_sdot4(a[x][q].w, 0x01010101, rs_lane[x], false);
+      for (int x = 0; x < 2; ++x) a[x] = *reinterpret_cast<const v4i*>(buf + ((2 * wm + x) * 4 + q) * 1024 + lane * 16);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const v4i b = unpack_b((uint32_t)bw[u][q]);
+#pragma unroll
+        for (int x = 0; x < 2; ++x) acc[x][u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[x], b, acc[x][u], 0, 0, 0);
       }
+      rs_lane = bytes_sum(wn == 0 ? a[0] : a[1], rs_lane);
     }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      b[u] = bn[u];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) a[u][q] = an[u][q];
-    }
+    barrier_only();  // every wave's reads of this buffer are done (their values fed the MFMAs)
+    if (ks + kPfStages < KS) issue(ks + kPfStages);
   }
 
+  // Epilogue in two passes through LDS (the stage buffers are free now):
+  // each wave writes its scaled bf16 values (relu^2*u for relu2) into the
+  // workgroup's output tile, then all threads write whole rows with 16-byte
+  // stores, adding the residual read the same way.
+  {
+    const int32_t rs_row = rs_lane + __shfl_xor(rs_lane, 32, 64);  // lanes l, l+32: halves of row l & 31
+    if (lane < 32) s_rs[(2 * wm + wn) * 32 + lane] = rs_row;
+    if (tid < kPfRB * 32) s_adq[tid] = adq_mine;  // loaded at the start; stored now, after the stage loads
+  }
+  __syncthreads();  // s_rs, s_adq visible; every wave is done with the stage buffers
+  int8_t* tile_lds = &stage[0][0];
+  constexpr int kOutCols = (EPI == EPI_RELU2) ? kPfCT * 16 : kPfCT * 32;  // output columns of the tile
+  constexpr int kPitch = kOutCols * 2 + 16;  // bytes per row; halves of a wave land 16 banks apart
+  static_assert(kPfRB * 32 * kPitch <= kPfStages * kPfChunks * 1024, "output tile fits in the stage buffers");
   const int j = lane & 31;
+  // weight scale per slot: segment ends are multiples of 32, so one per tile
+  float sw[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    if (EPI == EPI_RELU2) {
+      const int half = p.NT >> 1;
+      const int g = min(gn * 4 + 2 * wn + (u & 1), half - 1);
+      sw[u] = seg_scale_of(p, (u < 2 ? g : g + half) * 32);
+    } else {
+      sw[u] = seg_scale_of(p, min(gn * kPfCT + slot[u], p.NT - 1) * 32);
+    }
+  }
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
-    // lanes l and l+32 hold the two halves of row l & 31
-    const int32_t rs_row = rs_lane[x] + __shfl_xor(rs_lane[x], 32, 64);
-    if (!mok[x]) continue;
+    float ad[16];
+    int32_t rsr[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int32_t rs = __shfl(rs_row, acc_row(r, lane), 64);
-      const int i = mblk[x] * 32 + acc_row(r, lane);
-      if (i >= p.M) continue;
-      const float ad = p.a_dq[i];
-      if (EPI == EPI_RELU2) {
-        if (tok[0]) epi_relu2(p, i, tile[0] * 32 + j, tile[1] * 32 + j, acc[x][0][r] - rs, acc[x][1][r] - rs, ad);
-      } else {
+      ad[r] = s_adq[(2 * wm + x) * 32 + acc_row(r, lane)];
+      rsr[r] = s_rs[(2 * wm + x) * 32 + acc_row(r, lane)];
+    }
+    if (p.acc_out) {  // exact accumulators (debug output)
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-          if (tok[u]) epi_scale(p, i, tile[u] * 32 + j, acc[x][u][r] - rs, ad);
+      for (int r = 0; r < 16; ++r) {
+        const int i = gm * kPfRB * 32 + (2 * wm + x) * 32 + acc_row(r, lane);
+        if (i >= p.M) continue;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          int t;
+          if (EPI == EPI_RELU2) {
+            const int g = gn * 4 + 2 * wn + (u & 1);
+            t = g < (p.NT >> 1) ? (u < 2 ? g : g + (p.NT >> 1)) : -1;
+          } else {
+            t = gn * kPfCT + slot[u] < p.NT ? gn * kPfCT + slot[u] : -1;
+          }
+          if (t >= 0) p.acc_out[(int64_t)i * p.N + t * 32 + j] = acc[x][u][r] - rsr[r];
+        }
       }
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int32_t rs = rsr[r];
+      const int il = (2 * wm + x) * 32 + acc_row(r, lane);  // row within the tile
+      if (EPI == EPI_RELU2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int32_t ag = acc[x][u][r] - rs, au = acc[x][u + 2][r] - rs;
+          const float gg = bf2f(f2bf((float)ag * (sw[u] * ad[r])));
+          const float uu = bf2f(f2bf((float)au * (sw[u + 2] * ad[r])));
+          const float gr = gg > 0.0f ? gg : 0.0f;
+          *reinterpret_cast<uint16_t*>(tile_lds + il * kPitch + ((2 * wn + u) * 32 + j) * 2) = f2bf(bf2f(f2bf(gr * gr)) * uu);
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int32_t v = acc[x][u][r] - rs;
+          *reinterpret_cast<uint16_t*>(tile_lds + il * kPitch + (slot[u] * 32 + j) * 2) = f2bf((float)v * (sw[u] * ad[r]));
+        }
+      }
+    }
+  }
+  barrier_only();
+  constexpr int kChunksPerRow = kOutCols / 8;
+  constexpr int kPerThread = kPfRB * 32 * kChunksPerRow / 256;
+  const int col_base = gn * kOutCols;
+  const int n_cols = (EPI == EPI_RELU2) ? (p.NT >> 1) * 32 : p.NT * 32;  // == p.n_out
+  uint4 res[kPerThread];
+#pragma unroll
+  for (int k = 0; k < kPerThread; ++k) {
+    const int c = tid + 256 * k;
+    const int i = gm * kPfRB * 32 + c / kChunksPerRow;
+    const int col = col_base + (c % kChunksPerRow) * 8;
+    res[k] = make_uint4(0u, 0u, 0u, 0u);
+    if (EPI == EPI_SCALE && p.residual && i < p.M && col < n_cols)
+      res[k] = *reinterpret_cast<const uint4*>(p.residual + (int64_t)i * p.n_out + col);
+  }
+#pragma unroll
+  for (int k = 0; k < kPerThread; ++k) {
+    const int c = tid + 256 * k;
+    const int il = c / kChunksPerRow;
+    const int i = gm * kPfRB * 32 + il;
+    const int col = col_base + (c % kChunksPerRow) * 8;
+    if (i >= p.M || col >= n_cols) continue;
+    uint4 o = *reinterpret_cast<const uint4*>(tile_lds + il * kPitch + (c % kChunksPerRow) * 16);
+    if (EPI == EPI_SCALE && p.residual) {
+      uint32_t ow[4] = {o.x, o.y, o.z, o.w};
+      const uint32_t rw[4] = {res[k].x, res[k].y, res[k].z, res[k].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = f2bf(bf2f((uint16_t)(rw[e] & 0xffffu)) + bf2f((uint16_t)(ow[e] & 0xffffu)));
+        const uint32_t hi = f2bf(bf2f((uint16_t)(rw[e] >> 16)) + bf2f((uint16_t)(ow[e] >> 16)));
+        ow[e] = lo | (hi << 16);
+      }
+      o = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    }
+    *reinterpret_cast<uint4*>(p.out + (int64_t)i * p.n_out + col) = o;
   }
 }
 
@@ -613,6 +786,8 @@ static int check_gemm_args(const char* who, int64_t M, int64_t K, int64_t N, con
   if (!aligned(wdev, 16)) return set_error(BTL_ERR_ALIGN, "%s: wdev must be 16-byte aligned", who);
   if (!aligned(out, 4) || (residual && !aligned(residual, 4)))
     return set_error(BTL_ERR_ALIGN, "%s: out/residual must be 4-byte aligned", who);
+  if (M > 32 && (!aligned(out, 16) || (residual && !aligned(residual, 16))))
+    return set_error(BTL_ERR_ALIGN, "%s: out/residual must be 16-byte aligned for M > 32", who);
   return BTL_OK;
 }
 
@@ -650,12 +825,14 @@ static GemmArgs gemm_args(const int8_t* xa, const float* a_dq, int64_t M, int64_
 
 static int launch_gemm(const GemmArgs& a, int epilogue, const GemmPlan& pl, hipStream_t s) {
   if (pl.prefill) {
-    const int ngn = (epilogue == BTL_EPI_RELU2_MUL) ? (int)((a.NT / 2 + 1) / 2) : (a.NT + 3) / 4;
-    dim3 grid((unsigned)ngn, (unsigned)((a.Mb + 3) / 4));
+    const int ngn = (epilogue == BTL_EPI_RELU2_MUL) ? (a.NT / 2 + 3) / 4 : (a.NT + kPfCT - 1) / kPfCT;
+    const int ngm = (a.Mb + kPfRB - 1) / kPfRB;
+    const int per = (ngm * ngn + kPfXcds - 1) / kPfXcds;
+    dim3 grid((unsigned)(per * kPfXcds));
     if (epilogue == BTL_EPI_RELU2_MUL)
-      hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2>), grid, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2>), grid, dim3(256), 0, s, a, ngm, ngn);
     else
-      hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE>), grid, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE>), grid, dim3(256), 0, s, a, ngm, ngn);
     return check_launch("ternary gemm (prefill)");
   }
   const int nsb = decode_nsb(pl, a.KS, epilogue);

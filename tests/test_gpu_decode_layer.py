@@ -98,17 +98,17 @@ def test_repeated_launches_and_graph_replays():
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         step.reset_hidden()
-        step.step()
+        step.step_layers()
         torch.cuda.synchronize()
         first = H.bits_of(step.hidden)
         for _ in range(11):
             step.reset_hidden()
-            step.step()
+            step.step_layers()
         torch.cuda.synchronize()
         assert np.array_equal(H.bits_of(step.hidden), first)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
-        step.step()
+        step.step_layers()
     for rep in range(4):
         with torch.cuda.stream(s):
             step.reset_hidden()

@@ -140,6 +140,19 @@ def test_prefill_gemm_bit_exact(orc, m, k, n):
     assert np.array_equal(out, expected_out(orc, ref, a_dq, [0.02], [n], 0))
 
 
+@pytest.mark.parametrize("m,k,f", [(70, 384, 96), (512, 256, 160), (129, 640, 32)])
+def test_prefill_relu2_bit_exact(orc, m, k, f):
+    """relu2 prefill with F not a multiple of the 4 gate tiles of a workgroup."""
+    print(f"prefill relu2 m={m} k={k} f={f}", flush=True)
+    rng = np.random.default_rng(m * 7 + f)
+    q = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
+    w = H.ternary(k, 2 * f, seed=f + 1)
+    scales, ends = [0.021, 0.017], [f, 2 * f]
+    acc, out, a_dq, _ = run_gemm(orc, q, w, scales, ends, epi=1)
+    assert np.array_equal(acc, orc.gemm_i8t(q, w))
+    assert np.array_equal(out, expected_out(orc, acc, a_dq, scales, ends, 1))
+
+
 @pytest.mark.parametrize("m,k,n,epi", [(512, 2560, 3840, 0), (512, 2560, 13824, 1), (2048, 2560, 6912, 0),
                                        (2048, 6912, 2560, 0), (512, 2560, 2560, 0)])
 def test_prefill_full_size_properties(orc, m, k, n, epi):
