@@ -106,6 +106,62 @@ __device__ __forceinline__ void store8(int8_t* p, uint32_t lo, uint32_t hi) {
     *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
 }
 
+// ---- cross-lane partners of the xor butterfly ------------------------------
+// xor_partner<d>(v) is v of lane (lane ^ d), for d = 32, 16, 8, 4, 2, 1: the
+// swaps of v_permlane32/16_swap for 32 and 16, DPP row/quad permutations for
+// the rest (xor 8 = half-row mirror of the row mirror, xor 4 = quad reverse of
+// the half-row mirror).  No LDS round trip, so a 64-lane butterfly costs a few
+// ALU cycles per step instead of an LDS latency.
+template <int C>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, C, 0xF, 0xF, false);
+}
+template <int D>
+__device__ __forceinline__ uint32_t xor_partner_u(uint32_t x) {
+  static_assert(D == 32 || D == 16 || D == 8 || D == 4 || D == 2 || D == 1, "butterfly distance");
+  const int lane = __lane_id();
+  if (D == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return lane < 32 ? r[1] : r[0];
+  } else if (D == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  } else if (D == 8) {
+    return dpp_mov<0x141>(dpp_mov<0x140>(x));  // row_half_mirror(row_mirror)
+  } else if (D == 4) {
+    return dpp_mov<0x1B>(dpp_mov<0x141>(x));  // quad_perm(3,2,1,0)(row_half_mirror)
+  } else if (D == 2) {
+    return dpp_mov<0x4E>(x);  // quad_perm(2,3,0,1)
+  } else {
+    return dpp_mov<0xB1>(x);  // quad_perm(1,0,3,2)
+  }
+}
+template <int D>
+__device__ __forceinline__ float xor_partner(float v) {
+  return __uint_as_float(xor_partner_u<D>(__float_as_uint(v)));
+}
+
+// Butterfly over the 64 lanes, partners at distance 32, 16, 8, 4, 2, 1 in this
+// order (every lane ends with the same value).
+__device__ __forceinline__ float wave_xor_sum(float s) {
+  s = s + xor_partner<32>(s);
+  s = s + xor_partner<16>(s);
+  s = s + xor_partner<8>(s);
+  s = s + xor_partner<4>(s);
+  s = s + xor_partner<2>(s);
+  s = s + xor_partner<1>(s);
+  return s;
+}
+__device__ __forceinline__ float wave_xor_max(float m) {
+  m = fmaxf(m, xor_partner<32>(m));
+  m = fmaxf(m, xor_partner<16>(m));
+  m = fmaxf(m, xor_partner<8>(m));
+  m = fmaxf(m, xor_partner<4>(m));
+  m = fmaxf(m, xor_partner<2>(m));
+  m = fmaxf(m, xor_partner<1>(m));
+  return m;
+}
+
 // ---- pieces of the row prologue shared by every kernel that runs it -------
 // A row lives in registers as v[i][0..7] = elements 8c..8c+7 of chunk
 // c = tid + 256*i; only chunks c < nch hold data.  Threads >= 256 of a block
@@ -127,8 +183,7 @@ __device__ __forceinline__ float row_rms_inv(const float (&v)[CPT][8], int nch, 
         s = s + sq;
       }
     }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_xor(s, off, 64);
+  s = wave_xor_sum(s);
   if (active && lane == 0) s_sum[wv] = s;
   __syncthreads();
   const float ss = (s_sum[0] + s_sum[1]) + (s_sum[2] + s_sum[3]);
@@ -172,8 +227,7 @@ __device__ __forceinline__ float row_absmax(const float (&v)[CPT][8], int nch, f
 #pragma unroll
       for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[i][j]));
     }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  amax = wave_xor_max(amax);
   if (active && lane == 0) s_max[wv] = amax;
   __syncthreads();
   const float a = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));

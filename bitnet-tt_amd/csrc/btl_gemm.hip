@@ -77,11 +77,6 @@ constexpr int kSyncStride = 32;  // words: 128 bytes
 enum { kReadyFlag = 0, kPassGrp = 32, kPassTop = 40, kErrorWord = 41 };
 __device__ __forceinline__ uint32_t* sync_word(const FusedSync& fs, int w) { return fs.words + w * kSyncStride; }
 
-// 16-byte load that bypasses the per-XCD L2 (data published in this launch).
-__device__ __forceinline__ v4i ld128_coherent(__amdgpu_buffer_rsrc_t rsrc, int offset) {
-  return __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 16 /* sc1 */);
-}
-
 __device__ __forceinline__ float seg_scale_of(const GemmArgs& p, int n) {
   float s = p.seg_scale[0];
 #pragma unroll
@@ -144,10 +139,13 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
 
   const int sb0 = (s * p.KS) / p.splitk, sb1 = ((s + 1) * p.KS) / p.splitk;
   const int nsb = sb1 - sb0;
-  const int wb = sb0 + (wv * nsb) / WAVES, we = sb0 + ((wv + 1) * nsb) / WAVES;
+  // In the fused kernel the last wave only polls the ready flags: with no
+  // weight loads of its own in flight, a poll returns as soon as the flag
+  // lands (loads complete in issue order).  The other waves share K.
+  constexpr int KW = FUSED ? WAVES - 1 : WAVES;
+  const int wb = wv < KW ? sb0 + (wv * nsb) / KW : sb1;
+  const int we = wv < KW ? sb0 + ((wv + 1) * nsb) / KW : sb1;
 
-  __amdgpu_buffer_rsrc_t xa_rsrc;
-  if (FUSED) xa_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)p.xa, 0, p.xa_bytes, 0x00020000);
 
   v16i acc[TPW];
 #pragma unroll
@@ -192,7 +190,7 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
   float ad_pre[RR];
   if (FUSED) {
     // Every thread of the workgroup reaches this barrier, with or without work.
-    if (wv == 0) {
+    if (wv == WAVES - 1) {
       unsigned n = 0;
       for (;;) {
         const bool mine = lane >= fs.nact || ld_coherent(sync_word(fs, kReadyFlag + lane)) != 0u;
@@ -222,7 +220,11 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int off = ((sb * 4 + q) * 64 + lane) * 16;
-        a[i][q] = FUSED ? ld128_coherent(xa_rsrc, off) : ld128(p.xa + off);
+        // plain loads in both kernels: the tile is written once per launch
+        // (by this launch's activation blocks, before their ready flags) and
+        // caches start clean at every kernel boundary, so each XCD's L2
+        // fetches it once for all of its CUs
+        a[i][q] = ld128(p.xa + off);
       }
     }
 #pragma unroll
@@ -245,7 +247,7 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
   }
   __shared__ int32_t red_rs[WAVES][32];
   {
-    const int32_t rs_row = rs_lane + __shfl_xor(rs_lane, 32, 64);
+    const int32_t rs_row = rs_lane + (int32_t)xor_partner_u<32>((uint32_t)rs_lane);
     if (lane < 32) red_rs[wv][lane] = rs_row;
   }
 
@@ -497,7 +499,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   // workgroup's output tile, then all threads write whole rows with 16-byte
   // stores, adding the residual read the same way.
   {
-    const int32_t rs_row = rs_lane + __shfl_xor(rs_lane, 32, 64);  // lanes l, l+32: halves of row l & 31
+    const int32_t rs_row = rs_lane + (int32_t)xor_partner_u<32>((uint32_t)rs_lane);  // lanes l, l+32: halves of row l & 31
     if (lane < 32) s_rs[(2 * wm + wn) * 32 + lane] = rs_row;
     if (tid < kPfRB * 32) s_adq[tid] = adq_mine;  // loaded at the start; stored now, after the stage loads
   }
@@ -750,7 +752,8 @@ static void launch_fused_nsb(int nsb, dim3 grid, hipStream_t s, const GemmArgs& 
 // such slices run as passes of 6.
 static int decode_nsb(const GemmPlan& pl, int64_t KS, int epilogue) {
   const int per_wg = (int)((KS + pl.splitk - 1) / pl.splitk);
-  const int per_wave = (per_wg + pl.waves - 1) / pl.waves;
+  const int work_waves = pl.fused ? pl.waves - 1 : pl.waves;  // the fused kernel's last wave polls
+  const int per_wave = (per_wg + work_waves - 1) / work_waves;
   int nsb = nsb_bucket(per_wave);
   if (pl.waves == 8 && (pl.tpw == 2 || epilogue == BTL_EPI_RELU2_MUL) && nsb > 6) nsb = 6;
   return nsb;

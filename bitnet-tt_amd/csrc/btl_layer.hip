@@ -201,7 +201,7 @@ __device__ void layer_gemm(const LayerArgs& p, const LayerOp& op, const v4i (&w)
     }
   }
   {
-    const int32_t rs_row = rs_lane + __shfl_xor(rs_lane, 32, 64);
+    const int32_t rs_row = rs_lane + (int32_t)xor_partner_u<32>((uint32_t)rs_lane);
     if (lane < 32) red_rs[wv][lane] = rs_row;
   }
 #pragma unroll
