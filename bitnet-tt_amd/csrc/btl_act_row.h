@@ -98,14 +98,6 @@ __device__ __forceinline__ int64_t xa_offset(int m, int k0, int KS) {
   return ((((int64_t)mb * KS + ks) * 4 + qs) * 64 + (h * 32 + mr)) * 16 + p0;
 }
 
-template <bool COHERENT>
-__device__ __forceinline__ void store8(int8_t* p, uint32_t lo, uint32_t hi) {
-  if (COHERENT)
-    st_coherent(reinterpret_cast<uint64_t*>(p), (uint64_t)lo | ((uint64_t)hi << 32));
-  else
-    *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
-}
-
 // ---- cross-lane partners of the xor butterfly ------------------------------
 // xor_partner<d>(v) is v of lane (lane ^ d), for d = 32, 16, 8, 4, 2, 1: the
 // swaps of v_permlane32/16_swap for 32 and 16, DPP row/quad permutations for
@@ -160,6 +152,38 @@ __device__ __forceinline__ float wave_xor_max(float m) {
   m = fmaxf(m, xor_partner<2>(m));
   m = fmaxf(m, xor_partner<1>(m));
   return m;
+}
+
+template <bool COHERENT>
+__device__ __forceinline__ void store8(int8_t* p, uint32_t lo, uint32_t hi) {
+  if (COHERENT)
+    st_coherent(reinterpret_cast<uint64_t*>(p), (uint64_t)lo | ((uint64_t)hi << 32));
+  else
+    *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
+}
+
+// 16-byte device-coherent store (write-through to the memory side, like the
+// agent-scope atomic stores above; there is no 128-bit atomic store type).
+// Completion is covered by wait_memory().
+__device__ __forceinline__ void store16_coherent(void* p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  const u4 v = {a, b, c, d};
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+
+// Stores the quantised chunk c (8 bytes lo|hi) of row m.  Chunks c and c^1
+// (lanes t and t^1 of the same wave, both active) fill one 16-byte slot of the
+// operand layout: with COHERENT the even lane takes its neighbour's 8 bytes
+// and writes the slot with one 16-byte coherent store.
+template <bool COHERENT>
+__device__ __forceinline__ void store_chunk(int8_t* xa, int m, int c, int KS, uint32_t lo, uint32_t hi) {
+  if (COHERENT) {
+    const uint32_t lo_n = dpp_mov<0xB1>(lo);  // lane ^ 1
+    const uint32_t hi_n = dpp_mov<0xB1>(hi);
+    if ((c & 1) == 0) store16_coherent(xa + xa_offset(m, 8 * c, KS), lo, hi, lo_n, hi_n);
+  } else {
+    store8<false>(xa + xa_offset(m, 8 * c, KS), lo, hi);
+  }
 }
 
 // ---- pieces of the row prologue shared by every kernel that runs it -------
@@ -356,7 +380,7 @@ __device__ void act_row(const ActArgs& p, int m, int tid) {
     if (active && c < nch) {
       uint32_t lo, hi;
       quant8(v[i], scale, lo, hi, rs);
-      store8<COHERENT>(p.xa + xa_offset(m, 8 * c, p.KS), lo, hi);
+      store_chunk<COHERENT>(p.xa, m, c, p.KS, lo, hi);
       if (p.xq_rm) *reinterpret_cast<uint2*>(p.xq_rm + (int64_t)m * p.K + 8 * c) = make_uint2(lo, hi);
     }
   }

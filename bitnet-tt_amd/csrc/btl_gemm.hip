@@ -369,11 +369,10 @@ __global__ __launch_bounds__(512) void k_bitlinear_decode(GemmArgs p, ActArgs a,
 // operands (a few MB) stay in that XCD's L2.
 constexpr int kPfXcds = 8;
 constexpr int kPfGroupRows = 4;
-constexpr int kPfRB = 4;                              // row blocks of 32 per workgroup
-constexpr int kPfCT = 8;                              // column tiles of 32 per workgroup
-constexpr int kPfChunks = kPfRB * 4 + kPfCT;          // 1 KiB chunks per stage
-constexpr int kPfChunksPerWave = kPfChunks / 4;
+constexpr int kPfCT = 8;      // column tiles of 32 per workgroup
 constexpr int kPfStages = 3;
+// Row blocks of 32 per workgroup: 4 (128 rows), or 2 (64 rows, each wave one
+// row block) when 128-row tiles would leave CUs idle.
 
 template <int EPI>
 __device__ __forceinline__ int pf_tile(const GemmArgs& p, int gn, int slot) {
@@ -399,8 +398,31 @@ __device__ __forceinline__ void barrier_only() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-template <int EPI>
+template <int RB>
+struct PfShape {
+  static_assert(RB == 2 || RB == 4, "64- or 128-row tiles");
+  static constexpr int rb = RB;                  // row blocks of 32 per workgroup
+  static constexpr int xr = RB / 2;              // row blocks per wave
+  static constexpr int chunks = RB * 4 + kPfCT;  // 1 KiB chunks per stage
+  static constexpr int per_wave = chunks / 4;
+};
+
+// Issues this wave's direct-to-LDS loads of superblock ks (a plain function:
+// a lambda here keeps the host compiler from emitting the kernel's stub).
+template <int NC>
+__device__ __forceinline__ void pf_issue(int8_t* stage_base, int stage_bytes, const int8_t* const* src, const int* step,
+                                         int ks, int wv) {
+  int8_t* dst = stage_base + (ks % kPfStages) * stage_bytes + wv * NC * 1024;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) __builtin_amdgcn_global_load_lds(src[i] + (int64_t)ks * step[i], dst + i * 1024, 16, 0, 0);
+}
+
+template <int EPI, int RB>
 __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, int ngn) {
+  constexpr int kPfRB = PfShape<RB>::rb;
+  constexpr int XR = PfShape<RB>::xr;
+  constexpr int kPfChunks = PfShape<RB>::chunks;
+  constexpr int kPfChunksPerWave = PfShape<RB>::per_wave;
   // One LDS object: the stage buffers, then a_dq and the row sums of the
   // tile's rows.
   __shared__ __attribute__((aligned(16))) int8_t lds[kPfStages * kPfChunks * 1024 + kPfRB * 32 * 8];
@@ -438,30 +460,24 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
       step[i] = 1024;
     }
   }
-  auto issue = [&](int ks) {
-    int8_t* dst = &stage[ks % kPfStages][wv * kPfChunksPerWave * 1024];
-#pragma unroll
-    for (int i = 0; i < kPfChunksPerWave; ++i)
-      __builtin_amdgcn_global_load_lds(src[i] + (int64_t)ks * step[i], dst + i * 1024, 16, 0, 0);
-  };
-
   int slot[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) slot[u] = (EPI == EPI_RELU2) ? ((u < 2 ? 0 : 4) + 2 * wn + (u & 1)) : (4 * wn + u);
 
-  v16i acc[2][4];
+  v16i acc[XR][4];
 #pragma unroll
-  for (int x = 0; x < 2; ++x)
+  for (int x = 0; x < XR; ++x)
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc[x][u] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  // Row sums: wave (wm, wn) sums the bytes of its row block 2wm + wn only
-  // (the other wave of the pair takes the other block).
+  // Row sums: wave (wm, wn) sums the bytes of its row block XR*wm + wn only
+  // (the other wave of the pair takes the other block; with one row block
+  // per wave, wave wn = 0 does it).
   int32_t rs_lane = 0;
 
   const float adq_mine = p.a_dq[min(gm * kPfRB * 32 + (tid & (kPfRB * 32 - 1)), p.Mb * 32 - 1)];
 #pragma unroll
   for (int k = 0; k < kPfStages; ++k)
-    if (k < KS) issue(k);
+    if (k < KS) pf_issue<kPfChunksPerWave>(lds, kPfChunks * 1024, src, step, k, wv);
   for (int ks = 0; ks < KS; ++ks) {
     // this wave's loads of superblock ks are done once at most the loads of
     // the (up to kPfStages - 1) later superblocks are outstanding
@@ -479,19 +495,22 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
     for (int u = 0; u < 4; ++u) bw[u] = *reinterpret_cast<const v4i*>(buf + (kPfRB * 4 + slot[u]) * 1024 + lane * 16);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      v4i a[2];
+      v4i a[XR];
 #pragma unroll
-      for (int x = 0; x < 2; ++x) a[x] = *reinterpret_cast<const v4i*>(buf + ((2 * wm + x) * 4 + q) * 1024 + lane * 16);
+      for (int x = 0; x < XR; ++x) a[x] = *reinterpret_cast<const v4i*>(buf + ((XR * wm + x) * 4 + q) * 1024 + lane * 16);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const v4i b = unpack_b((uint32_t)bw[u][q]);
 #pragma unroll
-        for (int x = 0; x < 2; ++x) acc[x][u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[x], b, acc[x][u], 0, 0, 0);
+        for (int x = 0; x < XR; ++x) acc[x][u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[x], b, acc[x][u], 0, 0, 0);
       }
-      rs_lane = bytes_sum(wn == 0 ? a[0] : a[1], rs_lane);
+      if (XR == 2)
+        rs_lane = bytes_sum(wn == 0 ? a[0] : a[XR - 1], rs_lane);
+      else if (wn == 0)
+        rs_lane = bytes_sum(a[0], rs_lane);
     }
     barrier_only();  // every wave's reads of this buffer are done (their values fed the MFMAs)
-    if (ks + kPfStages < KS) issue(ks + kPfStages);
+    if (ks + kPfStages < KS) pf_issue<kPfChunksPerWave>(lds, kPfChunks * 1024, src, step, ks + kPfStages, wv);
   }
 
   // Epilogue in two passes through LDS (the stage buffers are free now):
@@ -500,7 +519,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   // stores, adding the residual read the same way.
   {
     const int32_t rs_row = rs_lane + (int32_t)xor_partner_u<32>((uint32_t)rs_lane);  // lanes l, l+32: halves of row l & 31
-    if (lane < 32) s_rs[(2 * wm + wn) * 32 + lane] = rs_row;
+    if (lane < 32 && (XR == 2 || wn == 0)) s_rs[(XR * wm + (XR == 2 ? wn : 0)) * 32 + lane] = rs_row;
     if (tid < kPfRB * 32) s_adq[tid] = adq_mine;  // loaded at the start; stored now, after the stage loads
   }
   __syncthreads();  // s_rs, s_adq visible; every wave is done with the stage buffers
@@ -522,18 +541,18 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
     }
   }
 #pragma unroll
-  for (int x = 0; x < 2; ++x) {
+  for (int x = 0; x < XR; ++x) {
     float ad[16];
     int32_t rsr[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      ad[r] = s_adq[(2 * wm + x) * 32 + acc_row(r, lane)];
-      rsr[r] = s_rs[(2 * wm + x) * 32 + acc_row(r, lane)];
+      ad[r] = s_adq[(XR * wm + x) * 32 + acc_row(r, lane)];
+      rsr[r] = s_rs[(XR * wm + x) * 32 + acc_row(r, lane)];
     }
     if (p.acc_out) {  // exact accumulators (debug output)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int i = gm * kPfRB * 32 + (2 * wm + x) * 32 + acc_row(r, lane);
+        const int i = gm * kPfRB * 32 + (XR * wm + x) * 32 + acc_row(r, lane);
         if (i >= p.M) continue;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -551,7 +570,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int32_t rs = rsr[r];
-      const int il = (2 * wm + x) * 32 + acc_row(r, lane);  // row within the tile
+      const int il = (XR * wm + x) * 32 + acc_row(r, lane);  // row within the tile
       if (EPI == EPI_RELU2) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -829,13 +848,22 @@ static GemmArgs gemm_args(const int8_t* xa, const float* a_dq, int64_t M, int64_
 static int launch_gemm(const GemmArgs& a, int epilogue, const GemmPlan& pl, hipStream_t s) {
   if (pl.prefill) {
     const int ngn = (epilogue == BTL_EPI_RELU2_MUL) ? (a.NT / 2 + 3) / 4 : (a.NT + kPfCT - 1) / kPfCT;
-    const int ngm = (a.Mb + kPfRB - 1) / kPfRB;
+    // 128-row tiles unless they would leave CUs idle
+    const int rb = ((a.Mb + 3) / 4) * ngn >= device_cus() ? 4 : 2;
+    const int ngm = (a.Mb + rb - 1) / rb;
     const int per = (ngm * ngn + kPfXcds - 1) / kPfXcds;
     dim3 grid((unsigned)(per * kPfXcds));
-    if (epilogue == BTL_EPI_RELU2_MUL)
-      hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2>), grid, dim3(256), 0, s, a, ngm, ngn);
-    else
-      hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE>), grid, dim3(256), 0, s, a, ngm, ngn);
+    if (epilogue == BTL_EPI_RELU2_MUL) {
+      if (rb == 4)
+        hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2, 4>), grid, dim3(256), 0, s, a, ngm, ngn);
+      else
+        hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2, 2>), grid, dim3(256), 0, s, a, ngm, ngn);
+    } else {
+      if (rb == 4)
+        hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE, 4>), grid, dim3(256), 0, s, a, ngm, ngn);
+      else
+        hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE, 2>), grid, dim3(256), 0, s, a, ngm, ngn);
+    }
     return check_launch("ternary gemm (prefill)");
   }
   const int nsb = decode_nsb(pl, a.KS, epilogue);

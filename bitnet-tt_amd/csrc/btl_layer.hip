@@ -281,7 +281,7 @@ __device__ float row_publish(const LayerArgs& p, const LayerOp& op, float (&v)[C
     if (tid < kActThreads && c < nch) {
       uint32_t lo, hi;
       quant8(v[i], scale, lo, hi, rs);
-      store8<true>(op.xa + xa_offset(m, 8 * c, op.KS), lo, hi);
+      store_chunk<true>(op.xa, m, c, op.KS, lo, hi);
     }
   }
   if (tid < kActThreads) {
