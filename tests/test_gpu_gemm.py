@@ -117,6 +117,25 @@ def test_segments_and_residual(orc):
         assert np.array_equal(acc, orc.gemm_i8t(q, w))
 
 
+@pytest.mark.parametrize("m,k,n", [(100, 512, 192), (64, 160, 96), (2048, 256, 4096), (32, 96, 64), (7, 160, 96)])
+def test_residual_segments_all_paths(orc, m, k, n):
+    """Residual and per-segment scales through the decode (M <= 32) and both
+    prefill tilings (64- and 128-row tiles: 2048 x 4096 fills the CUs with
+    128-row tiles); K not a multiple of 128 is zero-padded."""
+    print(f"residual m={m} k={k} n={n}", flush=True)
+    rng = np.random.default_rng(m + 3 * k + n)
+    q = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
+    w = H.ternary(k, n, seed=n + 5)
+    ends = [n // 2 - n // 2 % 32, n] if n >= 64 else [n]
+    scales = [0.013, 0.029][: len(ends)]
+    res = orc.f32_to_bf16(rng.standard_normal((m, n)).astype(np.float32))
+    acc, out, a_dq, _ = run_gemm(orc, q, w, scales, ends, residual_bits=res)
+    rows = np.arange(m) if m <= 128 else np.sort(rng.choice(m, 24, replace=False))
+    ref = orc.gemm_i8t(np.ascontiguousarray(q[rows]), w)
+    assert np.array_equal(acc[rows], ref)
+    assert np.array_equal(out[rows], expected_out(orc, ref, a_dq[rows], scales, ends, 0, res[rows]))
+
+
 @pytest.mark.parametrize("m,k,f", [(32, 256, 64), (32, 2560, 512), (5, 640, 96), (100, 256, 128)])
 def test_relu2_epilogue(orc, m, k, f):
     rng = np.random.default_rng(m + k + f)
