@@ -30,6 +30,8 @@
 // per superblock and shared by the four waves (64x128 each).
 #include <stdlib.h>
 
+#include <atomic>
+
 #include "btl_act_row.h"
 #include "btl_mfma.h"
 
@@ -70,7 +72,6 @@ struct FusedSync {
   int nact;         // activation workgroups (32)
   int ngemm;        // GEMM workgroups
   unsigned spin_limit;
-  int pre_sleep;    // s_sleep(8) rounds before the weight loads (row loads first)
 };
 constexpr int kSyncGroups = 8;
 constexpr int kSyncStride = 32;  // words: 128 bytes
@@ -163,8 +164,6 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
     }
   };
 
-  if (FUSED)
-    for (int i = 0; i < fs.pre_sleep; ++i) __builtin_amdgcn_s_sleep(8);
   if (wb < we) load_b(wb, (we - wb) < NSB ? (we - wb) : NSB);
   // The residual is an input of the launch: fetch it now, behind the weights.
   uint16_t res_pre[TPW][RR];
@@ -638,23 +637,25 @@ static int decode_waves() {
   return w;
 }
 
-// Compute units of the current device (256 on MI355X), cached per device.
+// Compute units of the current device (256 on MI355X), cached per device
+// (any thread may fill an entry; every writer stores the same value).  Host
+// code without a GPU (size queries) plans for 256.
 static int device_cus() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
     (void)hipGetLastError();
     return 256;
   }
-  if (!cached[dev]) {
-    int cus = 0;
+  int cus = cached[dev].load(std::memory_order_relaxed);
+  if (!cus) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
       (void)hipGetLastError();
       cus = 256;
     }
-    cached[dev] = cus;
+    cached[dev].store(cus, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return cus;
 }
 
 static int nsb_bucket(int per_wave) {
@@ -666,17 +667,6 @@ static int nsb_bucket(int per_wave) {
 
 constexpr int kFusedActBlocks = 32;
 constexpr int64_t kSyncBytes = 8192;  // handshake words of the fused decode kernel
-
-// Delay of the GEMM blocks' weight loads in the fused kernel (rounds of
-// s_sleep 8, about 0.2 us each) so the row loads of the activation blocks are
-// not queued behind the weight stream; BTL_FUSED_DELAY overrides it.
-static int fused_pre_sleep() {
-  static const int v = [] {
-    const char* e = getenv("BTL_FUSED_DELAY");
-    return e ? atoi(e) : 0;
-  }();
-  return v;
-}
 
 // max_wgs: cap on workgroups (the fused kernel keeps every block resident).
 static GemmPlan plan_decode(int64_t K, int64_t N, int epilogue, int splitk_req, int waves, int max_wgs) {
@@ -1008,7 +998,6 @@ int btl_bitlinear_fused(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, co
     fs.nact = kFusedActBlocks;
     fs.ngemm = pf.ngroups * pf.splitk;
     fs.spin_limit = 1u << 20;
-    fs.pre_sleep = fused_pre_sleep();
     const int nsb = decode_nsb(pf, ksb(K), epilogue);
     const dim3 grid((unsigned)(kFusedActBlocks + fs.ngemm));
     const int cpt = act_cpt(K);

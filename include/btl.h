@@ -150,7 +150,10 @@ int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, int64_t M, int64_t K, int
  * that is non-zero when a bounded wait of the single-launch decode kernel
  * ran out (the outputs of that call are then invalid).  The first 8192 bytes
  * of the workspace hold that kernel's handshake words; they must be zero
- * before the first call and every completed call leaves them zero. */
+ * before the first call and every completed call leaves them zero.  A wait
+ * can only run out when the launch's workgroups are not all resident at once
+ * (another kernel holding CUs); after that, zero-fill the workspace again
+ * before reusing it. */
 int64_t btl_fused_error_offset(void);
 
 /* One BitLinear launch sequence: [RMSNorm(gamma) ->] absmax quant -> ternary
@@ -201,7 +204,9 @@ int64_t btl_decode_layer_error_offset(void);
  * results).  M <= 32 rows; attn [M,Q], hidden [M,H] (in/out), ffn_h [M,F],
  * qkv_out [M,NQKV] bf16.  gate_up has two segments split at F.  The launch
  * uses one workgroup per CU and waits between its phases; nothing else may
- * share the GPU's compute units while it runs. */
+ * share the GPU's compute units while it runs (a wait that runs out sets the
+ * word at btl_decode_layer_error_offset(); zero-fill the workspace before
+ * reusing it then). */
 int btl_decode_layer(int64_t M, int64_t H, int64_t Q, int64_t F, int64_t NQKV, const btl_layer_weight_t* o_proj,
                      const btl_layer_weight_t* gate_up, const btl_layer_weight_t* down,
                      const btl_layer_weight_t* next_qkv, float eps, const uint16_t* attn, uint16_t* hidden,
