@@ -59,24 +59,33 @@ struct GemmArgs {
   uint32_t* ws_cnt;
 };
 
-// Producer/consumer handshake of the fused decode kernel (each word on its
-// own 128-byte line):
-//   ready: activation block m sets flag m once its row is published; a GEMM
-//          block polls the 32 flags with 32 lanes of one wave.
-//   pass:  a GEMM block bumps its group counter (8 groups) once it has passed
-//          the wait, and checks the result only when it exits; the last of a
-//          group bumps the top counter, and the block completing the top
-//          counter clears the flags and counters for the next call.
+// Producer/consumer handshake of the fused decode kernel: launch counters,
+// so no call has to reset anything for the next one.
+//   ready[m] (own 128-byte line each): the number of launches whose row m
+//          activation block has published its row.  Block m reads it when it
+//          starts and stores one more once the row is out.
+//   seen[j], j < kGemmSlots (packed words): the number of launches the GEMM
+//          slot has taken part in.  GEMM block g reads seen[g] when it starts,
+//          so e = seen[g] + 1 names this launch; it waits until every ready
+//          word has reached e, then stores e into the slots g, g + ngemm, ...
+//          so that slots beyond this launch's grid keep the count too.
+// Every completed launch leaves all ready and seen words at the same count
+// (zero-filled = no launch yet), whatever grid sizes share the workspace.
 struct FusedSync {
-  uint32_t* words;  // handshake words, 32 words apart
+  uint32_t* words;  // handshake words
   int nact;         // activation workgroups (32)
-  int ngemm;        // GEMM workgroups
+  int ngemm;        // GEMM workgroups (at most kGemmSlots)
   unsigned spin_limit;
 };
-constexpr int kSyncGroups = 8;
-constexpr int kSyncStride = 32;  // words: 128 bytes
-enum { kReadyFlag = 0, kPassGrp = 32, kPassTop = 40, kErrorWord = 41 };
+constexpr int kSyncStride = 32;   // words: 128 bytes
+constexpr int kReadyStride = kSyncStride;
+constexpr int kGemmSlots = 512;   // bound on the GEMM workgroups of one launch
+enum { kErrorWord = 32, kSeenLine = 33 };  // in 128-byte lines; ready words from line 0
 __device__ __forceinline__ uint32_t* sync_word(const FusedSync& fs, int w) { return fs.words + w * kSyncStride; }
+__device__ __forceinline__ uint32_t* ready_word(const FusedSync& fs, int m) { return fs.words + m * kReadyStride; }
+__device__ __forceinline__ uint32_t* seen_word(const FusedSync& fs, int j) {
+  return fs.words + kSeenLine * kSyncStride + j;
+}
 
 __device__ __forceinline__ float seg_scale_of(const GemmArgs& p, int n) {
   float s = p.seg_scale[0];
@@ -172,27 +181,14 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
 #pragma unroll
     for (int rr = 0; rr < RR; ++rr)
       res_pre[t][rr] = EPI == EPI_SCALE ? residual_at(p, acc_row(wv + WAVES * rr, lane), tile[t] * 32 + (lane & 31)) : 0;
-  // pass accounting of the fused handshake: issued after the wait, settled
-  // when the block exits (its latency hides behind the GEMM).
-  uint32_t pass_prev = 0;
-  const int pass_grp = bid % kSyncGroups;
-  auto settle_pass = [&]() {
-    if (!FUSED || tid != 0) return;
-    const int grp_size = fs.ngemm / kSyncGroups + (pass_grp < fs.ngemm % kSyncGroups ? 1 : 0);
-    if (pass_prev + 1 != (uint32_t)grp_size) return;
-    const int ngrp = fs.ngemm < kSyncGroups ? fs.ngemm : kSyncGroups;
-    if (atomicAdd(sync_word(fs, kPassTop), 1u) + 1 != (uint32_t)ngrp) return;
-    for (int i = 0; i < fs.nact; ++i) st_coherent(sync_word(fs, kReadyFlag + i), 0u);  // all GEMM blocks are past the wait
-    for (int i = 0; i < kSyncGroups; ++i) st_coherent(sync_word(fs, kPassGrp + i), 0u);
-    st_coherent(sync_word(fs, kPassTop), 0u);
-  };
   float ad_pre[RR];
   if (FUSED) {
     // Every thread of the workgroup reaches this barrier, with or without work.
     if (wv == WAVES - 1) {
+      const uint32_t e = ld_coherent(seen_word(fs, bid)) + 1u;  // this launch's number
       unsigned n = 0;
       for (;;) {
-        const bool mine = lane >= fs.nact || ld_coherent(sync_word(fs, kReadyFlag + lane)) != 0u;
+        const bool mine = lane >= fs.nact || (int32_t)(ld_coherent(ready_word(fs, lane)) - e) >= 0;
         if (__all(mine)) break;
         if (++n > fs.spin_limit) {
           if (lane == 0) st_coherent(sync_word(fs, kErrorWord), 1u);
@@ -200,9 +196,10 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
         }
         __builtin_amdgcn_s_sleep(1);
       }
+      // after the wait: stores count in the same wait counter as the polls
+      for (int j = bid + lane * fs.ngemm; j < kGemmSlots; j += 64 * fs.ngemm) st_coherent(seen_word(fs, j), e);
     }
     __syncthreads();
-    if (tid == 0) pass_prev = atomicAdd(sync_word(fs, kPassGrp + pass_grp), 1u);
     // Scales of the rows this thread finishes, loaded with the activations.
 #pragma unroll
     for (int rr = 0; rr < RR; ++rr) ad_pre[rr] = ld_coherent(p.a_dq + acc_row(wv + WAVES * rr, lane));
@@ -290,10 +287,7 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
       s_last = (prev == (unsigned)(p.splitk - 1));
     }
     __syncthreads();
-    if (!s_last) {
-      settle_pass();
-      return;
-    }
+    if (!s_last) return;
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
 #pragma unroll
@@ -324,7 +318,6 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
       for (int t = 0; t < TPW; ++t) epi_scale(p, i, tile[t] * 32 + j, v[t][rr], ad, res_pre[t][rr]);
     }
   }
-  settle_pass();
 }
 
 template <int TPW, int NSB, int EPI, int WAVES>
@@ -338,10 +331,12 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_decode(GemmArgs p) {
 template <int TPW, int NSB, int EPI, bool NORM, int CPT>
 __global__ __launch_bounds__(512) void k_bitlinear_decode(GemmArgs p, ActArgs a, FusedSync fs) {
   if ((int)blockIdx.x < fs.nact) {
+    uint32_t* ready = ready_word(fs, (int)blockIdx.x);
+    const uint32_t e = threadIdx.x == 0 ? ld_coherent(ready) + 1u : 0u;  // read while the row loads
     act_row<NORM, true, true, CPT>(a, blockIdx.x, threadIdx.x);
     wait_memory();
     __syncthreads();
-    if (threadIdx.x == 0) st_coherent(sync_word(fs, kReadyFlag + (int)blockIdx.x), 1u);
+    if (threadIdx.x == 0) st_coherent(ready, e);
     return;
   }
   gemm_decode_wg<TPW, NSB, EPI, 8, true>(p, blockIdx.x - fs.nact, fs);
@@ -667,6 +662,7 @@ static int nsb_bucket(int per_wave) {
 
 constexpr int kFusedActBlocks = 32;
 constexpr int64_t kSyncBytes = 8192;  // handshake words of the fused decode kernel
+static_assert((kSeenLine * kSyncStride + kGemmSlots) * 4 <= kSyncBytes, "handshake words overflow");
 
 // max_wgs: cap on workgroups (the fused kernel keeps every block resident).
 static GemmPlan plan_decode(int64_t K, int64_t N, int epilogue, int splitk_req, int waves, int max_wgs) {
@@ -718,7 +714,7 @@ static GemmPlan plan_fused(int64_t M, int64_t K, int64_t N, int epilogue, int sp
   // the 2B shapes: o_proj 8.6 us unsplit vs 9.6 us split in two).
   if (splitk_req <= 0) splitk_req = 1;
   GemmPlan pl = plan_decode(K, N, epilogue, splitk_req, 8, max_wgs);
-  pl.fused = (int64_t)pl.ngroups * pl.splitk <= max_wgs && act_cpt(K) <= 4;
+  pl.fused = (int64_t)pl.ngroups * pl.splitk <= max_wgs && pl.ngroups * pl.splitk <= kGemmSlots && act_cpt(K) <= 4;
   return pl;
 }
 

@@ -149,11 +149,12 @@ int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, int64_t M, int64_t K, int
 /* Byte offset, inside a btl_bitlinear_fused workspace, of the 32-bit word
  * that is non-zero when a bounded wait of the single-launch decode kernel
  * ran out (the outputs of that call are then invalid).  The first 8192 bytes
- * of the workspace hold that kernel's handshake words; they must be zero
- * before the first call and every completed call leaves them zero.  A wait
- * can only run out when the launch's workgroups are not all resident at once
- * (another kernel holding CUs); after that, zero-fill the workspace again
- * before reusing it. */
+ * of the workspace hold that kernel's launch counters; they must be zero
+ * before the first call (a zero-filled workspace), and every completed call
+ * leaves them ready for the next one, whatever shapes share the workspace.
+ * A wait can only run out when the launch's workgroups are not all resident
+ * at once (another kernel holding CUs); after that, zero-fill the workspace
+ * again before reusing it. */
 int64_t btl_fused_error_offset(void);
 
 /* One BitLinear launch sequence: [RMSNorm(gamma) ->] absmax quant -> ternary

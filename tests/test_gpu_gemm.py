@@ -216,7 +216,9 @@ def test_fused_entry_matches_split_path(orc):
 
 def test_fused_decode_handshake_clean(orc):
     """The single-launch decode path (activation blocks + GEMM blocks) leaves its
-    producer/consumer words at zero and never reports a timed-out wait."""
+    launch counters all equal (ready words of the 32 activation blocks and the
+    512 GEMM slots, across calls with different GEMM grids) and never reports
+    a timed-out wait."""
     from bitnet_tt.ternary_matmul import PackedTernaryWeight, ternary_matmul
 
     for m, k, n, epi in [(32, 2560, 3840, "none"), (5, 6912, 2560, "none"), (32, 2560, 1024, "relu2_mul")]:
@@ -236,4 +238,10 @@ def test_fused_decode_handshake_clean(orc):
             continue  # decode-layer workspaces keep launch counters
         words = ws[:8192].view(torch.int32).cpu().numpy()
         assert words[err // 4] == 0, "a bounded wait ran out"
-        assert not words.any(), "handshake counters must be reset after every call"
+        ready = words[0:32 * 32:32]  # one per 128-byte line
+        seen = words[33 * 32:33 * 32 + 512]
+        assert ready.min() == ready.max() == seen.min() == seen.max() > 0, "launch counters out of step"
+        rest = words.copy()
+        rest[0:32 * 32:32] = 0
+        rest[33 * 32:33 * 32 + 512] = 0
+        assert not rest.any(), "stray handshake words"
