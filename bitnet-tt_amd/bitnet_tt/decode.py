@@ -33,6 +33,8 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import numpy as np
+
 from . import _native as N
 from .config import BitNetConfig
 from .ternary_matmul import PackedTernaryWeight, ternary_matmul_into
@@ -134,6 +136,97 @@ class BitLinearDecodeStep:
         pos, neg = counts[0].item() / n_total, counts[2].item() / n_total
         self.ternary_split = (pos, 1.0 - pos - neg, neg)
         return self
+
+    @classmethod
+    def from_state_dict(cls, config: BitNetConfig, state_dict: dict, device, batch: int = 32,
+                        num_layers: int | None = None):
+        """Weights from a state dict under the reference's keys (what
+        ``utils.weights.load_bitnet_weights`` returns): float latents are
+        quantised on the device by the absmean rule, ``TernaryWeight`` entries
+        (HF's pre-packed checkpoint) are taken as they are."""
+        from .utils.weights import get_layer_weights
+
+        self = cls(config, device, batch)
+        L = config.num_layers if num_layers is None else num_layers
+        self.layers = [None] * L
+        self._counts = [0, 0, 0]
+        for i in range(L):
+            lw = get_layer_weights(state_dict, i)
+            if not lw:
+                raise KeyError(f"layer {i}: the state dict holds no 'layers.{i}.*' entries")
+            self.load_layer_weights(i, lw)
+        return self
+
+    def load_layer_weights(self, layer_idx: int, weights: dict) -> None:
+        """One layer from its state-dict entries (keys without the
+        ``layers.<i>.`` prefix, utils/weights.py:158-181): q|k|v fused with
+        three scales (attention.py:481-506), o_proj, gate|up fused with two
+        scales (ffn.py:22-34), down, and the four RMSNorm gains."""
+        import torch
+
+        from .layers.bitlinear import pack_for_device, to_device_bf16
+        from .utils.quantization import weight_quant_ternary
+        from .utils.weights import TernaryWeight
+
+        c = self.config
+        H, F = c.hidden_size, c.intermediate_size
+        qd, kvd = c.num_attention_heads * c.head_dim, c.num_kv_heads * c.head_dim
+
+        def entry(name):
+            key = name + ".weight"
+            if key not in weights:
+                raise KeyError(f"layer {layer_idx}: missing {key!r}")
+            return weights[key]
+
+        def ternary(name, rows, cols):
+            w = entry(name)
+            if isinstance(w, TernaryWeight):
+                if w.q.shape[1] != cols or w.q.shape[0] < rows:
+                    raise ValueError(f"layer {layer_idx} {name}: ternary weight {w.q.shape}, expected ({rows}, {cols})")
+                q = torch.from_numpy(np.ascontiguousarray(w.q[:rows])).to(device=self.device)
+                return q, float(w.scale)
+            a = np.asarray(w, dtype=np.float32)
+            if a.shape != (rows, cols):
+                raise ValueError(f"layer {layer_idx} {name}: weight {a.shape}, expected ({rows}, {cols})")
+            return weight_quant_ternary(torch.from_numpy(a).to(device=self.device))
+
+        def fused(parts):
+            qs, scales, ends, total = [], [], [], 0
+            for name, rows, cols in parts:
+                q, sc = ternary(name, rows, cols)
+                qs.append(q)
+                scales.append(float(sc))
+                total += rows
+                ends.append(total)
+            q = qs[0] if len(qs) == 1 else torch.cat(qs, dim=0)
+            if getattr(self, "_counts", None) is not None:
+                self._counts[0] += int((q == 1).sum().item())
+                self._counts[1] += int((q == -1).sum().item())
+                self._counts[2] += q.numel()
+                pos, neg = self._counts[0] / self._counts[2], self._counts[1] / self._counts[2]
+                self.ternary_split = (pos, 1.0 - pos - neg, neg)
+            return pack_for_device(q, self.device, tuple(scales), tuple(ends))
+
+        def gamma(name, n):
+            g = np.asarray(entry(name), dtype=np.float32).reshape(-1)
+            if g.size != n:
+                raise ValueError(f"layer {layer_idx} {name}: {g.size} gains, expected {n}")
+            return to_device_bf16(g, self.device)
+
+        lw = LayerWeights(
+            fused([("self_attn.q_proj", qd, H), ("self_attn.k_proj", kvd, H), ("self_attn.v_proj", kvd, H)]),
+            fused([("self_attn.o_proj", H, qd)]),
+            fused([("mlp.gate_proj", F, H), ("mlp.up_proj", F, H)]),
+            fused([("mlp.down_proj", H, F)]),
+            gamma("input_layernorm", H),
+            gamma("self_attn.attn_sub_norm", qd),
+            gamma("post_attention_layernorm", H),
+            gamma("mlp.ffn_sub_norm", F),
+        )
+        while len(self.layers) <= layer_idx:
+            self.layers.append(None)
+        self.layers[layer_idx] = lw
+        self._lw = None  # layer structs of the persistent launch are rebuilt
 
     # -- buffers -----------------------------------------------------------
     def alloc_buffers(self, seed: int = 1):

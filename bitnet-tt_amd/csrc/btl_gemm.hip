@@ -383,6 +383,22 @@ __device__ __forceinline__ int pf_tile(const GemmArgs& p, int gn, int slot) {
 // vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
 #define BTL_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 
+// Waits until at most min(later, S - 1) superblocks' worth (PW loads each) of
+// this wave's direct-to-LDS loads are outstanding (the immediate of s_waitcnt
+// is a compile-time constant, hence the recursion).
+template <int PW, int S>
+__device__ __forceinline__ void pf_wait(int later) {
+  if constexpr (S > 1) {
+    if (later >= S - 1) {
+      BTL_WAIT_VMCNT((S - 1) * PW);
+      return;
+    }
+    pf_wait<PW, S - 1>(later);
+  } else {
+    BTL_WAIT_VMCNT(0);
+  }
+}
+
 // Workgroup barrier without the memory fence of __syncthreads (whose release
 // part would wait for every load in flight, the LDS-direct ones included);
 // the compiler fences keep LDS accesses on their side of it.
@@ -475,13 +491,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   for (int ks = 0; ks < KS; ++ks) {
     // this wave's loads of superblock ks are done once at most the loads of
     // the (up to kPfStages - 1) later superblocks are outstanding
-    const int later = KS - 1 - ks;
-    if (later >= 2)
-      BTL_WAIT_VMCNT(2 * kPfChunksPerWave);
-    else if (later == 1)
-      BTL_WAIT_VMCNT(kPfChunksPerWave);
-    else
-      BTL_WAIT_VMCNT(0);
+    pf_wait<kPfChunksPerWave, kPfStages>(KS - 1 - ks);
     barrier_only();
     const int8_t* buf = stage[ks % kPfStages];
     v4i bw[4];

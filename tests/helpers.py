@@ -71,3 +71,71 @@ def rowmajor_to_xa(q: np.ndarray) -> np.ndarray:
     full = np.zeros((mb * 32, ks * 128), np.int8)
     full[:m, :k] = q
     return np.ascontiguousarray(full.reshape(mb, 32, ks, 4, 2, 16).transpose(0, 2, 3, 4, 1, 5)).reshape(-1).view(np.uint8)
+
+
+HF_BITLINEARS = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                 "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+
+
+def bitlinear_shapes(cfg):
+    """(out, in) of each BitLinear of a layer, by HF module name."""
+    H_, F = cfg.hidden_size, cfg.intermediate_size
+    qd, kvd = cfg.num_attention_heads * cfg.head_dim, cfg.num_kv_heads * cfg.head_dim
+    return {"self_attn.q_proj": (qd, H_), "self_attn.k_proj": (kvd, H_), "self_attn.v_proj": (kvd, H_),
+            "self_attn.o_proj": (H_, qd), "mlp.gate_proj": (F, H_), "mlp.up_proj": (F, H_),
+            "mlp.down_proj": (H_, F)}
+
+
+def write_hf_snapshot(path, cfg, seed, packed=False, embed=True):
+    """A small HF-style checkpoint directory (config.json + one safetensors
+    file, HF key names).  Latents ~N(0, 0.02) and gains ~N(1, 0.1) stored in
+    bf16; with ``packed`` every BitLinear weight is absmean-quantised and
+    stored in HF's uint8 layout with a bf16 ``weight_scale`` = 1/scale.
+    Returns {hf key: float32 latent or (int8 ternary, float32 scale)}."""
+    import json
+    import os
+
+    import torch
+    from safetensors.torch import save_file
+
+    from bitnet_tt.utils.quantization import weight_quant_ternary
+    from bitnet_tt.utils.weights import pack_hf_ternary
+
+    rng = np.random.default_rng(seed)
+    tensors, expect = {}, {}
+
+    def bf16(a):
+        return torch.from_numpy(np.asarray(a, dtype=np.float32)).to(torch.bfloat16)
+
+    qd = cfg.num_attention_heads * cfg.head_dim
+    for i in range(cfg.num_layers):
+        pre = f"model.layers.{i}."
+        for name, (o, n) in bitlinear_shapes(cfg).items():
+            w = bf16(rng.standard_normal((o, n)) * 0.02)
+            wf = w.float().numpy()
+            key = pre + name + ".weight"
+            if packed:
+                q, s = weight_quant_ternary(wf)
+                tensors[key] = torch.from_numpy(pack_hf_ternary(q))
+                ws = bf16([1.0 / float(s)])
+                tensors[pre + name + ".weight_scale"] = ws
+                expect[key] = (q, np.float32(1.0) / ws.float().numpy()[0])
+            else:
+                tensors[key] = w
+                expect[key] = wf
+        for name, n in (("input_layernorm", cfg.hidden_size), ("post_attention_layernorm", cfg.hidden_size),
+                        ("self_attn.attn_sub_norm", qd), ("mlp.ffn_sub_norm", cfg.intermediate_size)):
+            g = bf16(1.0 + 0.1 * rng.standard_normal(n))
+            tensors[pre + name + ".weight"] = g
+            expect[pre + name + ".weight"] = g.float().numpy()
+    if embed:
+        tensors["model.embed_tokens.weight"] = bf16(rng.standard_normal((cfg.vocab_size, cfg.hidden_size)))
+    tensors["model.norm.weight"] = bf16(np.ones(cfg.hidden_size))
+    os.makedirs(path, exist_ok=True)
+    save_file(tensors, os.path.join(path, "model.safetensors"))
+    with open(os.path.join(path, "config.json"), "w") as f:
+        json.dump({"hidden_size": cfg.hidden_size, "num_hidden_layers": cfg.num_layers,
+                   "num_attention_heads": cfg.num_attention_heads, "num_key_value_heads": cfg.num_key_value_heads,
+                   "intermediate_size": cfg.intermediate_size, "vocab_size": cfg.vocab_size,
+                   "rms_norm_eps": cfg.rms_norm_eps, "rope_theta": cfg.rope_theta}, f)
+    return expect
