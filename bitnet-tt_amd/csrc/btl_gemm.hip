@@ -352,9 +352,12 @@ __global__ __launch_bounds__(512) void k_bitlinear_decode(GemmArgs p, ActArgs a,
 // 16i), so staging costs no registers.  kPfStages superblocks are in flight:
 // a stage is waited for (vmcnt of the wave's own loads, then a barrier), its
 // MFMAs run, and after a second barrier the freed buffer is refilled with the
-// superblock kPfStages ahead.  Wave (wm, wn) = (wv & 1, wv >> 1) computes row
-// blocks 2wm, 2wm+1 against four slots: 4wn..4wn+3 (scale) or gate slots 2wn,
-// 2wn+1 with up slots 4+2wn, 5+2wn (relu2).
+// superblock kPfStages ahead.  The four waves form a WR x (4/WR) grid: wave
+// (wm, wn) = (wv % WR, wv / WR) computes the RB/WR row blocks from
+// (RB/WR)*wm against US = 2*WR column slots: US*wn.. (scale), or US/2 gate
+// slots from (US/2)*wn with the up slots 4 above them (relu2: a column's gate
+// and up tiles stay in one wave).  With WR = 1 a wave covers every row block,
+// so each unpacked weight operand feeds RB MFMAs.
 //
 // Tile order is XCD-aware: workgroup b runs on XCD b % 8, so tiles are
 // numbered in groups of kPfGroupRows row tiles (column tiles inner) and XCD x
@@ -408,11 +411,13 @@ __device__ __forceinline__ void barrier_only() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-template <int RB>
+template <int RB, int WR>
 struct PfShape {
   static_assert(RB == 2 || RB == 4, "64- or 128-row tiles");
+  static_assert(WR == 1 || WR == 2, "waves along the rows");
   static constexpr int rb = RB;                  // row blocks of 32 per workgroup
-  static constexpr int xr = RB / 2;              // row blocks per wave
+  static constexpr int xr = RB / WR;             // row blocks per wave
+  static constexpr int us = 2 * WR;              // column slots per wave
   static constexpr int chunks = RB * 4 + kPfCT;  // 1 KiB chunks per stage
   static constexpr int per_wave = chunks / 4;
 };
@@ -427,12 +432,14 @@ __device__ __forceinline__ void pf_issue(int8_t* stage_base, int stage_bytes, co
   for (int i = 0; i < NC; ++i) __builtin_amdgcn_global_load_lds(src[i] + (int64_t)ks * step[i], dst + i * 1024, 16, 0, 0);
 }
 
-template <int EPI, int RB>
+template <int EPI, int RB, int WR>
 __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, int ngn) {
-  constexpr int kPfRB = PfShape<RB>::rb;
-  constexpr int XR = PfShape<RB>::xr;
-  constexpr int kPfChunks = PfShape<RB>::chunks;
-  constexpr int kPfChunksPerWave = PfShape<RB>::per_wave;
+  constexpr int kPfRB = PfShape<RB, WR>::rb;
+  constexpr int XR = PfShape<RB, WR>::xr;
+  constexpr int US = PfShape<RB, WR>::us;
+  constexpr int HU = US / 2;  // relu2: gate (and up) slots per wave
+  constexpr int kPfChunks = PfShape<RB, WR>::chunks;
+  constexpr int kPfChunksPerWave = PfShape<RB, WR>::per_wave;
   // One LDS object: the stage buffers, then a_dq and the row sums of the
   // tile's rows.
   __shared__ __attribute__((aligned(16))) int8_t lds[kPfStages * kPfChunks * 1024 + kPfRB * 32 * 8];
@@ -440,7 +447,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   float* s_adq = reinterpret_cast<float*>(lds + kPfStages * kPfChunks * 1024);
   int32_t* s_rs = reinterpret_cast<int32_t*>(lds + kPfStages * kPfChunks * 1024 + kPfRB * 32 * 4);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int wm = wv & 1, wn = wv >> 1;
+  const int wm = wv % WR, wn = wv / WR;
   const int ntiles = ngm * ngn;
   const int per = (ntiles + kPfXcds - 1) / kPfXcds;
   const int t = (int)(blockIdx.x % kPfXcds) * per + (int)(blockIdx.x / kPfXcds);
@@ -470,18 +477,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
       step[i] = 1024;
     }
   }
-  int slot[4];
+  int slot[US];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) slot[u] = (EPI == EPI_RELU2) ? ((u < 2 ? 0 : 4) + 2 * wn + (u & 1)) : (4 * wn + u);
+  for (int u = 0; u < US; ++u) slot[u] = (EPI == EPI_RELU2) ? ((u < HU ? 0 : 4) + HU * wn + u % HU) : (US * wn + u);
 
-  v16i acc[XR][4];
+  v16i acc[XR][US];
 #pragma unroll
   for (int x = 0; x < XR; ++x)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc[x][u] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  // Row sums: wave (wm, wn) sums the bytes of its row block XR*wm + wn only
-  // (the other wave of the pair takes the other block; with one row block
-  // per wave, wave wn = 0 does it).
+    for (int u = 0; u < US; ++u) acc[x][u] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  // Row sums: each row block of the tile is summed by one wave: wave (wm, wn)
+  // takes its row block XR*wm + wn when wn < XR.
   int32_t rs_lane = 0;
 
   const float adq_mine = p.a_dq[min(gm * kPfRB * 32 + (tid & (kPfRB * 32 - 1)), p.Mb * 32 - 1)];
@@ -494,24 +500,23 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
     pf_wait<kPfChunksPerWave, kPfStages>(KS - 1 - ks);
     barrier_only();
     const int8_t* buf = stage[ks % kPfStages];
-    v4i bw[4];
+    v4i bw[US];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) bw[u] = *reinterpret_cast<const v4i*>(buf + (kPfRB * 4 + slot[u]) * 1024 + lane * 16);
+    for (int u = 0; u < US; ++u) bw[u] = *reinterpret_cast<const v4i*>(buf + (kPfRB * 4 + slot[u]) * 1024 + lane * 16);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       v4i a[XR];
 #pragma unroll
       for (int x = 0; x < XR; ++x) a[x] = *reinterpret_cast<const v4i*>(buf + ((XR * wm + x) * 4 + q) * 1024 + lane * 16);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < US; ++u) {
         const v4i b = unpack_b((uint32_t)bw[u][q]);
 #pragma unroll
         for (int x = 0; x < XR; ++x) acc[x][u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[x], b, acc[x][u], 0, 0, 0);
       }
-      if (XR == 2)
-        rs_lane = bytes_sum(wn == 0 ? a[0] : a[XR - 1], rs_lane);
-      else if (wn == 0)
-        rs_lane = bytes_sum(a[0], rs_lane);
+#pragma unroll
+      for (int x = 0; x < XR; ++x)
+        if (x == wn) rs_lane = bytes_sum(a[x], rs_lane);  // wn is uniform across the wave
     }
     barrier_only();  // every wave's reads of this buffer are done (their values fed the MFMAs)
     if (ks + kPfStages < KS) pf_issue<kPfChunksPerWave>(lds, kPfChunks * 1024, src, step, ks + kPfStages, wv);
@@ -523,7 +528,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   // stores, adding the residual read the same way.
   {
     const int32_t rs_row = rs_lane + (int32_t)xor_partner_u<32>((uint32_t)rs_lane);  // lanes l, l+32: halves of row l & 31
-    if (lane < 32 && (XR == 2 || wn == 0)) s_rs[(XR * wm + (XR == 2 ? wn : 0)) * 32 + lane] = rs_row;
+    if (lane < 32 && wn < XR) s_rs[(XR * wm + wn) * 32 + lane] = rs_row;
     if (tid < kPfRB * 32) s_adq[tid] = adq_mine;  // loaded at the start; stored now, after the stage loads
   }
   __syncthreads();  // s_rs, s_adq visible; every wave is done with the stage buffers
@@ -533,13 +538,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   static_assert(kPfRB * 32 * kPitch <= kPfStages * kPfChunks * 1024, "output tile fits in the stage buffers");
   const int j = lane & 31;
   // weight scale per slot: segment ends are multiples of 32, so one per tile
-  float sw[4];
+  float sw[US];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < US; ++u) {
     if (EPI == EPI_RELU2) {
       const int half = p.NT >> 1;
-      const int g = min(gn * 4 + 2 * wn + (u & 1), half - 1);
-      sw[u] = seg_scale_of(p, (u < 2 ? g : g + half) * 32);
+      const int g = min(gn * 4 + HU * wn + u % HU, half - 1);
+      sw[u] = seg_scale_of(p, (u < HU ? g : g + half) * 32);
     } else {
       sw[u] = seg_scale_of(p, min(gn * kPfCT + slot[u], p.NT - 1) * 32);
     }
@@ -559,11 +564,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
         const int i = gm * kPfRB * 32 + (XR * wm + x) * 32 + acc_row(r, lane);
         if (i >= p.M) continue;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < US; ++u) {
           int t;
           if (EPI == EPI_RELU2) {
-            const int g = gn * 4 + 2 * wn + (u & 1);
-            t = g < (p.NT >> 1) ? (u < 2 ? g : g + (p.NT >> 1)) : -1;
+            const int g = gn * 4 + HU * wn + u % HU;
+            t = g < (p.NT >> 1) ? (u < HU ? g : g + (p.NT >> 1)) : -1;
           } else {
             t = gn * kPfCT + slot[u] < p.NT ? gn * kPfCT + slot[u] : -1;
           }
@@ -577,16 +582,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
       const int il = (XR * wm + x) * 32 + acc_row(r, lane);  // row within the tile
       if (EPI == EPI_RELU2) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int32_t ag = acc[x][u][r] - rs, au = acc[x][u + 2][r] - rs;
+        for (int u = 0; u < HU; ++u) {
+          const int32_t ag = acc[x][u][r] - rs, au = acc[x][u + HU][r] - rs;
           const float gg = bf2f(f2bf((float)ag * (sw[u] * ad[r])));
-          const float uu = bf2f(f2bf((float)au * (sw[u + 2] * ad[r])));
+          const float uu = bf2f(f2bf((float)au * (sw[u + HU] * ad[r])));
           const float gr = gg > 0.0f ? gg : 0.0f;
-          *reinterpret_cast<uint16_t*>(tile_lds + il * kPitch + ((2 * wn + u) * 32 + j) * 2) = f2bf(bf2f(f2bf(gr * gr)) * uu);
+          *reinterpret_cast<uint16_t*>(tile_lds + il * kPitch + ((HU * wn + u) * 32 + j) * 2) = f2bf(bf2f(f2bf(gr * gr)) * uu);
         }
       } else {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < US; ++u) {
           const int32_t v = acc[x][u][r] - rs;
           *reinterpret_cast<uint16_t*>(tile_lds + il * kPitch + (slot[u] * 32 + j) * 2) = f2bf((float)v * (sw[u] * ad[r]));
         }
@@ -854,16 +859,22 @@ static int launch_gemm(const GemmArgs& a, int epilogue, const GemmPlan& pl, hipS
     const int ngm = (a.Mb + rb - 1) / rb;
     const int per = (ngm * ngn + kPfXcds - 1) / kPfXcds;
     dim3 grid((unsigned)(per * kPfXcds));
+    // Every wave takes two row blocks, so each unpacked weight operand feeds
+    // two MFMAs: 64-row tiles run the 1 x 4 wave grid (2 column slots per
+    // wave), 128-row tiles the 2 x 2 grid (4 slots).  Measured on MI355X at
+    // the 2B shapes, one row block per wave is 5-9 % slower (VALU unpacking
+    // that does not overlap the MFMAs) and four per wave ~10 % slower (LDS
+    // reads and 237 VGPRs).
     if (epilogue == BTL_EPI_RELU2_MUL) {
       if (rb == 4)
-        hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2, 4>), grid, dim3(256), 0, s, a, ngm, ngn);
+        hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2, 4, 2>), grid, dim3(256), 0, s, a, ngm, ngn);
       else
-        hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2, 2>), grid, dim3(256), 0, s, a, ngm, ngn);
+        hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2, 2, 1>), grid, dim3(256), 0, s, a, ngm, ngn);
     } else {
       if (rb == 4)
-        hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE, 4>), grid, dim3(256), 0, s, a, ngm, ngn);
+        hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE, 4, 2>), grid, dim3(256), 0, s, a, ngm, ngn);
       else
-        hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE, 2>), grid, dim3(256), 0, s, a, ngm, ngn);
+        hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE, 2, 1>), grid, dim3(256), 0, s, a, ngm, ngn);
     }
     return check_launch("ternary gemm (prefill)");
   }
