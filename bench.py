@@ -49,6 +49,7 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=10, help="repetitions of the per-kernel event pass")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-lm-head", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="approximate CPU-baseline sample length")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="run only the workload of the rocprofv3 --pmc traffic runs and exit")
@@ -229,6 +230,72 @@ def prefill_mfma(torch, N, dev):
     return out
 
 
+# ------------------------------------------------------------------ LM head ----
+def lm_head_timing(torch, N, dev, reps=20):
+    """Final norm + LM head + argmax at the 2B shape (32 rows, hidden 2560,
+    vocab 128256; a random bf16 head of 656 MB in the kernel's layout).  The
+    head kernel alone and norm + head are each timed as a graph of `reps`
+    calls bracketed by HIP events on the launch stream."""
+    from bitnet_tt.lm_head import LMHead
+
+    M, H_, V = 32, 2560, 128256
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(31)
+    head = LMHead(H_, V, dev, eps=1e-5)
+    w = (torch.randn((V, H_), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    g = (1.0 + 0.1 * torch.randn(H_, generator=gen, device=dev))
+    head.load_final_weights(g, w)
+    del w
+    x = torch.randn((M, H_), generator=gen, device=dev).to(torch.bfloat16)
+    xn = torch.empty((M, H_), dtype=torch.bfloat16, device=dev)
+    logits = torch.empty((M, V), dtype=torch.float32, device=dev)
+    tokens = torch.empty(M, dtype=torch.int32, device=dev)
+    L = N.lib()
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        head(x, normed_out=xn, logits_out=logits, tokens_out=tokens)  # eager: workspace exists before capture
+    torch.cuda.synchronize()
+    ws = N.workspace(dev, int(L.btl_lm_head_workspace_bytes()), kind="lm_head")
+
+    def kernel_only(rows=M):
+        N.check(L.btl_lm_head(N.ptr(xn), rows, H_, V, N.ptr(head.weight), N.ptr(logits), N.ptr(tokens), N.ptr(ws),
+                              ws.numel(), N.stream_of(dev)), "btl_lm_head")
+
+    res = {}
+    for name, fn in (("kernel", kernel_only), ("kernel_row0", lambda: kernel_only(1)),
+                     ("norm_and_head", lambda: head(x, normed_out=xn, logits_out=logits, tokens_out=tokens))):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=s):
+            for _ in range(reps):
+                fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        times = []
+        with torch.cuda.stream(s):
+            gr.replay()
+            for _ in range(3):
+                e0.record(s)
+                gr.replay()
+                e1.record(s)
+                e1.synchronize()
+                times.append(e0.elapsed_time(e1) * 1e3 / reps)
+        res[name] = sorted(times)[1]
+        del gr
+    torch.cuda.synchronize()
+    wbytes = 2 * V * H_
+    nbytes = wbytes + 2 * M * H_ + 4 * M * V + 4 * M  # head + normed rows + fp32 logits + tokens
+    us = res["kernel"]
+    return {
+        "workload": "final RMSNorm + LM head 2560 -> 128256 (bf16 weights) + argmax, 32 rows",
+        "us_kernel": round(us, 2),
+        "us_norm_and_head": round(res["norm_and_head"], 2),
+        "us_kernel_one_row": round(res["kernel_row0"], 2),
+        "bytes_per_launch": nbytes,
+        "achieved_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+        "roofline_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+    }
+
+
 # ------------------------------------------------------------ CPU baseline ----
 def cpu_baseline(step, torch, seconds):
     """Scalar C oracle (one thread) on a bounded sample of the same workload:
@@ -391,6 +458,14 @@ def main():
             log(f"[bench] prefill M={p['M']} K={p['K']} N={p['N']}: {p['us']} us, {p['tops']} TOPS, "
                 f"MFMA-i8 {100 * p['mfma_i8_util']:.1f}%")
 
+    head = None
+    if not args.no_lm_head:
+        head = lm_head_timing(torch, N, dev)
+        log(f"[bench] LM head (32 x 2560 -> 128256 + argmax): {head['us_kernel']} us kernel, "
+            f"{head['us_norm_and_head']} us with the final norm, {head['us_kernel_one_row']} us for one row; "
+            f"{head['achieved_GBps']} GB/s, "
+            f"{100 * head['roofline_frac']:.1f} % of HBM")
+
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle) ...")
@@ -425,6 +500,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "prefill_mfma": prefill,
+        "lm_head": head,
     }
     print(json.dumps(line), flush=True)
 

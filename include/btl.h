@@ -214,6 +214,30 @@ int btl_decode_layer(int64_t M, int64_t H, int64_t Q, int64_t F, int64_t NQKV, c
                      uint16_t* ffn_h, uint16_t* qkv_out, void* workspace, size_t workspace_bytes,
                      btl_stream_t stream);
 
+/* ---- LM head (final norm is btl_rmsnorm) ------------------------------
+ * Replaces the head matmul of src/bitnet_tt/inference/generator_batch32.py:
+ * 768-811 (ttnn.matmul of the normed hidden state with the head weight that
+ * src/bitnet_tt/model/bitnet.py:139-215 loads) and its argmax (:1170-1174,
+ * ttnn.argmax over the vocabulary).
+ *
+ * btl_lm_head_weight_bytes: bytes of the head in the device layout (16 vocab
+ *   rows x 32 k per KiB in MFMA operand order, K padded to a multiple of 256;
+ *   0 for unsupported shapes: K % 16 != 0 or K > 3072).
+ * btl_lm_head_repack: W [V,K] bf16 row-major (the HF / reference (vocab,
+ *   hidden) matrix) -> the device layout.
+ * btl_lm_head_workspace_bytes: workspace of btl_lm_head.  Its first 384
+ *   bytes (argmax keys and a done counter) must be zero before the first call
+ *   and every completed call leaves them zero; the rest is scratch. */
+int64_t btl_lm_head_weight_bytes(int64_t V, int64_t K);
+int64_t btl_lm_head_workspace_bytes(void);
+int btl_lm_head_repack(const uint16_t* w, int64_t V, int64_t K, uint16_t* wdev, btl_stream_t stream);
+
+/* logits[M,V] fp32 = xn[M,K] (bf16, the normalised rows) @ W^T, accumulated
+ * in fp32 (MFMA bf16); tokens[M] int32 = the first index of each row's
+ * largest logit (NaNs ignored).  M <= 32.  logits may be NULL. */
+int btl_lm_head(const uint16_t* xn, int64_t M, int64_t K, int64_t V, const uint16_t* wdev, float* logits,
+                int32_t* tokens, void* workspace, size_t workspace_bytes, btl_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -343,3 +343,21 @@ def permute_halfsplit_to_adjacent(weight_t: np.ndarray, num_heads: int, head_dim
             out[:, h * head_dim + 2 * kk] = weight_t[:, h * head_dim + kk]
             out[:, h * head_dim + 2 * kk + 1] = weight_t[:, h * head_dim + kk + half]
     return out
+
+
+# --------------------------------------------------------------- LM head ----
+def lm_head(xn_bf16: np.ndarray, w_bf16: np.ndarray):
+    """src/bitnet_tt/inference/generator_batch32.py:768-811 -- logits of the
+    normalised rows against the (vocab, hidden) head (model/bitnet.py:139-215)
+    in float64 (bf16 x bf16 products are exact there), with the bound on the
+    rounding of an fp32 accumulation of the same K products: 2 K 2^-24 sum|x w|."""
+    x = bf16_to_f32(np.asarray(xn_bf16, dtype=np.uint16)).astype(np.float64)
+    w = bf16_to_f32(np.asarray(w_bf16, dtype=np.uint16)).astype(np.float64)
+    k = x.shape[-1]
+    return x @ w.T, (2.0 * k * 2.0 ** -24) * (np.abs(x) @ np.abs(w).T)
+
+
+def argmax_first(logits: np.ndarray) -> np.ndarray:
+    """generator_batch32.py:1170-1174 -- greedy token: the first index of each
+    row's largest logit (the tie rule of torch/ttnn argmax)."""
+    return np.argmax(np.asarray(logits), axis=-1)

@@ -186,3 +186,28 @@ def test_decode_layer_sizes_and_argument_checks(L):
     assert call(o=None) == 1
     assert "o_proj" in N.last_error()
 
+
+
+def test_lm_head_sizes_and_argument_checks(L):
+    # 16 vocab rows x 32 k per KiB, K padded to the supported multiple of 256
+    assert L.btl_lm_head_weight_bytes(128256, 2560) == 128256 * 2560 * 2
+    assert L.btl_lm_head_weight_bytes(37, 272) == 3 * 16 * 512 * 2  # 3 tiles, K 272 -> 512
+    assert L.btl_lm_head_weight_bytes(1000, 100) == 0  # K % 16
+    assert L.btl_lm_head_weight_bytes(1000, 4096) == 0  # K > 3072
+    assert L.btl_lm_head_workspace_bytes() == 512
+    SHAPE, NULL, ALIGN, WS = 2, 1, 3, 4
+
+    def call(M=32, K=2560, V=128256, xn=FAKE, w=FAKE, logits=FAKE, tok=FAKE, ws=FAKE, nbytes=512):
+        return L.btl_lm_head(xn, M, K, V, w, logits, tok, ws, nbytes, None)
+
+    assert call(M=0) == SHAPE
+    assert call(M=33) == SHAPE
+    assert call(K=100) == SHAPE
+    assert call(V=0) == SHAPE
+    assert call(xn=None) == NULL
+    assert call(tok=None) == NULL
+    assert call(ws=None) == NULL
+    assert call(xn=FAKE + 4) == ALIGN
+    assert call(nbytes=100) == WS
+    assert L.btl_lm_head_repack(None, 100, 256, FAKE, None) == NULL
+    assert L.btl_lm_head_repack(FAKE, 100, 250, FAKE, None) == SHAPE
