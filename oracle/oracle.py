@@ -16,7 +16,10 @@ Reference semantics restated here (paths relative to the bitnet-tt root):
 * ``src/bitnet_tt/layers/ffn.py:129-183`` -- gate||up, relu(g)^2*u, ffn_sub_norm,
   down; ``ffn.py:22-34`` and ``layers/attention.py:462-506`` -- fused builders;
 * ``src/bitnet_tt/inference/generator_batch32.py:713-761`` -- per-layer order of
-  the decode step (fused RMSNorm->QKV, o_proj, residual, norm, FFN, residual).
+  the decode step (fused RMSNorm->QKV, o_proj, residual, norm, FFN, residual);
+  ``:768-811`` and ``:1170-1174`` -- final norm, LM head and greedy argmax
+  (float64 matmul, a library routine, with the fp32 rounding bound; the first
+  index wins ties, as numpy's and torch's argmax do).
 
 Which check pins each function is listed in ``btl_oracle.c``'s header.
 """

@@ -377,3 +377,20 @@ def test_devlayout_is_the_mfma_operand_order(orc):
     d2 = orc.devlayout_encode(w2)
     lane, q = 0, 3  # rows 96..111: padding
     assert int(d2[0, 0, lane * 4 + q]) == 0x55555555
+
+
+def test_lm_head_oracle_closed_forms(orc):
+    """Head rows that are unit vectors pick single columns of the normalised
+    rows (W = I gives the rows themselves); a tie takes the first index; the
+    bound scales with sum|x w| and vanishes for exact products."""
+    rng = np.random.default_rng(4)
+    x = orc.f32_to_bf16(rng.standard_normal((3, 64)).astype(np.float32))
+    eye = orc.f32_to_bf16(np.eye(64, dtype=np.float32))
+    logits, bound = orc.lm_head(x, eye)
+    assert np.array_equal(logits, orc.bf16_to_f32(x).astype(np.float64))
+    assert np.allclose(bound, 2 * 64 * 2.0 ** -24 * np.abs(orc.bf16_to_f32(x)))
+    w = orc.f32_to_bf16(np.stack([np.zeros(64), np.ones(64), np.ones(64), -np.ones(64)]).astype(np.float32))
+    ones = orc.f32_to_bf16(np.ones((1, 64), dtype=np.float32))
+    lg, _ = orc.lm_head(ones, w)
+    assert lg.tolist() == [[0.0, 64.0, 64.0, -64.0]]
+    assert orc.argmax_first(lg).tolist() == [1]  # tie between 1 and 2: the first
