@@ -50,6 +50,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-lm-head", action="store_true")
+    ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="approximate CPU-baseline sample length")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="run only the workload of the rocprofv3 --pmc traffic runs and exit")
@@ -228,6 +229,65 @@ def prefill_mfma(torch, N, dev):
         out.append({"M": M, "K": K, "N": Nf, "us": round(us, 2), "tops": round(tops, 1),
                     "mfma_i8_util": round(tops / MFMA_I8_PEAK_TOPS, 4)})
     return out
+
+
+# ------------------------------------------------------------ full step ----
+def full_step_timing(step, torch, s, args, ctx=512):
+    """The 30-layer step with the decode attention in place (150 launches,
+    one graph), and the attention launches alone (a graph of one per layer,
+    bracketed by HIP events on the launch stream)."""
+    step.alloc_attention(max_seq_len=ctx)
+    with torch.cuda.stream(s):
+        step.reset_hidden()
+        step.step_full()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step.step_full()
+    with torch.cuda.stream(s):
+        for _ in range(max(args.warmup, 1)):
+            g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with torch.cuda.stream(s):
+        for _ in range(args.steps):
+            g.replay()
+    torch.cuda.synchronize()
+    us_full = (time.perf_counter() - t0) * 1e6 / args.steps
+    del g
+    n = len(step.layers)
+    ga = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(ga, stream=s):
+        for i in range(n):
+            step.attention(step.qkv_out, step.kv[i], step.pos, out=step.attn_out)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    with torch.cuda.stream(s):
+        ga.replay()
+        for _ in range(3):
+            e0.record(s)
+            ga.replay()
+            e1.record(s)
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3 / n)
+    del ga
+    torch.cuda.synchronize()
+    c = step.config
+    B, Hkv, D, H_ = step.batch, c.num_kv_heads, c.head_dim, c.num_attention_heads
+    # compulsory bytes: cached K and V rows [0, pos], the qkv rows, the new cache rows, the output
+    nbytes = 2 * B * Hkv * ctx * D * 2 + B * c.qkv_dim * 2 + 2 * B * Hkv * D * 2 + B * H_ * D * 2
+    us_att = sorted(times)[1]
+    for kv in step.kv:  # release the caches (1.3 GB)
+        del kv.key_cache, kv.value_cache
+    step.kv = None
+    return {
+        "workload": f"30 layers x (QKV, decode attention over context {ctx}, o_proj, gate||up, down), batch 32",
+        "us_per_step": round(us_full, 1),
+        "attention_us_per_layer": round(us_att, 2),
+        "attention_bytes_per_launch": nbytes,
+        "attention_GBps": round(nbytes / (us_att * 1e-6) / 1e9, 1),
+        "attention_roofline_frac": round(nbytes / (us_att * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+    }
 
 
 # ------------------------------------------------------------------ LM head ----
@@ -424,6 +484,15 @@ def main():
     del graph_l
     log(f"[bench] persistent per-layer launches: {us_layers:.1f} us per step")
 
+    # the whole step: decode attention (context 512, every user at the last
+    # position) between each layer's QKV and o_proj
+    full = None
+    if not args.no_attention:
+        full = full_step_timing(step, torch, s, args)
+        log(f"[bench] full step with decode attention (context 512): {full['us_per_step']:.1f} us; attention "
+            f"{full['attention_us_per_layer']:.2f} us per layer, {full['attention_GBps']:.0f} GB/s, "
+            f"{100 * full['attention_roofline_frac']:.1f} % of HBM")
+
     kt = kernel_event_timing(step, torch, args.kernel_reps)
     for name, r in kt.items():
         log(f"[bench] {name}: {r['us_per_launch_median']:.2f} us per launch (median of {args.kernel_reps})")
@@ -501,6 +570,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill_mfma": prefill,
         "lm_head": head,
+        "full_step": full,
     }
     print(json.dumps(line), flush=True)
 

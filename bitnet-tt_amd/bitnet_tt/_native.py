@@ -101,6 +101,9 @@ EXPORTS = {
     "btl_lm_head_workspace_bytes": ([], _I64),
     "btl_lm_head_repack": ([_P, _I64, _I64, _P, _P], _I),
     "btl_lm_head": ([_P, _I64, _I64, _I64, _P, _P, _P, _P, _SZ, _P], _I),
+    "btl_decode_attention_workspace_bytes": ([_I64, _I64, _I64, _I64], _I64),
+    "btl_decode_attention_error_offset": ([_I64, _I64], _I64),
+    "btl_decode_attention": ([_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I, _F, _P, _P, _P, _P, _SZ, _P], _I),
     "btl_decode_layer": (
         [_I64, _I64, _I64, _I64, _I64, _LWP, _LWP, _LWP, _LWP, _F, _P, _P, _P, _P, _P, _SZ, _P],
         _I,

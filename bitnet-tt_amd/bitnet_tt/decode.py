@@ -22,8 +22,11 @@ epilogues.  Two launch structures compute the same bits:
   per-call chain: the in-kernel hand-offs cost about what kernel boundaries
   cost, so the default stays with the per-call launches.
 
-The attention core (RoPE, KV cache, SDPA) is outside this package: the step
-takes its output as an input buffer.
+``step`` takes the attention output as an input buffer (the BitLinear
+portion alone).  After ``alloc_attention`` the step can also run whole:
+``step_full`` puts the decode attention (RoPE, KV-cache update, SDPA over the
+cached context, one ``btl_decode_attention`` launch per layer) between each
+layer's QKV and o_proj (150 launches per 30-layer step).
 
 All buffers are allocated once, so :meth:`BitLinearDecodeStep.step` is
 allocation-free and can be captured in a HIP graph.
@@ -248,6 +251,50 @@ class BitLinearDecodeStep:
 
     def reset_hidden(self):
         self.hidden.copy_(self.hidden0)
+
+    def alloc_attention(self, max_seq_len: int = 512, pos: int | None = None, seed: int = 3,
+                        use_fused_rope: bool = False):
+        """Decode attention for ``step_full``: one KV cache per layer
+        [batch, kv_heads, max_seq_len, head_dim] bf16 holding an earlier
+        context ~N(0, 1), every user at position ``pos`` (default: the last,
+        so each step attends over the whole context).  The step's Q/K weights
+        are unpermuted, so RoPE pairs (i, i + D/2) unless ``use_fused_rope``."""
+        import torch
+
+        from .layers.attention import DecodeAttention
+
+        c = self.config
+        self.attention = DecodeAttention(c.num_attention_heads, c.num_kv_heads, c.head_dim, max_seq_len, self.device,
+                                         rope_theta=c.rope_theta, use_fused_rope=use_fused_rope)
+        gen = torch.Generator(device=self.device)
+        gen.manual_seed(seed)
+        self.kv = []
+        for _ in self.layers:
+            kv = self.attention.new_cache(self.batch)
+            kv.key_cache.normal_(generator=gen)
+            kv.value_cache.normal_(generator=gen)
+            self.kv.append(kv)
+        self.pos = torch.full((self.batch,), max_seq_len - 1 if pos is None else pos, dtype=torch.int32,
+                              device=self.device)
+        return self
+
+    def layer_full(self, i: int):
+        """Layer i with the decode attention between QKV and o_proj."""
+        w = self.layers[i]
+        eps = self.eps
+        ternary_matmul_into(self.hidden, w.qkv, self.qkv_out, norm_weight=w.input_layernorm, norm_epsilon=eps)
+        self.attention(self.qkv_out, self.kv[i], self.pos, out=self.attn_out)
+        ternary_matmul_into(self.attn_out, w.o_proj, self.hidden, norm_weight=w.attn_sub_norm, norm_epsilon=eps,
+                            residual=self.hidden)
+        ternary_matmul_into(self.hidden, w.gate_up, self.ffn_h, norm_weight=w.post_attention_layernorm,
+                            norm_epsilon=eps, epilogue="relu2_mul")
+        ternary_matmul_into(self.ffn_h, w.down, self.hidden, norm_weight=w.ffn_sub_norm, norm_epsilon=eps,
+                            residual=self.hidden)
+
+    def step_full(self):
+        for i in range(len(self.layers)):
+            self.layer_full(i)
+        return self.hidden
 
     # -- the step ----------------------------------------------------------
     def layer(self, i: int, hidden, attn_out, qkv_out, ffn_h):

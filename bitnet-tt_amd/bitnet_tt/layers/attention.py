@@ -2,7 +2,9 @@
 prologue, and the o_proj projection (API pieces of bitnet-tt's
 ``src/bitnet_tt/layers/attention.py``).
 
-The attention core (RoPE, KV cache, SDPA) is not part of this package.
+``DecodeAttention`` is the decode attention between the QKV projection and
+o_proj (attention.py:1040-1262): RoPE, KV-cache update and SDPA over the
+cached positions, one gfx950 launch per layer.
 
 Fused QKV: q, k and v are quantised separately (three absmean scales), the
 Q and K column blocks are optionally permuted from HF half-split to
@@ -84,3 +86,97 @@ class QKVProjection:
     def __call__(self, hidden, norm_weight=None, norm_epsilon: float | None = None):
         """bf16 [..., hidden] -> bf16 [..., q+k+v]."""
         return self.qkv(hidden, norm_weight=norm_weight, norm_epsilon=norm_epsilon)
+
+
+class KVCache:
+    """Pre-allocated per-layer cache (attention.py KVCache): key_cache and
+    value_cache [batch, kv_heads, max_seq_len, head_dim] bf16."""
+
+    def __init__(self, batch: int, num_kv_heads: int, max_seq_len: int, head_dim: int, device) -> None:
+        import torch
+
+        shape = (batch, num_kv_heads, max_seq_len, head_dim)
+        self.key_cache = torch.zeros(shape, dtype=torch.bfloat16, device=device)
+        self.value_cache = torch.zeros(shape, dtype=torch.bfloat16, device=device)
+        self.seq_len_cached = 0
+
+
+class DecodeAttention:
+    """Decode attention of one layer (attention.py:1040-1262):
+
+    q, k, v = split(qkv); q, k = RoPE(q, k; pos); cache[pos] = k, v;
+    out = concat_h softmax(scale * q_h K^T) V over positions [0, pos]
+
+    ``use_fused_rope`` selects the reference's adjacent-pair RoPE (for Q/K
+    weights permuted as ``build_fused_qkv_weight(permute_for_rope=True)``
+    does); otherwise HF's half-split RoPE on unpermuted weights.  ``scale``
+    defaults to 1/sqrt(head_dim); with the QKV scales folded out of the
+    projection it is that times q_scale * k_scale (attention.py:817-839)."""
+
+    def __init__(self, num_heads: int, num_kv_heads: int, head_dim: int, max_seq_len: int, device=None,
+                 rope_theta: float = 500000.0, use_fused_rope: bool = False, scale: float | None = None) -> None:
+        import math
+
+        import torch
+
+        from ..utils.rope import rope_tables
+
+        if head_dim != 128 or num_heads % num_kv_heads or num_heads // num_kv_heads > 4:
+            raise ValueError("the decode-attention kernel takes head_dim 128 and up to 4 query heads per KV head")
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.max_seq_len = max_seq_len
+        self.device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        self.use_fused_rope = use_fused_rope
+        self.scale = 1.0 / math.sqrt(head_dim) if scale is None else float(scale)
+        cos, sin = rope_tables(head_dim, max_seq_len, rope_theta)
+        self.rope_cos = torch.from_numpy(cos).to(self.device)
+        self.rope_sin = torch.from_numpy(sin).to(self.device)
+
+    def new_cache(self, batch: int) -> KVCache:
+        return KVCache(batch, self.num_kv_heads, self.max_seq_len, self.head_dim, self.device)
+
+    def __call__(self, qkv, kv_cache: KVCache, pos, out=None):
+        """qkv bf16 [B, (H + 2 Hkv) D]; pos int32 [B] on the device (each user's
+        new position; a device tensor so a captured graph can advance it);
+        returns bf16 [B, H D] (written into ``out`` when given)."""
+        import torch
+
+        from .. import _native as N
+
+        B = qkv.shape[0]
+        H, Hkv, D, S = self.num_heads, self.num_kv_heads, self.head_dim, self.max_seq_len
+        N.require_cuda(qkv, "qkv")
+        N.require_cuda(pos, "pos")
+        if qkv.dtype != torch.bfloat16 or tuple(qkv.shape) != (B, (H + 2 * Hkv) * D):
+            raise ValueError(f"qkv must be bf16 [B, {(H + 2 * Hkv) * D}]")
+        if pos.dtype != torch.int32 or pos.numel() != B:
+            raise ValueError("pos must be int32 [B]")
+        if tuple(kv_cache.key_cache.shape) != (B, Hkv, S, D):
+            raise ValueError("cache shape does not match")
+        if out is None:
+            out = torch.empty((B, H * D), dtype=torch.bfloat16, device=qkv.device)
+        L = N.lib()
+        nbytes = int(L.btl_decode_attention_workspace_bytes(B, H, Hkv, S))
+        if torch.cuda.is_current_stream_capturing() and not N.has_workspace(qkv.device, nbytes, "attention"):
+            raise RuntimeError("run one eager attention call on this stream before capturing it in a graph")
+        ws = N.workspace(qkv.device, nbytes, kind="attention")
+        N.check(
+            L.btl_decode_attention(N.ptr(qkv), B, H, Hkv, D, S, N.ptr(pos), N.ptr(self.rope_cos), N.ptr(self.rope_sin),
+                                   int(self.use_fused_rope), float(self.scale), N.ptr(kv_cache.key_cache),
+                                   N.ptr(kv_cache.value_cache), N.ptr(out), N.ptr(ws), ws.numel(),
+                                   N.stream_of(qkv.device)),
+            "btl_decode_attention",
+        )
+        return out
+
+    def error_word(self, device=None, B: int = 32) -> int:
+        """Non-zero once a position outside [0, max_seq_len) reached a call on
+        the current stream."""
+        from .. import _native as N
+
+        L = N.lib()
+        ws = N.workspace(self.device if device is None else device, 0, kind="attention")
+        off = int(L.btl_decode_attention_error_offset(B, self.num_kv_heads))
+        return int(ws[off:off + 4].view(__import__("torch").int32).item())

@@ -238,6 +238,31 @@ int btl_lm_head_repack(const uint16_t* w, int64_t V, int64_t K, uint16_t* wdev, 
 int btl_lm_head(const uint16_t* xn, int64_t M, int64_t K, int64_t V, const uint16_t* wdev, float* logits,
                 int32_t* tokens, void* workspace, size_t workspace_bytes, btl_stream_t stream);
 
+/* ---- decode attention between QKV and o_proj --------------------------
+ * Replaces the decode attention of src/bitnet_tt/layers/attention.py:
+ * 1040-1262 (nlp_create_qkv_heads_decode, rotary_embedding_llama,
+ * paged_update_cache, scaled_dot_product_attention_decode,
+ * nlp_concat_heads_decode), called from generator_batch32.py:739-746.
+ *
+ * qkv [B, (H + 2 Hkv) D] bf16 (the fused QKV output: Q heads, K heads, V
+ * heads), pos [B] int32 on the device (each user's new position), rope_cos /
+ * rope_sin [S, D/2] fp32 = cos / sin of position x theta^(-2i/D)
+ * (utils/rope.py:7-23), k_cache / v_cache [B, Hkv, S, D] bf16.  RoPE pairs
+ * (2i, 2i+1) when rope_adjacent (Q/K weights permuted as attention.py:
+ * 462-478 does) else (i, i + D/2).  Writes the rotated k row and the v row
+ * at pos into the caches, then out [B, H D] bf16 = softmax(scale q k^T) v over
+ * positions [0, pos], query head h reading key-value head h / (H / Hkv).
+ * D = 128, H / Hkv <= 4.  The workspace's counters must be zero before the
+ * first call (completed calls leave them zero); the int32 at
+ * btl_decode_attention_error_offset becomes non-zero when a position is
+ * outside [0, S) (that row's output is then zero). */
+int64_t btl_decode_attention_workspace_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t S);
+int64_t btl_decode_attention_error_offset(int64_t B, int64_t Hkv);
+int btl_decode_attention(const uint16_t* qkv, int64_t B, int64_t H, int64_t Hkv, int64_t D, int64_t S,
+                         const int32_t* pos, const float* rope_cos, const float* rope_sin, int rope_adjacent,
+                         float scale, uint16_t* k_cache, uint16_t* v_cache, uint16_t* out, void* workspace,
+                         size_t workspace_bytes, btl_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -364,3 +364,58 @@ def argmax_first(logits: np.ndarray) -> np.ndarray:
     """generator_batch32.py:1170-1174 -- greedy token: the first index of each
     row's largest logit (the tie rule of torch/ttnn argmax)."""
     return np.argmax(np.asarray(logits), axis=-1)
+
+
+# ------------------------------------------------------- decode attention ----
+def rope_tables(dim: int, max_pos: int, theta: float):
+    """utils/rope.py:7-23 -- float32 frequencies 1/theta^(2i/dim), angles
+    position x frequency in float32, cos/sin in float32; [max_pos, dim/2]."""
+    freqs = 1.0 / (theta ** (np.arange(0, dim, 2, dtype=np.float32) / dim))
+    ang = np.outer(np.arange(max_pos, dtype=np.float32), freqs)
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def rope_rotate(x: np.ndarray, c: np.ndarray, s: np.ndarray, adjacent: bool) -> np.ndarray:
+    """attention.py:1325-1350 -- rotation of every pair of the last axis by its
+    frequency's angle: pairs (2i, 2i+1) (adjacent-pair RoPE of permuted Q/K
+    weights) or (i, i + D/2) (HF rotate_half); x float64, c/s [D/2]."""
+    d = x.shape[-1]
+    i0 = np.arange(0, d, 2) if adjacent else np.arange(d // 2)
+    i1 = i0 + 1 if adjacent else i0 + d // 2
+    y = np.empty_like(x)
+    y[..., i0] = x[..., i0] * c - x[..., i1] * s
+    y[..., i1] = x[..., i1] * c + x[..., i0] * s
+    return y
+
+
+def decode_attention(qkv_bf16, kc_bf16, vc_bf16, pos, H, Hkv, cos, sin, adjacent, scale):
+    """attention.py:1040-1262 -- split qkv into heads, RoPE q and k at each
+    user's position, write k and v at that position of copies of the caches,
+    then softmax(scale q k^T) v over positions [0, pos] per query head (head h
+    reads key-value head h // (H / Hkv)).  Rotated q and k are rounded to bf16
+    (the operands the caches and the score products hold); everything else is
+    float64.  Returns (out [B, H*D] float64, new k cache bits, new v cache bits)."""
+    qkv = bf16_to_f32(np.asarray(qkv_bf16, dtype=np.uint16)).astype(np.float64)
+    B = qkv.shape[0]
+    D = kc_bf16.shape[-1]
+    G = H // Hkv
+    kc = np.array(kc_bf16, dtype=np.uint16, copy=True)
+    vc = np.array(vc_bf16, dtype=np.uint16, copy=True)
+    out = np.zeros((B, H * D))
+    for b in range(B):
+        p = int(pos[b])
+        c, s = cos[p].astype(np.float64), sin[p].astype(np.float64)
+        q = qkv[b, :H * D].reshape(H, D)
+        k = qkv[b, H * D:(H + Hkv) * D].reshape(Hkv, D)
+        v_bits = np.asarray(qkv_bf16, dtype=np.uint16)[b, (H + Hkv) * D:].reshape(Hkv, D)
+        qr = bf16_to_f32(f32_to_bf16(rope_rotate(q, c, s, adjacent).astype(np.float32))).astype(np.float64)
+        kr_bits = f32_to_bf16(rope_rotate(k, c, s, adjacent).astype(np.float32))
+        kc[b, :, p, :] = kr_bits
+        vc[b, :, p, :] = v_bits
+        K = bf16_to_f32(kc[b, :, : p + 1, :]).astype(np.float64)
+        V = bf16_to_f32(vc[b, :, : p + 1, :]).astype(np.float64)
+        for h in range(H):
+            sc = scale * (K[h // G] @ qr[h])
+            e = np.exp(sc - sc.max())
+            out[b, h * D:(h + 1) * D] = (e / e.sum()) @ V[h // G]
+    return out, kc, vc
