@@ -9,17 +9,20 @@
 // caches [B, Hkv, S, D] bf16 (the reference's KV-cache shape); output
 // [B, H D] bf16 (heads concatenated, o_proj's input).  D = 128.
 //
-// One workgroup per (user, key-value head, chunk of 128 positions): it
-// applies RoPE to the G = H / Hkv query rows of the group; the chunk that
-// holds the user's position also writes the rotated k row and the v row into
-// the caches.  Scores come from v_mfma_f32_16x16x32_bf16 (the G query rows,
-// padded to 16, against 16 cached key rows per MFMA; keys are contiguous
-// along D, the contraction), softmax runs in fp32 in a fixed order, and the
-// probability-weighted sum of value rows runs on the VALU (a wave per query
-// head, lanes over D, value rows read whole).  Chunks meet through a
-// workspace: each writes (max, sum, unnormalised output) per head, and the
-// last chunk of a (user, head group) to finish -- an atomic counter it resets
-// -- combines them in chunk order and writes the output.
+// One workgroup per (user, key-value head) streams the cached context in
+// chunks of 128 positions, each wave taking 32 of them: the wave's K operands
+// and value rows of the next chunk are in flight in registers while the
+// current chunk is processed.  The prologue rotates the G = H / Hkv query
+// rows of the group and the new k row (RoPE), which goes with the v row into
+// the caches before the rows of the last chunk -- the one that holds it -- are
+// read.  Scores come from
+// v_mfma_f32_16x16x32_bf16 (the G query rows, padded to 16, against 16 cached
+// key rows per MFMA; keys are contiguous along D, the contraction).  The
+// softmax is the running (online) form in fp32: every wave derives the same
+// chunk maximum, rescale factor and sum from the chunk's scores in LDS, so
+// the waves' partial outputs share one scale and are summed in a fixed order
+// at the end.  The probability-weighted value rows accumulate on the VALU
+// (lanes over D, value rows read whole).
 #include <hip/hip_runtime.h>
 
 #include "btl.h"
@@ -34,7 +37,6 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kAtD = 128;       // head dimension
 constexpr int kAtChunk = 128;   // positions per workgroup
 constexpr int kAtMaxG = 4;      // query heads per key-value head handled (one wave each)
-constexpr int kAtPart = 2 + kAtD;  // floats per head partial: max, sum, output
 
 struct AttnArgs {
   const uint16_t* qkv;
@@ -45,10 +47,8 @@ struct AttnArgs {
   uint16_t* kc;            // [B, Hkv, S, D]
   uint16_t* vc;            // [B, Hkv, S, D]
   uint16_t* out;           // [B, H * D]
-  float* part;             // [B, Hkv, NS, G, kAtPart]
-  uint32_t* count;         // [B, Hkv] chunks done (zero between calls)
   int32_t* error;          // set when a position is outside [0, S)
-  int B, H, Hkv, G, S, NS;
+  int B, H, Hkv, G, S;
   float scale;
   int adjacent;            // 1: RoPE pairs (2i, 2i+1); 0: (i, i + D/2)
 };
@@ -59,155 +59,243 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, 
   y1 = x1 * c + x0 * s;
 }
 
-__global__ __launch_bounds__(256) void k_decode_attention(AttnArgs p) {
-  __shared__ __attribute__((aligned(16))) uint16_t s_q[16][kAtD];  // MFMA A operand: G rotated query rows, rest 0
-  __shared__ float s_p[kAtMaxG][kAtChunk];                          // scores, then exp(score - max)
-  __shared__ int s_last;
+// Cached rows of one chunk held in registers by a wave (its 32 positions):
+// the K operands of its two 16-position MFMA blocks (4 k-steps each), and its
+// value rows as 16-byte pieces: v[t] = dims 8 (lane & 15) .. + 8 of the row
+// 4 t + (lane >> 4).
+struct AttnChunkRegs {
+  uint4 k[2][kAtD / 32];
+  uint4 v[8];
+};
+
+__global__ __launch_bounds__(256, 1) void k_decode_attention(AttnArgs p) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[16][kAtD];   // MFMA A operand: G rotated query rows, rest 0
+  __shared__ __attribute__((aligned(16))) uint16_t s_new[2][kAtD];  // the new k (rotated) and v rows
+  __shared__ float s_pw[4][kAtMaxG][32];                             // each wave's probabilities of a chunk
+  __shared__ float s_ml[4][kAtMaxG][2];                              // each wave's running max and sum
+  __shared__ float s_o[4][kAtMaxG][kAtD];                            // each wave's unnormalised output
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int sp = blockIdx.x % p.NS;
-  const int hk = (blockIdx.x / p.NS) % p.Hkv;
-  const int b = blockIdx.x / (p.NS * p.Hkv);
+  const int dg = lane & 15, rg = lane >> 4;  // value piece: dims 8 dg .. + 8 of rows rg + 4 t
+  const int hk = blockIdx.x % p.Hkv;
+  const int b = blockIdx.x / p.Hkv;
   const int G = p.G;
   const int pos = p.pos[b];
   const bool pos_ok = pos >= 0 && pos < p.S;
-  const int last_pos = pos_ok ? pos : -1;
-  const int s0 = sp * kAtChunk;
-  const int s1 = min(s0 + kAtChunk, last_pos + 1);  // this chunk covers [s0, s1)
-  if (!pos_ok && tid == 0 && sp == 0) st_coherent(p.error, 1);
-
+  if (!pos_ok && tid == 0 && hk == 0) st_coherent(p.error, 1);
+  const int nold = pos_ok ? pos : 0;             // cached positions [0, nold); the new one is pos
+  const int nch = (nold + kAtChunk - 1) / kAtChunk;
+  const int pc = pos_ok ? pos : 0;
   const uint16_t* qrow = p.qkv + (int64_t)b * p.ldq;
   const int64_t kv_base = ((int64_t)b * p.Hkv + hk) * p.S;  // row index of (b, hk, position 0)
   const int half = kAtD / 2;
 
-  // rotated query rows of the group into LDS; the chunk holding the position
-  // writes the rotated k row and the v row into the caches
-  for (int t = tid; t < 16 * half; t += 256) {
-    const int g = t / half, i = t % half;
-    const int d0 = p.adjacent ? 2 * i : i, d1 = p.adjacent ? 2 * i + 1 : i + half;
-    uint16_t o0 = 0, o1 = 0;
-    if (g < G && pos_ok) {
-      const uint16_t* q = qrow + (hk * G + g) * kAtD;
-      float y0, y1;
-      rope_pair(bf2f(q[d0]), bf2f(q[d1]), p.rcos[pos * half + i], p.rsin[pos * half + i], y0, y1);
-      o0 = f2bf(y0);
-      o1 = f2bf(y1);
-    }
-    s_q[g][d0] = o0;
-    s_q[g][d1] = o1;
-  }
-  const bool owner = pos_ok && pos >= s0 && pos < s0 + kAtChunk;
-  if (owner) {
-    if (tid < half) {
-      const int i = tid;
-      const int d0 = p.adjacent ? 2 * i : i, d1 = p.adjacent ? 2 * i + 1 : i + half;
-      const uint16_t* k = qrow + (p.H + hk) * kAtD;
-      float y0, y1;
-      rope_pair(bf2f(k[d0]), bf2f(k[d1]), p.rcos[pos * half + i], p.rsin[pos * half + i], y0, y1);
-      uint16_t* dst = p.kc + (kv_base + pos) * kAtD;
-      dst[d0] = f2bf(y0);
-      dst[d1] = f2bf(y1);
-    } else if (tid < 2 * half) {
-      const int d = 2 * (tid - half);
-      const uint32_t v = *reinterpret_cast<const uint32_t*>(qrow + (p.H + p.Hkv + hk) * kAtD + d);
-      *reinterpret_cast<uint32_t*>(p.vc + (kv_base + pos) * kAtD + d) = v;
-    }
-    wait_memory();  // the rows are in L2 before this workgroup reads them back
-  }
-  __syncthreads();
-
-  // scores: wave w takes position blocks of 16 from s0 + 16 w, step 64
-  for (int blk = s0 + 16 * wv; blk < s1; blk += 64) {
-    v4f acc = (v4f){0.f, 0.f, 0.f, 0.f};
-    const int prow = blk + (lane & 15);
-    const int prc = prow < s1 ? prow : s1 - 1;  // a valid row; its score is masked below
-    const uint16_t* krow = p.kc + (kv_base + prc) * kAtD + 8 * (lane >> 4);
+  // this wave's rows of chunk c: positions c*128 + 32 wv + [0, 32)
+  auto load_chunk = [&](AttnChunkRegs& r, int c) __attribute__((always_inline)) {
+    const int cc = c < nch ? c : (nch > 0 ? nch - 1 : 0);  // a valid chunk; extra ones are never used
+    const int base = cc * kAtChunk + 32 * wv;
 #pragma unroll
-    for (int ks = 0; ks < kAtD / 32; ++ks) {
-      const uint4 kb = *reinterpret_cast<const uint4*>(krow + 32 * ks);
-      const uint4 qa = *reinterpret_cast<const uint4*>(&s_q[lane & 15][32 * ks + 8 * (lane >> 4)]);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, qa), __builtin_bit_cast(v8bf, kb), acc,
-                                                    0, 0, 0);
-    }
-    // lanes 0..15 hold rows 0..3 (the query heads) at column lane: position blk + lane
-    if (lane < 16) {
+    for (int blk = 0; blk < 2; ++blk) {
+      const int row = min(base + 16 * blk + (lane & 15), p.S - 1);
+      const uint16_t* kr = p.kc + (kv_base + row) * kAtD + 8 * (lane >> 4);
 #pragma unroll
-      for (int g = 0; g < kAtMaxG; ++g)
-        if (g < G) s_p[g][blk + lane - s0] = blk + lane < s1 ? acc[g] * p.scale : -__builtin_inff();
+      for (int ks = 0; ks < kAtD / 32; ++ks) r.k[blk][ks] = *reinterpret_cast<const uint4*>(kr + 32 * ks);
     }
-  }
-  __syncthreads();
-
-  // softmax statistics and the weighted value sum: wave g = query head g
-  const int g = wv;
-  const int n = s1 - s0;  // positions of this chunk (may be <= 0)
-  float m = -__builtin_inff(), l = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  if (g < G && n > 0) {
-    float mx = -__builtin_inff();
-    for (int j = lane; j < n; j += 64) mx = fmaxf(mx, s_p[g][j]);
-    m = wave_xor_max(mx);
-    float sum = 0.0f;
-    for (int j = lane; j < n; j += 64) {
-      const float e = __expf(s_p[g][j] - m);
-      s_p[g][j] = e;
-      sum += e;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int row = min(base + 4 * t + rg, p.S - 1);
+      r.v[t] = *reinterpret_cast<const uint4*>(p.vc + (kv_base + row) * kAtD + 8 * dg);
     }
-    l = wave_xor_sum(sum);
-  }
-  __syncthreads();  // exponentials visible to the whole wave (written by other lanes)
-  if (g < G && n > 0) {
-    const uint16_t* vrow = p.vc + (kv_base + s0) * kAtD + 2 * lane;
-    for (int j = 0; j < n; ++j) {
-      const uint32_t v = *reinterpret_cast<const uint32_t*>(vrow + (int64_t)j * kAtD);
-      const float e = s_p[g][j];
-      o0 += e * bf2f((uint16_t)(v & 0xffffu));
-      o1 += e * bf2f((uint16_t)(v >> 16));
-    }
-  }
-
-  const int64_t bh = (int64_t)b * p.Hkv + hk;
-  auto write_out = [&](int gg, float v0, float v1) {
-    uint16_t* o = p.out + (int64_t)b * p.H * kAtD + (hk * G + gg) * kAtD + 2 * lane;
-    *reinterpret_cast<uint32_t*>(o) = (uint32_t)f2bf(v0) | ((uint32_t)f2bf(v1) << 16);
   };
-  if (p.NS == 1) {
-    if (g < G) {
-      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-      write_out(g, o0 * inv, o1 * inv);
+
+  // the rows of the first two chunks go out first (they never include the
+  // new position), then the small loads of the new q, k, v rows
+  AttnChunkRegs ra, rb;
+  load_chunk(ra, 0);
+  load_chunk(rb, 1);
+  float qx0[4], qx1[4], rc, rs, kx0, kx1;
+  uint32_t vnew;
+  {
+    const int i = tid & (half - 1);
+    const int d0 = p.adjacent ? 2 * i : i, d1 = p.adjacent ? 2 * i + 1 : i + half;
+    rc = p.rcos[pc * half + i];
+    rs = p.rsin[pc * half + i];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int g = min((tid + 256 * u) / half, G - 1);
+      const uint16_t* q = qrow + (hk * G + g) * kAtD;
+      qx0[u] = bf2f(q[d0]);
+      qx1[u] = bf2f(q[d1]);
     }
-    return;
+    const uint16_t* k = qrow + (p.H + hk) * kAtD;
+    kx0 = bf2f(k[d0]);
+    kx1 = bf2f(k[d1]);
+    vnew = *reinterpret_cast<const uint32_t*>(qrow + (p.H + p.Hkv + hk) * kAtD + 2 * i);
   }
-  // publish this chunk's partials; the last chunk of (b, hk) combines
-  if (g < G) {
-    float* pp = p.part + ((bh * p.NS + sp) * G + g) * kAtPart;
-    if (lane == 0) {
-      st_coherent(pp, m);
-      st_coherent(pp + 1, l);
+  // RoPE of the group's query rows (rows >= G stay 0) and of the new k row;
+  // the new rows go to LDS and to the caches (read by later calls)
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = tid + 256 * u, g = t / half, i = t % half;
+    const int d0 = p.adjacent ? 2 * i : i, d1 = p.adjacent ? 2 * i + 1 : i + half;
+    float y0, y1;
+    rope_pair(qx0[u], qx1[u], rc, rs, y0, y1);
+    const bool live = g < G && pos_ok;
+    s_q[g][d0] = live ? f2bf(y0) : (uint16_t)0;
+    s_q[g][d1] = live ? f2bf(y1) : (uint16_t)0;
+  }
+  if (tid < half) {
+    const int i = tid;
+    const int d0 = p.adjacent ? 2 * i : i, d1 = p.adjacent ? 2 * i + 1 : i + half;
+    float y0, y1;
+    rope_pair(kx0, kx1, rc, rs, y0, y1);
+    const uint16_t k0 = f2bf(y0), k1 = f2bf(y1);
+    s_new[0][d0] = k0;
+    s_new[0][d1] = k1;
+    if (pos_ok) {
+      uint16_t* dst = p.kc + (kv_base + pos) * kAtD;
+      dst[d0] = k0;
+      dst[d1] = k1;
     }
-    st_coherent(pp + 2 + 2 * lane, o0);
-    st_coherent(pp + 3 + 2 * lane, o1);
+  } else if (tid < 2 * half) {
+    const int d = 2 * (tid - half);
+    *reinterpret_cast<uint32_t*>(&s_new[1][d]) = vnew;
+    if (pos_ok) *reinterpret_cast<uint32_t*>(p.vc + (kv_base + pos) * kAtD + d) = vnew;
   }
-  wait_memory();
   __syncthreads();
-  if (tid == 0) s_last = atomicAdd(p.count + bh, 1u) + 1u == (uint32_t)p.NS;
-  __syncthreads();
-  if (!s_last) return;
-  if (g < G) {
-    float M = -__builtin_inff();
-    for (int c = 0; c < p.NS; ++c) M = fmaxf(M, ld_coherent(p.part + ((bh * p.NS + c) * G + g) * kAtPart));
-    float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
-    for (int c = 0; c < p.NS; ++c) {
-      const float* pp = p.part + ((bh * p.NS + c) * G + g) * kAtPart;
-      const float mc = ld_coherent(pp);
-      if (mc == -__builtin_inff()) continue;  // an empty chunk
-      const float w = __expf(mc - M);
-      L += w * ld_coherent(pp + 1);
-      O0 += w * ld_coherent(pp + 2 + 2 * lane);
-      O1 += w * ld_coherent(pp + 3 + 2 * lane);
-    }
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    write_out(g, O0 * inv, O1 * inv);
+
+  // each wave: running softmax over its own positions, per head
+  float m[kAtMaxG], l[kAtMaxG], o[kAtMaxG][8];
+#pragma unroll
+  for (int g = 0; g < kAtMaxG; ++g) {
+    m[g] = -__builtin_inff();
+    l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
   }
-  if (tid == 0) st_coherent(p.count + bh, 0u);
+
+  auto process = [&](AttnChunkRegs& r, int c) __attribute__((always_inline)) {
+    const int base = c * kAtChunk + 32 * wv;  // this wave's first position
+    v4f acc[2];
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      acc[blk] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < kAtD / 32; ++ks) {
+        const uint4 qa = *reinterpret_cast<const uint4*>(&s_q[lane & 15][32 * ks + 8 * (lane >> 4)]);
+        acc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, qa),
+                                                           __builtin_bit_cast(v8bf, r.k[blk][ks]), acc[blk], 0, 0, 0);
+      }
+    }
+    // lanes 0..15: head g's scores of positions base + lane (block 0) and
+    // base + 16 + lane (block 1); reduce over those 16 lanes
+#pragma unroll
+    for (int g = 0; g < kAtMaxG; ++g) {
+      const bool ok0 = lane < 16 && base + lane < nold, ok1 = lane < 16 && base + 16 + lane < nold;
+      const float s0 = ok0 ? acc[0][g] * p.scale : -__builtin_inff();
+      const float s1 = ok1 ? acc[1][g] * p.scale : -__builtin_inff();
+      // butterflies within each 16-lane row (DPP), then lane 0's row for all
+      float mx = fmaxf(s0, s1);
+      mx = fmaxf(mx, xor_partner<8>(mx));
+      mx = fmaxf(mx, xor_partner<4>(mx));
+      mx = fmaxf(mx, xor_partner<2>(mx));
+      mx = fmaxf(mx, xor_partner<1>(mx));
+      mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 0));
+      const float mn = fmaxf(m[g], mx);
+      const float alpha = m[g] == -__builtin_inff() ? 0.0f : __expf(m[g] - mn);
+      const float e0 = ok0 ? __expf(s0 - mn) : 0.0f, e1 = ok1 ? __expf(s1 - mn) : 0.0f;
+      float sm = e0 + e1;
+      sm += xor_partner<8>(sm);
+      sm += xor_partner<4>(sm);
+      sm += xor_partner<2>(sm);
+      sm += xor_partner<1>(sm);
+      sm = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sm), 0));
+      l[g] = l[g] * alpha + sm;
+      m[g] = mn;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
+      if (lane < 16) {
+        s_pw[wv][g][lane] = e0;
+        s_pw[wv][g][16 + lane] = e1;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the wave's own LDS writes are read back by other lanes
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      // rows past the context count as zero (whatever the cache holds there)
+      const bool vok = base + 4 * t + rg < nold;
+      const uint32_t w4[4] = {vok ? r.v[t].x : 0u, vok ? r.v[t].y : 0u, vok ? r.v[t].z : 0u, vok ? r.v[t].w : 0u};
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[2 * e] = bf2f((uint16_t)(w4[e] & 0xffffu));
+        v[2 * e + 1] = bf2f((uint16_t)(w4[e] >> 16));
+      }
+#pragma unroll
+      for (int g = 0; g < kAtMaxG; ++g) {
+        const float pe = s_pw[wv][g][4 * t + rg];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] += pe * v[e];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // reads done before the next chunk rewrites s_pw
+  };
+
+  for (int c = 0; c < nch; c += 2) {
+    process(ra, c);
+    load_chunk(ra, c + 2);
+    if (c + 1 < nch) process(rb, c + 1);
+    load_chunk(rb, c + 3);
+  }
+
+  // each wave's partial (row groups summed within the wave) into LDS
+#pragma unroll
+  for (int g = 0; g < kAtMaxG; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float x = o[g][e];
+      x += xor_partner<16>(x);
+      x += xor_partner<32>(x);
+      o[g][e] = x;
+    }
+  if (rg == 0) {
+#pragma unroll
+    for (int g = 0; g < kAtMaxG; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_o[wv][g][8 * dg + e] = o[g][e];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < kAtMaxG; ++g) {
+      s_ml[wv][g][0] = m[g];
+      s_ml[wv][g][1] = l[g];
+    }
+  }
+  __syncthreads();
+
+  // wave g merges head g: the four waves' partials and the new position
+  const int g = wv;
+  if (g < G) {
+    // score of the new position (lanes over D, fixed-order sum)
+    float d = bf2f(s_q[g][2 * lane]) * bf2f(s_new[0][2 * lane]) + bf2f(s_q[g][2 * lane + 1]) * bf2f(s_new[0][2 * lane + 1]);
+    const float snew = wave_xor_sum(d) * p.scale;
+    float M = snew;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][g][0]);
+    const float wn = __expf(snew - M);
+    float L = wn;
+    float O0 = wn * bf2f(s_new[1][2 * lane]), O1 = wn * bf2f(s_new[1][2 * lane + 1]);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float mw = s_ml[w][g][0];
+      const float ww = mw == -__builtin_inff() ? 0.0f : __expf(mw - M);
+      L += ww * s_ml[w][g][1];
+      O0 += ww * s_o[w][g][2 * lane];
+      O1 += ww * s_o[w][g][2 * lane + 1];
+    }
+    const float inv = pos_ok ? 1.0f / L : 0.0f;
+    uint16_t* out = p.out + (int64_t)b * p.H * kAtD + (hk * G + g) * kAtD + 2 * lane;
+    *reinterpret_cast<uint32_t*>(out) = (uint32_t)f2bf(O0 * inv) | ((uint32_t)f2bf(O1 * inv) << 16);
+  }
 }
 
 }  // namespace btl
@@ -218,12 +306,14 @@ extern "C" {
 
 int64_t btl_decode_attention_workspace_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t S) {
   if (B <= 0 || Hkv <= 0 || H <= 0 || H % Hkv || H / Hkv > kAtMaxG || S <= 0) return 0;
-  const int64_t ns = (S + kAtChunk - 1) / kAtChunk;
-  const int64_t counters = round_up(B * Hkv * 4 + 4, 256);  // counters, then the error word
-  return counters + B * Hkv * ns * (H / Hkv) * kAtPart * 4;
+  return 256;  // the error word
 }
 
-int64_t btl_decode_attention_error_offset(int64_t B, int64_t Hkv) { return B * Hkv * 4; }
+int64_t btl_decode_attention_error_offset(int64_t B, int64_t Hkv) {
+  (void)B;
+  (void)Hkv;
+  return 0;
+}
 
 int btl_decode_attention(const uint16_t* qkv, int64_t B, int64_t H, int64_t Hkv, int64_t D, int64_t S,
                          const int32_t* pos, const float* rope_cos, const float* rope_sin, int rope_adjacent,
@@ -257,14 +347,11 @@ int btl_decode_attention(const uint16_t* qkv, int64_t B, int64_t H, int64_t Hkv,
   a.Hkv = (int)Hkv;
   a.G = (int)(H / Hkv);
   a.S = (int)S;
-  a.NS = (int)((S + kAtChunk - 1) / kAtChunk);
   a.scale = scale;
   a.adjacent = rope_adjacent ? 1 : 0;
   char* ws = reinterpret_cast<char*>(workspace);
-  a.count = reinterpret_cast<uint32_t*>(ws);
-  a.error = reinterpret_cast<int32_t*>(ws + btl_decode_attention_error_offset(B, Hkv));
-  a.part = reinterpret_cast<float*>(ws + round_up(B * Hkv * 4 + 4, 256));
-  const dim3 grid((unsigned)(B * Hkv * a.NS));
+  a.error = reinterpret_cast<int32_t*>(ws);
+  const dim3 grid((unsigned)(B * Hkv));
   hipLaunchKernelGGL(k_decode_attention, grid, dim3(256), 0, (hipStream_t)stream, a);
   return check_launch("decode attention");
 }

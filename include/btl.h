@@ -252,10 +252,10 @@ int btl_lm_head(const uint16_t* xn, int64_t M, int64_t K, int64_t V, const uint1
  * 462-478 does) else (i, i + D/2).  Writes the rotated k row and the v row
  * at pos into the caches, then out [B, H D] bf16 = softmax(scale q k^T) v over
  * positions [0, pos], query head h reading key-value head h / (H / Hkv).
- * D = 128, H / Hkv <= 4.  The workspace's counters must be zero before the
- * first call (completed calls leave them zero); the int32 at
- * btl_decode_attention_error_offset becomes non-zero when a position is
- * outside [0, S) (that row's output is then zero). */
+ * D = 128, H / Hkv <= 4.  The workspace holds one int32 at
+ * btl_decode_attention_error_offset (zero-filled before the first call): it
+ * becomes non-zero when a position is outside [0, S) (that user's output is
+ * then zero and its caches are not written). */
 int64_t btl_decode_attention_workspace_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t S);
 int64_t btl_decode_attention_error_offset(int64_t B, int64_t Hkv);
 int btl_decode_attention(const uint16_t* qkv, int64_t B, int64_t H, int64_t Hkv, int64_t D, int64_t S,
