@@ -25,7 +25,7 @@ static void launch_rows(unsigned rows, hipStream_t s, const ActArgs& p) {
 int launch_act(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint16_t* gamma, float norm_eps,
                int8_t* xa, float* a_dq, int32_t* rowsum, float* act_scale, int8_t* xq_rm, uint16_t* y_rm,
                uint32_t* zero_words, int n_zero_words, hipStream_t stream) {
-  ActArgs p;
+  ActArgs p = {};
   p.act_scale = act_scale;
   p.x = x;
   p.ldx = ldx;

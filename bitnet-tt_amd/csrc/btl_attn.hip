@@ -9,34 +9,44 @@
 // caches [B, Hkv, S, D] bf16 (the reference's KV-cache shape); output
 // [B, H D] bf16 (heads concatenated, o_proj's input).  D = 128.
 //
-// One workgroup per (user, key-value head) streams the cached context in
-// chunks of 128 positions, each wave taking 32 of them: the wave's K operands
-// and value rows of the next chunk are in flight in registers while the
-// current chunk is processed.  The prologue rotates the G = H / Hkv query
-// rows of the group and the new k row (RoPE), which goes with the v row into
-// the caches before the rows of the last chunk -- the one that holds it -- are
-// read.  Scores come from
-// v_mfma_f32_16x16x32_bf16 (the G query rows, padded to 16, against 16 cached
-// key rows per MFMA; keys are contiguous along D, the contraction).  The
-// softmax is the running (online) form in fp32: every wave derives the same
-// chunk maximum, rescale factor and sum from the chunk's scores in LDS, so
-// the waves' partial outputs share one scale and are summed in a fixed order
-// at the end.  The probability-weighted value rows accumulate on the VALU
-// (lanes over D, value rows read whole).
+// One workgroup of 8 waves per (user, key-value head); a round covers 512
+// cached positions, 64 per wave, and every wave issues all of its key and
+// value loads (256 B per lane each) before computing, so a round is one
+// memory round trip with 256 KiB in flight per CU (at the 2B shape, context
+// 512, the whole context is one round).  Measured on MI355X, splitting the
+// context over more workgroups (to use all 256 CUs) and merging their
+// partials through the workspace was slower at this shape: the merge's
+// store-acknowledge-count-reload chain costs more than the extra CUs gain.
+//  - Scores: v_mfma_f32_16x16x32_bf16, the G rotated query rows (padded to
+//    16 with zeros) against 16 cached key rows per MFMA (keys contiguous
+//    along D, the contraction, so the B operands load straight from the
+//    cache).
+//  - Softmax: the running (online) form in fp32 per wave and head.
+//  - Probability-weighted values: MFMA as well.  The wave's value rows go
+//    to LDS (rows padded by 8 bytes, so the four position groups of an
+//    operand read fall in different banks) and are read back as B operands
+//    (8 positions of one dimension per lane); the probabilities enter as two
+//    bf16 parts, p = hi + lo, which keeps them to ~16 bits.
+//  - The waves' (max, sum, output) partials and the new position (rotated k,
+//    v) merge in LDS in a fixed order.
 #include <hip/hip_runtime.h>
 
 #include "btl.h"
 #include "btl_act_row.h"
 #include "btl_common.h"
+#include "btl_trace.h"
 
 namespace btl {
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int kAtD = 128;       // head dimension
-constexpr int kAtChunk = 128;   // positions per workgroup
-constexpr int kAtMaxG = 4;      // query heads per key-value head handled (one wave each)
+constexpr int kAtD = 128;                        // head dimension
+constexpr int kAtWaves = 8;                      // waves per workgroup
+constexpr int kAtPosWave = 64;                   // positions per wave and round
+constexpr int kAtRound = kAtWaves * kAtPosWave;  // positions per round
+constexpr int kAtMaxG = 4;                       // query heads per key-value head
+constexpr int kAtVPitch = kAtD + 4;              // bf16 per LDS value row (8-byte pad)
 
 struct AttnArgs {
   const uint16_t* qkv;
@@ -59,248 +69,269 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, 
   y1 = x1 * c + x0 * s;
 }
 
-// Cached rows of one chunk held in registers by a wave (its 32 positions):
-// the K operands of its two 16-position MFMA blocks (4 k-steps each), and its
-// value rows as 16-byte pieces: v[t] = dims 8 (lane & 15) .. + 8 of the row
-// 4 t + (lane >> 4).
-struct AttnChunkRegs {
-  uint4 k[2][kAtD / 32];
-  uint4 v[8];
-};
+// Max and sum over the 16 lanes of a row (lanes 0..15 hold the values).
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, xor_partner<8>(v));
+  v = fmaxf(v, xor_partner<4>(v));
+  v = fmaxf(v, xor_partner<2>(v));
+  v = fmaxf(v, xor_partner<1>(v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v = v + xor_partner<8>(v);
+  v = v + xor_partner<4>(v);
+  v = v + xor_partner<2>(v);
+  v = v + xor_partner<1>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+}
 
-__global__ __launch_bounds__(256, 1) void k_decode_attention(AttnArgs p) {
-  __shared__ __attribute__((aligned(16))) uint16_t s_q[16][kAtD];   // MFMA A operand: G rotated query rows, rest 0
-  __shared__ __attribute__((aligned(16))) uint16_t s_new[2][kAtD];  // the new k (rotated) and v rows
-  __shared__ float s_pw[4][kAtMaxG][32];                             // each wave's probabilities of a chunk
-  __shared__ float s_ml[4][kAtMaxG][2];                              // each wave's running max and sum
-  __shared__ float s_o[4][kAtMaxG][kAtD];                            // each wave's unnormalised output
+__device__ __forceinline__ float wexp(float m, float M) { return m == -__builtin_inff() ? 0.0f : __expf(m - M); }
+
+__global__ __launch_bounds__(64 * kAtWaves, 1) void k_decode_attention(AttnArgs p) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[kAtMaxG][kAtD];   // rotated query rows of the group
+  __shared__ __attribute__((aligned(16))) uint16_t s_new[2][kAtD];       // the new k (rotated) and v rows
+  __shared__ float s_snew[kAtMaxG];                                       // scores of the new position
+  __shared__ __attribute__((aligned(16))) uint16_t s_p[kAtWaves][2][kAtMaxG][kAtPosWave];  // probabilities hi, lo
+  __shared__ float s_ml[kAtWaves][kAtMaxG][2];                            // each wave's running max and sum
+  // value rows of each wave's round; after the last round, each wave's
+  // unnormalised output [G][D] fp32 (the LDS is reused)
+  __shared__ __attribute__((aligned(16))) uint16_t s_v[kAtWaves][kAtPosWave][kAtVPitch];
+  static_assert(sizeof(float) * kAtWaves * kAtMaxG * kAtD <= sizeof(uint16_t) * kAtWaves * kAtPosWave * kAtVPitch,
+                "output partials fit in the value buffer");
+  float (*s_o)[kAtMaxG][kAtD] = reinterpret_cast<float (*)[kAtMaxG][kAtD]>(&s_v[0][0][0]);
+
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int dg = lane & 15, rg = lane >> 4;  // value piece: dims 8 dg .. + 8 of rows rg + 4 t
+  BTL_TRACE_AT(0);
   const int hk = blockIdx.x % p.Hkv;
   const int b = blockIdx.x / p.Hkv;
   const int G = p.G;
   const int pos = p.pos[b];
   const bool pos_ok = pos >= 0 && pos < p.S;
   if (!pos_ok && tid == 0 && hk == 0) st_coherent(p.error, 1);
-  const int nold = pos_ok ? pos : 0;             // cached positions [0, nold); the new one is pos
-  const int nch = (nold + kAtChunk - 1) / kAtChunk;
+  const int nold = pos_ok ? pos : 0;  // cached positions [0, nold); the new one is pos
+  const int nrounds = (nold + kAtRound - 1) / kAtRound;
   const int pc = pos_ok ? pos : 0;
   const uint16_t* qrow = p.qkv + (int64_t)b * p.ldq;
   const int64_t kv_base = ((int64_t)b * p.Hkv + hk) * p.S;  // row index of (b, hk, position 0)
   const int half = kAtD / 2;
+  const int r16 = lane & 15, grp = lane >> 4;
 
-  // this wave's rows of chunk c: positions c*128 + 32 wv + [0, 32)
-  auto load_chunk = [&](AttnChunkRegs& r, int c) __attribute__((always_inline)) {
-    const int cc = c < nch ? c : (nch > 0 ? nch - 1 : 0);  // a valid chunk; extra ones are never used
-    const int base = cc * kAtChunk + 32 * wv;
+  // this wave's rows of round rd: positions rd*512 + 64 wv + [0, 64)
+  uint4 kr[4][kAtD / 32];  // K operands: 4 blocks of 16 positions x 4 k-steps
+  uint4 vr[16];            // value pieces: dims 8 r16 .. + 8 of row 4 t + grp
+  auto load_round = [&](int rd) __attribute__((always_inline)) {
+    const int base = rd * kAtRound + kAtPosWave * wv;
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      const int row = min(base + 16 * blk + (lane & 15), p.S - 1);
-      const uint16_t* kr = p.kc + (kv_base + row) * kAtD + 8 * (lane >> 4);
+    for (int blk = 0; blk < 4; ++blk) {
+      const int row = min(base + 16 * blk + r16, p.S - 1);
+      const uint16_t* kp = p.kc + (kv_base + row) * kAtD + 8 * grp;
 #pragma unroll
-      for (int ks = 0; ks < kAtD / 32; ++ks) r.k[blk][ks] = *reinterpret_cast<const uint4*>(kr + 32 * ks);
+      for (int ks = 0; ks < kAtD / 32; ++ks) kr[blk][ks] = *reinterpret_cast<const uint4*>(kp + 32 * ks);
     }
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int row = min(base + 4 * t + rg, p.S - 1);
-      r.v[t] = *reinterpret_cast<const uint4*>(p.vc + (kv_base + row) * kAtD + 8 * dg);
+    for (int t = 0; t < 16; ++t) {
+      const int row = min(base + 4 * t + grp, p.S - 1);
+      vr[t] = *reinterpret_cast<const uint4*>(p.vc + (kv_base + row) * kAtD + 8 * r16);
     }
   };
+  const bool wave_work = kAtPosWave * wv < nold;  // this wave has cached positions in round 0
+  if (wave_work) load_round(0);
+  BTL_TRACE_AT(1);
 
-  // the rows of the first two chunks go out first (they never include the
-  // new position), then the small loads of the new q, k, v rows
-  AttnChunkRegs ra, rb;
-  load_chunk(ra, 0);
-  load_chunk(rb, 1);
-  float qx0[4], qx1[4], rc, rs, kx0, kx1;
-  uint32_t vnew;
+  // the new q, k, v rows: RoPE of the group's query rows and of the new k
+  // row; the new rows go to LDS and to the caches (read by later calls)
   {
     const int i = tid & (half - 1);
     const int d0 = p.adjacent ? 2 * i : i, d1 = p.adjacent ? 2 * i + 1 : i + half;
-    rc = p.rcos[pc * half + i];
-    rs = p.rsin[pc * half + i];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int g = min((tid + 256 * u) / half, G - 1);
-      const uint16_t* q = qrow + (hk * G + g) * kAtD;
-      qx0[u] = bf2f(q[d0]);
-      qx1[u] = bf2f(q[d1]);
+    const float rc = p.rcos[pc * half + i], rs = p.rsin[pc * half + i];
+    const int u = tid / half;  // 0..7: query rows 0..3, then the k row, then v
+    if (u < kAtMaxG) {
+      float y0 = 0.0f, y1 = 0.0f;
+      if (u < G && pos_ok) {
+        const uint16_t* q = qrow + (hk * G + u) * kAtD;
+        rope_pair(bf2f(q[d0]), bf2f(q[d1]), rc, rs, y0, y1);
+      }
+      s_q[u][d0] = f2bf(y0);
+      s_q[u][d1] = f2bf(y1);
+    } else if (u == kAtMaxG) {
+      const uint16_t* k = qrow + (p.H + hk) * kAtD;
+      float y0, y1;
+      rope_pair(bf2f(k[d0]), bf2f(k[d1]), rc, rs, y0, y1);
+      const uint16_t k0 = f2bf(y0), k1 = f2bf(y1);
+      s_new[0][d0] = k0;
+      s_new[0][d1] = k1;
+      if (pos_ok) {
+        uint16_t* dst = p.kc + (kv_base + pos) * kAtD;
+        dst[d0] = k0;
+        dst[d1] = k1;
+      }
+    } else if (u == kAtMaxG + 1) {
+      const int d = 2 * i;
+      const uint32_t vnew = *reinterpret_cast<const uint32_t*>(qrow + (p.H + p.Hkv + hk) * kAtD + d);
+      *reinterpret_cast<uint32_t*>(&s_new[1][d]) = vnew;
+      if (pos_ok) *reinterpret_cast<uint32_t*>(p.vc + (kv_base + pos) * kAtD + d) = vnew;
     }
-    const uint16_t* k = qrow + (p.H + hk) * kAtD;
-    kx0 = bf2f(k[d0]);
-    kx1 = bf2f(k[d1]);
-    vnew = *reinterpret_cast<const uint32_t*>(qrow + (p.H + p.Hkv + hk) * kAtD + 2 * i);
-  }
-  // RoPE of the group's query rows (rows >= G stay 0) and of the new k row;
-  // the new rows go to LDS and to the caches (read by later calls)
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int t = tid + 256 * u, g = t / half, i = t % half;
-    const int d0 = p.adjacent ? 2 * i : i, d1 = p.adjacent ? 2 * i + 1 : i + half;
-    float y0, y1;
-    rope_pair(qx0[u], qx1[u], rc, rs, y0, y1);
-    const bool live = g < G && pos_ok;
-    s_q[g][d0] = live ? f2bf(y0) : (uint16_t)0;
-    s_q[g][d1] = live ? f2bf(y1) : (uint16_t)0;
-  }
-  if (tid < half) {
-    const int i = tid;
-    const int d0 = p.adjacent ? 2 * i : i, d1 = p.adjacent ? 2 * i + 1 : i + half;
-    float y0, y1;
-    rope_pair(kx0, kx1, rc, rs, y0, y1);
-    const uint16_t k0 = f2bf(y0), k1 = f2bf(y1);
-    s_new[0][d0] = k0;
-    s_new[0][d1] = k1;
-    if (pos_ok) {
-      uint16_t* dst = p.kc + (kv_base + pos) * kAtD;
-      dst[d0] = k0;
-      dst[d1] = k1;
-    }
-  } else if (tid < 2 * half) {
-    const int d = 2 * (tid - half);
-    *reinterpret_cast<uint32_t*>(&s_new[1][d]) = vnew;
-    if (pos_ok) *reinterpret_cast<uint32_t*>(p.vc + (kv_base + pos) * kAtD + d) = vnew;
   }
   __syncthreads();
+  BTL_TRACE_AT(2);
+  if (wv < G) {  // score of the new position for head wv (lanes over D, fixed-order sum)
+    const float d = bf2f(s_q[wv][2 * lane]) * bf2f(s_new[0][2 * lane]) +
+                    bf2f(s_q[wv][2 * lane + 1]) * bf2f(s_new[0][2 * lane + 1]);
+    const float sn = wave_xor_sum(d) * p.scale;
+    if (lane == 0) s_snew[wv] = sn;
+  }
+  // query operands (A: row r16 = head, k-step ks: dims 32 ks + 8 grp ..)
+  v8bf qa[kAtD / 32];
+#pragma unroll
+  for (int ks = 0; ks < kAtD / 32; ++ks) {
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (r16 < G) v = *reinterpret_cast<const uint4*>(&s_q[r16][32 * ks + 8 * grp]);
+    qa[ks] = __builtin_bit_cast(v8bf, v);
+  }
 
-  // each wave: running softmax over its own positions, per head
-  float m[kAtMaxG], l[kAtMaxG], o[kAtMaxG][8];
+  // running softmax state of this wave, per head (lanes 0..15 hold the
+  // output rows: acc o[m][j] = head j, dimension 16 m + r16)
+  float mrun[kAtMaxG], lrun[kAtMaxG];
+  v4f o[kAtD / 16];
 #pragma unroll
   for (int g = 0; g < kAtMaxG; ++g) {
-    m[g] = -__builtin_inff();
-    l[g] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
+    mrun[g] = -__builtin_inff();
+    lrun[g] = 0.0f;
   }
+#pragma unroll
+  for (int m = 0; m < kAtD / 16; ++m) o[m] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  auto process = [&](AttnChunkRegs& r, int c) __attribute__((always_inline)) {
-    const int base = c * kAtChunk + 32 * wv;  // this wave's first position
-    v4f acc[2];
+  for (int rd = 0; rd < nrounds; ++rd) {
+    const int base = rd * kAtRound + kAtPosWave * wv;
+    if (base >= nold) break;  // wave-uniform: nothing cached from here on
+    if (rd > 0) load_round(rd);
+    // scores: 4 blocks of 16 positions
+    v4f sc[4];
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      acc[blk] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int blk = 0; blk < 4; ++blk) {
+      sc[blk] = (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < kAtD / 32; ++ks) {
-        const uint4 qa = *reinterpret_cast<const uint4*>(&s_q[lane & 15][32 * ks + 8 * (lane >> 4)]);
-        acc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, qa),
-                                                           __builtin_bit_cast(v8bf, r.k[blk][ks]), acc[blk], 0, 0, 0);
-      }
+      for (int ks = 0; ks < kAtD / 32; ++ks)
+        sc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], __builtin_bit_cast(v8bf, kr[blk][ks]), sc[blk], 0,
+                                                          0, 0);
     }
-    // lanes 0..15: head g's scores of positions base + lane (block 0) and
-    // base + 16 + lane (block 1); reduce over those 16 lanes
+    // value rows to LDS (rows past the context as zeros, whatever the cache
+    // holds there: a zero probability times a non-finite value is NaN)
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const bool ok = base + 4 * t + grp < nold;
+      const uint4 v = ok ? vr[t] : make_uint4(0u, 0u, 0u, 0u);
+      uint2* dst = reinterpret_cast<uint2*>(&s_v[wv][4 * t + grp][8 * r16]);
+      dst[0] = make_uint2(v.x, v.y);
+      dst[1] = make_uint2(v.z, v.w);
+    }
+    // online softmax per head over the wave's 64 positions (lanes 0..15:
+    // block blk's position 16 blk + lane)
 #pragma unroll
     for (int g = 0; g < kAtMaxG; ++g) {
-      const bool ok0 = lane < 16 && base + lane < nold, ok1 = lane < 16 && base + 16 + lane < nold;
-      const float s0 = ok0 ? acc[0][g] * p.scale : -__builtin_inff();
-      const float s1 = ok1 ? acc[1][g] * p.scale : -__builtin_inff();
-      // butterflies within each 16-lane row (DPP), then lane 0's row for all
-      float mx = fmaxf(s0, s1);
-      mx = fmaxf(mx, xor_partner<8>(mx));
-      mx = fmaxf(mx, xor_partner<4>(mx));
-      mx = fmaxf(mx, xor_partner<2>(mx));
-      mx = fmaxf(mx, xor_partner<1>(mx));
-      mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 0));
-      const float mn = fmaxf(m[g], mx);
-      const float alpha = m[g] == -__builtin_inff() ? 0.0f : __expf(m[g] - mn);
-      const float e0 = ok0 ? __expf(s0 - mn) : 0.0f, e1 = ok1 ? __expf(s1 - mn) : 0.0f;
-      float sm = e0 + e1;
-      sm += xor_partner<8>(sm);
-      sm += xor_partner<4>(sm);
-      sm += xor_partner<2>(sm);
-      sm += xor_partner<1>(sm);
-      sm = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sm), 0));
-      l[g] = l[g] * alpha + sm;
-      m[g] = mn;
+      float s4[4];
+      float mx = -__builtin_inff();
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
-      if (lane < 16) {
-        s_pw[wv][g][lane] = e0;
-        s_pw[wv][g][16 + lane] = e1;
+      for (int blk = 0; blk < 4; ++blk) {
+        const bool ok = lane < 16 && base + 16 * blk + lane < nold;
+        s4[blk] = ok ? sc[blk][g] * p.scale : -__builtin_inff();
+        mx = fmaxf(mx, s4[blk]);
       }
+      mx = row16_max(mx);
+      const float mn = fmaxf(mrun[g], mx);
+      const float alpha = wexp(mrun[g], mn);
+      float sm = 0.0f;
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        const float e = wexp(s4[blk], mn);
+        sm += e;
+        if (lane < 16) {
+          const uint16_t hi = f2bf(e);
+          s_p[wv][0][g][16 * blk + lane] = hi;
+          s_p[wv][1][g][16 * blk + lane] = f2bf(e - bf2f(hi));
+        }
+      }
+      sm = row16_sum(sm);
+      lrun[g] = lrun[g] * alpha + sm;
+      mrun[g] = mn;
+      // rows j of the output accumulators are heads: lanes 0..15 hold them
+#pragma unroll
+      for (int m = 0; m < kAtD / 16; ++m) o[m][g] *= alpha;
     }
+    BTL_TRACE_AT(3);
     __builtin_amdgcn_wave_barrier();  // the wave's own LDS writes are read back by other lanes
+    // probability-weighted values: 2 k-steps of 32 positions x 8 column
+    // blocks of 16 dimensions, probabilities as hi + lo parts
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      // rows past the context count as zero (whatever the cache holds there)
-      const bool vok = base + 4 * t + rg < nold;
-      const uint32_t w4[4] = {vok ? r.v[t].x : 0u, vok ? r.v[t].y : 0u, vok ? r.v[t].z : 0u, vok ? r.v[t].w : 0u};
-      float v[8];
+    for (int k2 = 0; k2 < 2; ++k2) {
+      v8bf pa[2];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[2 * e] = bf2f((uint16_t)(w4[e] & 0xffffu));
-        v[2 * e + 1] = bf2f((uint16_t)(w4[e] >> 16));
+      for (int part = 0; part < 2; ++part) {
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (r16 < G) v = *reinterpret_cast<const uint4*>(&s_p[wv][part][r16][32 * k2 + 8 * grp]);
+        pa[part] = __builtin_bit_cast(v8bf, v);
       }
 #pragma unroll
-      for (int g = 0; g < kAtMaxG; ++g) {
-        const float pe = s_pw[wv][g][4 * t + rg];
+      for (int m = 0; m < kAtD / 16; ++m) {
+        // B operand: dimension 16 m + r16 of positions 32 k2 + 8 grp + [0, 8)
+        const uint16_t* col = &s_v[wv][32 * k2 + 8 * grp][16 * m + r16];
+        uint32_t w[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[g][e] += pe * v[e];
+        for (int e = 0; e < 4; ++e)
+          w[e] = (uint32_t)col[(2 * e) * kAtVPitch] | ((uint32_t)col[(2 * e + 1) * kAtVPitch] << 16);
+        const v8bf vb = __builtin_bit_cast(v8bf, make_uint4(w[0], w[1], w[2], w[3]));
+        o[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vb, o[m], 0, 0, 0);
+        o[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vb, o[m], 0, 0, 0);
       }
     }
-    __builtin_amdgcn_wave_barrier();  // reads done before the next chunk rewrites s_pw
-  };
-
-  for (int c = 0; c < nch; c += 2) {
-    process(ra, c);
-    load_chunk(ra, c + 2);
-    if (c + 1 < nch) process(rb, c + 1);
-    load_chunk(rb, c + 3);
+    __builtin_amdgcn_wave_barrier();  // reads done before the next round rewrites the buffers
   }
+  BTL_TRACE_AT(4);
 
-  // each wave's partial (row groups summed within the wave) into LDS
-#pragma unroll
-  for (int g = 0; g < kAtMaxG; ++g)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float x = o[g][e];
-      x += xor_partner<16>(x);
-      x += xor_partner<32>(x);
-      o[g][e] = x;
-    }
-  if (rg == 0) {
-#pragma unroll
-    for (int g = 0; g < kAtMaxG; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s_o[wv][g][8 * dg + e] = o[g][e];
-  }
+  // merge: every wave's partial, then the new position, in a fixed order
   if (lane == 0) {
 #pragma unroll
     for (int g = 0; g < kAtMaxG; ++g) {
-      s_ml[wv][g][0] = m[g];
-      s_ml[wv][g][1] = l[g];
+      s_ml[wv][g][0] = mrun[g];
+      s_ml[wv][g][1] = lrun[g];
     }
+  }
+  __syncthreads();  // every wave is done with its value rows: s_o reuses them
+  if (lane < 16) {
+#pragma unroll
+    for (int m = 0; m < kAtD / 16; ++m)
+#pragma unroll
+      for (int g = 0; g < kAtMaxG; ++g) s_o[wv][g][16 * m + lane] = o[m][g];
   }
   __syncthreads();
-
-  // wave g merges head g: the four waves' partials and the new position
-  const int g = wv;
-  if (g < G) {
-    // score of the new position (lanes over D, fixed-order sum)
-    float d = bf2f(s_q[g][2 * lane]) * bf2f(s_new[0][2 * lane]) + bf2f(s_q[g][2 * lane + 1]) * bf2f(s_new[0][2 * lane + 1]);
-    const float snew = wave_xor_sum(d) * p.scale;
-    float M = snew;
+  {
+    const int g = tid / kAtD, d = tid % kAtD;  // 512 threads: 4 heads x 128 dims
+    if (g < G) {
+      const float snew = s_snew[g];
+      float M = snew;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][g][0]);
-    const float wn = __expf(snew - M);
-    float L = wn;
-    float O0 = wn * bf2f(s_new[1][2 * lane]), O1 = wn * bf2f(s_new[1][2 * lane + 1]);
+      for (int w = 0; w < kAtWaves; ++w) M = fmaxf(M, s_ml[w][g][0]);
+      const float wn = __expf(snew - M);
+      float L = wn;
+      float O = wn * bf2f(s_new[1][d]);
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float mw = s_ml[w][g][0];
-      const float ww = mw == -__builtin_inff() ? 0.0f : __expf(mw - M);
-      L += ww * s_ml[w][g][1];
-      O0 += ww * s_o[w][g][2 * lane];
-      O1 += ww * s_o[w][g][2 * lane + 1];
+      for (int w = 0; w < kAtWaves; ++w) {
+        const float ww = wexp(s_ml[w][g][0], M);
+        L += ww * s_ml[w][g][1];
+        O += ww * s_o[w][g][d];
+      }
+      const float inv = pos_ok ? 1.0f / L : 0.0f;
+      p.out[(int64_t)b * p.H * kAtD + (hk * G + g) * kAtD + d] = f2bf(O * inv);
     }
-    const float inv = pos_ok ? 1.0f / L : 0.0f;
-    uint16_t* out = p.out + (int64_t)b * p.H * kAtD + (hk * G + g) * kAtD + 2 * lane;
-    *reinterpret_cast<uint32_t*>(out) = (uint32_t)f2bf(O0 * inv) | ((uint32_t)f2bf(O1 * inv) << 16);
   }
+  BTL_TRACE_AT(5);
 }
 
 }  // namespace btl
 
 using namespace btl;
+
+BTL_TRACE_READ_FN
 
 extern "C" {
 
@@ -349,10 +380,9 @@ int btl_decode_attention(const uint16_t* qkv, int64_t B, int64_t H, int64_t Hkv,
   a.S = (int)S;
   a.scale = scale;
   a.adjacent = rope_adjacent ? 1 : 0;
-  char* ws = reinterpret_cast<char*>(workspace);
-  a.error = reinterpret_cast<int32_t*>(ws);
+  a.error = reinterpret_cast<int32_t*>(workspace);
   const dim3 grid((unsigned)(B * Hkv));
-  hipLaunchKernelGGL(k_decode_attention, grid, dim3(256), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(k_decode_attention, grid, dim3(64 * kAtWaves), 0, (hipStream_t)stream, a);
   return check_launch("decode attention");
 }
 

@@ -238,10 +238,40 @@ def test_fused_decode_handshake_clean(orc):
             continue  # decode-layer workspaces keep launch counters
         words = ws[:8192].view(torch.int32).cpu().numpy()
         assert words[err // 4] == 0, "a bounded wait ran out"
-        ready = words[0:32 * 32:32]  # one per 128-byte line
+        ready_idx = np.arange(32) * 32  # one per 128-byte line
+        ready = words[ready_idx]
         seen = words[33 * 32:33 * 32 + 512]
         assert ready.min() == ready.max() == seen.min() == seen.max() > 0, "launch counters out of step"
         rest = words.copy()
-        rest[0:32 * 32:32] = 0
+        rest[ready_idx] = 0
         rest[33 * 32:33 * 32 + 512] = 0
         assert not rest.any(), "stray handshake words"
+
+
+def test_fused_workspace_shared_across_shapes(orc):
+    """One stream's workspace carries calls of different K, M and N, and a
+    prefill call in between: the single-launch path's two operand tiles are
+    cleared for the next launch over the widest row, so a shorter row before
+    a longer one, or the split path writing its own buffers, never leaves
+    bytes that a later launch could take for its own."""
+    from bitnet_tt.ternary_matmul import PackedTernaryWeight, ternary_matmul
+
+    seq = [(32, 2560, 512, None), (32, 6912, 256, "g"), (5, 2560, 384, "g"), (64, 2560, 256, "g"),
+           (32, 8192, 256, "g"), (1, 6912, 512, None), (32, 2560, 512, "g"), (31, 4096, 256, None)]
+    for i, (m, k, n, norm) in enumerate(seq):
+        xb = H.activations(orc, m, k, seed=100 + i)
+        gb = H.gamma(orc, k, seed=200 + i) if norm else None
+        w = H.ternary(k, n, seed=300 + i)
+        pw = PackedTernaryWeight(device_weight(orc, w), k, n, (0.021,), (n,))
+        acc = torch.empty((m, n), dtype=torch.int32, device=H.dev())
+        kw = dict(norm_weight=H.to_dev_bf16(gb), norm_epsilon=1e-5) if norm else {}
+        print(f"call {i}: M={m} K={k} N={n} norm={bool(norm)}", flush=True)
+        out = ternary_matmul(H.to_dev_bf16(xb), pw, acc_out=acc, **kw)
+        torch.cuda.synchronize()
+        ref = orc.bitlinear(xb, w, [0.021], [n], gamma_bf16=gb, norm_eps=1e-5)
+        assert np.array_equal(acc.cpu().numpy(), ref["acc"]), f"call {i}: accumulators differ"
+        assert np.array_equal(H.bits_of(out), ref["out"]), f"call {i}: outputs differ"
+    err = int(N.lib().btl_fused_error_offset())
+    for key, ws in N._workspaces.items():
+        if key[0] == "bitlinear":
+            assert int(ws[:8192].view(torch.int32)[err // 4]) == 0, "a bounded wait ran out"
