@@ -249,11 +249,10 @@ def test_fused_decode_handshake_clean(orc):
 
 
 def test_fused_workspace_shared_across_shapes(orc):
-    """One stream's workspace carries calls of different K, M and N, and a
-    prefill call in between: the single-launch path's two operand tiles are
-    cleared for the next launch over the widest row, so a shorter row before
-    a longer one, or the split path writing its own buffers, never leaves
-    bytes that a later launch could take for its own."""
+    """One stream's workspace carries calls of different K, M and N, with a
+    prefill call (M > 32, the split path) in between: a shorter row before a
+    longer one, or the split path's own buffers, never leave bytes or counters
+    that a later launch takes for its own."""
     from bitnet_tt.ternary_matmul import PackedTernaryWeight, ternary_matmul
 
     seq = [(32, 2560, 512, None), (32, 6912, 256, "g"), (5, 2560, 384, "g"), (64, 2560, 256, "g"),
