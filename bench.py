@@ -189,9 +189,14 @@ def prefill_mfma(torch, N, dev):
     gen.manual_seed(77)
     for M, K, Nf in shapes:
         KS = (K + 127) // 128
-        xa = torch.randint(-128, 128, (int(L.btl_act_bytes(M, K)),), generator=gen, device=dev,
-                           dtype=torch.int16).to(torch.int8)
-        a_dq = torch.full((32 * ((M + 31) // 32),), 0.01, device=dev)
+        # activations as the layer makes them: absmax int8 operand, scales and
+        # row sums from the activation kernel
+        x = torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16)
+        xa = torch.empty((int(L.btl_act_bytes(M, K)),), dtype=torch.int8, device=dev)
+        a_dq = torch.empty((32 * ((M + 31) // 32),), dtype=torch.float32, device=dev)
+        rowsum = torch.empty((32 * ((M + 31) // 32),), dtype=torch.int32, device=dev)
+        N.check(L.btl_quant_absmax(N.ptr(x), M, K, K, None, 0.0, N.ptr(xa), N.ptr(a_dq), N.ptr(rowsum), None, None,
+                                   None, N.stream_of(dev)), "prefill activations")
         copies = 4
         wd = [torch.randint(0, 1 << 30, (Nf // 32, KS, 256), generator=gen, device=dev, dtype=torch.int32) & 0x55555555
               for _ in range(copies)]  # codes 0/1 only: valid ternary offsets
@@ -200,7 +205,7 @@ def prefill_mfma(torch, N, dev):
         stream = N.stream_of(dev)
 
         def launch(i):
-            N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(a_dq), M, K, Nf, N.ptr(wd[i % copies]), sc, en,
+            N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(a_dq), N.ptr(rowsum), M, K, Nf, N.ptr(wd[i % copies]), sc, en,
                                     nseg, 0, None, N.ptr(o), None, None, 0, 1, stream), "prefill gemm")
 
         reps = 20

@@ -88,7 +88,7 @@ EXPORTS = {
     "btl_quant_absmax": ([_P, _I64, _I64, _I64, _P, _F, _P, _P, _P, _P, _P, _P, _P], _I),
     "btl_rmsnorm": ([_P, _I64, _I64, _I64, _P, _F, _P, _P], _I),
     "btl_gemm_i8t2": (
-        [_P, _P, _I64, _I64, _I64, _P, _P, _P, _I, _I, _P, _P, _P, _P, _SZ, _I, _P],
+        [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I, _I, _P, _P, _P, _P, _SZ, _I, _P],
         _I,
     ),
     "btl_bitlinear_fused": (

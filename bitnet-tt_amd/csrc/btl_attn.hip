@@ -331,7 +331,7 @@ __global__ __launch_bounds__(64 * kAtWaves, 1) void k_decode_attention(AttnArgs 
 
 using namespace btl;
 
-BTL_TRACE_READ_FN
+BTL_TRACE_READ_FN(btl_trace_read_attention)
 
 extern "C" {
 

@@ -56,7 +56,7 @@ GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req
 // handshake words of the single-launch decode kernel, its error word among
 // them).
 struct FusedLayout {
-  int64_t xa, a_dq, gemm_ws, total;
+  int64_t xa, a_dq, rowsum, gemm_ws, total;
 };
 FusedLayout fused_layout(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req);
 

@@ -8,7 +8,9 @@
 // sum_k q*u, and the exact accumulator is recovered as
 //   acc = sum_k q*u - sum_k q
 // with the row sum taken from the A operand in the same pass (v_dot4 of the
-// operand bytes with 0x01010101; each K slice subtracts its own part).
+// operand bytes with 0x01010101; each K slice subtracts its own part), or,
+// in prefill, from the row sums the activation kernel wrote when the caller
+// passes them (the loop is then MFMAs and unpacking only).
 // |acc| <= 128*2*16384 < 2^31, so every step is exact.
 //
 // Decode (M <= 32): the whole activation block is one 32-row MFMA operand.
@@ -34,6 +36,7 @@
 
 #include "btl_act_row.h"
 #include "btl_mfma.h"
+#include "btl_trace.h"
 
 namespace btl {
 
@@ -45,6 +48,7 @@ int check_act_args(const char* who, const uint16_t* x, int64_t M, int64_t K, int
 struct GemmArgs {
   const int8_t* xa;
   const float* a_dq;
+  const int32_t* rowsum;  // optional [M] sum_k q (prefill: else summed from the tile's operand)
   const uint32_t* wdev;
   int M, KS, NT, N, n_out, Mb;
   int splitk, ngroups;
@@ -432,7 +436,9 @@ __device__ __forceinline__ void pf_issue(int8_t* stage_base, int stage_bytes, co
   for (int i = 0; i < NC; ++i) __builtin_amdgcn_global_load_lds(src[i] + (int64_t)ks * step[i], dst + i * 1024, 16, 0, 0);
 }
 
-template <int EPI, int RB, int WR>
+// PRS: the row sums come in p.rowsum (the activation kernel's); without it
+// one wave per row block sums that block's operand bytes in the loop.
+template <int EPI, int RB, int WR, bool PRS>
 __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, int ngn) {
   constexpr int kPfRB = PfShape<RB, WR>::rb;
   constexpr int XR = PfShape<RB, WR>::xr;
@@ -447,7 +453,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   float* s_adq = reinterpret_cast<float*>(lds + kPfStages * kPfChunks * 1024);
   int32_t* s_rs = reinterpret_cast<int32_t*>(lds + kPfStages * kPfChunks * 1024 + kPfRB * 32 * 4);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int wm = wv % WR, wn = wv / WR;
+  // wave-uniform as far as the compiler knows (a branch on wn then costs no
+  // select over both sides)
+  const int wm = __builtin_amdgcn_readfirstlane(wv % WR), wn = __builtin_amdgcn_readfirstlane(wv / WR);
   const int ntiles = ngm * ngn;
   const int per = (ntiles + kPfXcds - 1) / kPfXcds;
   const int t = (int)(blockIdx.x % kPfXcds) * per + (int)(blockIdx.x / kPfXcds);
@@ -486,19 +494,24 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   for (int x = 0; x < XR; ++x)
 #pragma unroll
     for (int u = 0; u < US; ++u) acc[x][u] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  // Row sums: each row block of the tile is summed by one wave: wave (wm, wn)
-  // takes its row block XR*wm + wn when wn < XR.
+  // Row sums (!PRS): each row block of the tile is summed by one wave: wave
+  // (wm, wn) takes its row block XR*wm + wn when wn < XR.
   int32_t rs_lane = 0;
 
-  const float adq_mine = p.a_dq[min(gm * kPfRB * 32 + (tid & (kPfRB * 32 - 1)), p.Mb * 32 - 1)];
+  const int row_mine = gm * kPfRB * 32 + (tid & (kPfRB * 32 - 1));
+  const float adq_mine = p.a_dq[min(row_mine, p.Mb * 32 - 1)];
+  if (PRS) rs_lane = p.rowsum[min(row_mine, p.M - 1)];  // rows past M are not stored
 #pragma unroll
   for (int k = 0; k < kPfStages; ++k)
     if (k < KS) pf_issue<kPfChunksPerWave>(lds, kPfChunks * 1024, src, step, k, wv);
+  BTL_TRACE_AT(0);
   for (int ks = 0; ks < KS; ++ks) {
     // this wave's loads of superblock ks are done once at most the loads of
     // the (up to kPfStages - 1) later superblocks are outstanding
     pf_wait<kPfChunksPerWave, kPfStages>(KS - 1 - ks);
+    if (ks < 6) BTL_TRACE_AT(1 + 2 * ks);
     barrier_only();
+    if (ks < 6) BTL_TRACE_AT(2 + 2 * ks);
     const int8_t* buf = stage[ks % kPfStages];
     v4i bw[US];
 #pragma unroll
@@ -514,10 +527,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
 #pragma unroll
         for (int x = 0; x < XR; ++x) acc[x][u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[x], b, acc[x][u], 0, 0, 0);
       }
+      if (!PRS) {
 #pragma unroll
-      for (int x = 0; x < XR; ++x)
-        if (x == wn) rs_lane = bytes_sum(a[x], rs_lane);  // wn is uniform across the wave
+        for (int x = 0; x < XR; ++x)
+          if (x == wn) rs_lane = bytes_sum(a[x], rs_lane);  // wn is uniform across the wave
+      }
     }
+    if (ks == KS - 1) BTL_TRACE_AT(13);
     barrier_only();  // every wave's reads of this buffer are done (their values fed the MFMAs)
     if (ks + kPfStages < KS) pf_issue<kPfChunksPerWave>(lds, kPfChunks * 1024, src, step, ks + kPfStages, wv);
   }
@@ -526,11 +542,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   // each wave writes its scaled bf16 values (relu^2*u for relu2) into the
   // workgroup's output tile, then all threads write whole rows with 16-byte
   // stores, adding the residual read the same way.
-  {
+  if (PRS) {
+    if (tid < kPfRB * 32) s_rs[tid] = rs_lane;  // loaded at the start with a_dq
+  } else {
     const int32_t rs_row = rs_lane + (int32_t)xor_partner_u<32>((uint32_t)rs_lane);  // lanes l, l+32: halves of row l & 31
     if (lane < 32 && wn < XR) s_rs[(XR * wm + wn) * 32 + lane] = rs_row;
-    if (tid < kPfRB * 32) s_adq[tid] = adq_mine;  // loaded at the start; stored now, after the stage loads
   }
+  if (tid < kPfRB * 32) s_adq[tid] = adq_mine;  // loaded at the start; stored now, after the stage loads
   __syncthreads();  // s_rs, s_adq visible; every wave is done with the stage buffers
   int8_t* tile_lds = &stage[0][0];
   constexpr int kOutCols = (EPI == EPI_RELU2) ? kPfCT * 16 : kPfCT * 32;  // output columns of the tile
@@ -738,7 +756,8 @@ FusedLayout fused_layout(int64_t M, int64_t K, int64_t N, int epilogue, int spli
   const int64_t rows = mblocks(M) * 32;
   L.xa = kSyncBytes;
   L.a_dq = L.xa + round_up(btl_act_bytes(M, K), 256);
-  L.gemm_ws = L.a_dq + round_up(rows * 4, 256);
+  L.rowsum = L.a_dq + round_up(rows * 4, 256);
+  L.gemm_ws = L.rowsum + round_up(rows * 4, 256);
   const GemmPlan pf = plan_fused(M, K, N, epilogue, splitk_req);
   const GemmPlan pg = plan_gemm(M, K, N, epilogue, splitk_req);
   L.total = L.gemm_ws + (pf.ws_bytes > pg.ws_bytes ? pf.ws_bytes : pg.ws_bytes);
@@ -819,13 +838,14 @@ static int check_gemm_args(const char* who, int64_t M, int64_t K, int64_t N, con
   return BTL_OK;
 }
 
-static GemmArgs gemm_args(const int8_t* xa, const float* a_dq, int64_t M, int64_t K,
+static GemmArgs gemm_args(const int8_t* xa, const float* a_dq, const int32_t* rowsum, int64_t M, int64_t K,
                           int64_t N, const uint32_t* wdev, const float* seg_scale, const int64_t* seg_end, int nseg,
                           int epilogue, const uint16_t* residual, uint16_t* out, int32_t* acc_out, char* ws,
                           const GemmPlan& pl) {
   GemmArgs a = {};
   a.xa = xa;
   a.a_dq = a_dq;
+  a.rowsum = pl.prefill ? rowsum : nullptr;  // the decode kernels sum their operand
   a.wdev = wdev;
   a.M = (int)M;
   a.KS = (int)ksb(K);
@@ -851,6 +871,21 @@ static GemmArgs gemm_args(const int8_t* xa, const float* a_dq, int64_t M, int64_
   return a;
 }
 
+template <bool PRS>
+static void launch_prefill(int epilogue, int rb, dim3 grid, hipStream_t s, const GemmArgs& a, int ngm, int ngn) {
+  if (epilogue == BTL_EPI_RELU2_MUL) {
+    if (rb == 4)
+      hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2, 4, 2, PRS>), grid, dim3(256), 0, s, a, ngm, ngn);
+    else
+      hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2, 2, 1, PRS>), grid, dim3(256), 0, s, a, ngm, ngn);
+  } else {
+    if (rb == 4)
+      hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE, 4, 2, PRS>), grid, dim3(256), 0, s, a, ngm, ngn);
+    else
+      hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE, 2, 1, PRS>), grid, dim3(256), 0, s, a, ngm, ngn);
+  }
+}
+
 static int launch_gemm(const GemmArgs& a, int epilogue, const GemmPlan& pl, hipStream_t s) {
   if (pl.prefill) {
     const int ngn = (epilogue == BTL_EPI_RELU2_MUL) ? (a.NT / 2 + 3) / 4 : (a.NT + kPfCT - 1) / kPfCT;
@@ -865,17 +900,10 @@ static int launch_gemm(const GemmArgs& a, int epilogue, const GemmPlan& pl, hipS
     // the 2B shapes, one row block per wave is 5-9 % slower (VALU unpacking
     // that does not overlap the MFMAs) and four per wave ~10 % slower (LDS
     // reads and 237 VGPRs).
-    if (epilogue == BTL_EPI_RELU2_MUL) {
-      if (rb == 4)
-        hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2, 4, 2>), grid, dim3(256), 0, s, a, ngm, ngn);
-      else
-        hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2, 2, 1>), grid, dim3(256), 0, s, a, ngm, ngn);
-    } else {
-      if (rb == 4)
-        hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE, 4, 2>), grid, dim3(256), 0, s, a, ngm, ngn);
-      else
-        hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE, 2, 1>), grid, dim3(256), 0, s, a, ngm, ngn);
-    }
+    if (a.rowsum)
+      launch_prefill<true>(epilogue, rb, grid, s, a, ngm, ngn);
+    else
+      launch_prefill<false>(epilogue, rb, grid, s, a, ngm, ngn);
     return check_launch("ternary gemm (prefill)");
   }
   const int nsb = decode_nsb(pl, a.KS, epilogue);
@@ -942,7 +970,7 @@ int64_t btl_fused_workspace_bytes(int64_t M, int64_t K, int64_t N, int epilogue,
   return fused_layout(M, K, N, epilogue, splitk).total;
 }
 
-int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, int64_t M, int64_t K, int64_t N,
+int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, const int32_t* rowsum, int64_t M, int64_t K, int64_t N,
                   const uint32_t* wdev, const float* seg_scale, const int64_t* seg_end, int nseg, int epilogue,
                   const uint16_t* residual, uint16_t* out, int32_t* acc_out, void* workspace, size_t workspace_bytes,
                   int splitk, btl_stream_t stream) {
@@ -950,8 +978,8 @@ int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, int64_t M, int64_t K, int
   int rc = check_gemm_args("btl_gemm_i8t2", M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out);
   if (rc) return rc;
   if (!xa || !a_dq) return set_error(BTL_ERR_NULL, "btl_gemm_i8t2: activation pointer is NULL");
-  if (!aligned(xa, 16) || !aligned(a_dq, 4) || (acc_out && !aligned(acc_out, 4)))
-    return set_error(BTL_ERR_ALIGN, "btl_gemm_i8t2: misaligned activation or acc_out buffer");
+  if (!aligned(xa, 16) || !aligned(a_dq, 4) || (rowsum && !aligned(rowsum, 4)) || (acc_out && !aligned(acc_out, 4)))
+    return set_error(BTL_ERR_ALIGN, "btl_gemm_i8t2: misaligned activation, rowsum or acc_out buffer");
   if (splitk < 0) return set_error(BTL_ERR_ARG, "btl_gemm_i8t2: splitk=%d", splitk);
   const GemmPlan pl = plan_gemm(M, K, N, epilogue, splitk);
   if (pl.ws_bytes > 0) {
@@ -961,7 +989,7 @@ int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, int64_t M, int64_t K, int
                        (long long)pl.ws_bytes);
     if (!aligned(workspace, 256)) return set_error(BTL_ERR_ALIGN, "btl_gemm_i8t2: workspace must be 256-byte aligned");
   }
-  const GemmArgs a = gemm_args(xa, a_dq, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out,
+  const GemmArgs a = gemm_args(xa, a_dq, rowsum, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out,
                                acc_out, (char*)workspace, pl);
   return launch_gemm(a, epilogue, pl, (hipStream_t)stream);
 }
@@ -1008,7 +1036,7 @@ int btl_bitlinear_fused(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, co
     // interrupted call is repaired by the next one.
     a.zero_words = pf.splitk > 1 ? (uint32_t*)(ws + L.gemm_ws) : nullptr;
     a.n_zero_words = pf.splitk > 1 ? pf.ngroups : 0;
-    const GemmArgs g = gemm_args(xa, a_dq, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out,
+    const GemmArgs g = gemm_args(xa, a_dq, nullptr, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out,
                                  acc_out, ws + L.gemm_ws, pf);
     FusedSync fs;
     fs.words = (uint32_t*)ws;
@@ -1026,12 +1054,17 @@ int btl_bitlinear_fused(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, co
   }
 
   const GemmPlan pl = plan_gemm(M, K, N, epilogue, splitk);
-  rc = launch_act(x, M, K, ldx, gamma, norm_eps, xa, a_dq, nullptr, nullptr, xq_debug, nullptr,
+  // The prefill GEMM takes the row sums from the activation kernel, which
+  // has them in registers anyway; the decode GEMM sums its own operand.
+  int32_t* rowsum = pl.prefill ? (int32_t*)(ws + L.rowsum) : nullptr;
+  rc = launch_act(x, M, K, ldx, gamma, norm_eps, xa, a_dq, rowsum, nullptr, xq_debug, nullptr,
                   pl.splitk > 1 ? (uint32_t*)(ws + L.gemm_ws) : nullptr, pl.splitk > 1 ? pl.ngroups : 0, s);
   if (rc) return rc;
-  const GemmArgs g = gemm_args(xa, a_dq, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out,
+  const GemmArgs g = gemm_args(xa, a_dq, rowsum, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out,
                                acc_out, ws + L.gemm_ws, pl);
   return launch_gemm(g, epilogue, pl, s);
 }
 
 }  // extern "C"
+
+BTL_TRACE_READ_FN(btl_trace_read_gemm)

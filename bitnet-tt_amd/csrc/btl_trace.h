@@ -1,8 +1,9 @@
 // Phase timestamps for measurement builds (-DBTL_TRACE only; compiled out
 // otherwise): lane 0 of each wave stores s_memrealtime (100 MHz, one clock
 // for the whole device) at a kernel's numbered events into
-// g_trace[block][wave][event]; btl_trace_read (measurement builds) copies the
-// table out and clears it.  Each translation unit has its own table.
+// g_trace[block][wave][event]; BTL_TRACE_READ_FN(name) defines name(dst, bytes),
+// which copies the table out and clears it (measurement builds).  Each
+// translation unit has its own table.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -18,8 +19,8 @@ static __device__ uint64_t g_trace[kTraceBlocks][kTraceWaves][kTraceEvents];
     if (__lane_id() == 0 && blockIdx.x < (unsigned)::btl::kTraceBlocks)                                    \
       ::btl::g_trace[blockIdx.x][threadIdx.x >> 6][(ev)] = __builtin_amdgcn_s_memrealtime();               \
   } while (0)
-#define BTL_TRACE_READ_FN                                                                                  \
-  extern "C" int btl_trace_read(void* dst, size_t bytes) {                                                 \
+#define BTL_TRACE_READ_FN(name)                                                                            \
+  extern "C" int name(void* dst, size_t bytes) {                                                           \
     if (bytes > sizeof(::btl::g_trace)) bytes = sizeof(::btl::g_trace);                                    \
     if (hipMemcpyFromSymbol(dst, HIP_SYMBOL(::btl::g_trace), bytes, 0, hipMemcpyDeviceToHost) != hipSuccess) \
       return 1;                                                                                            \
@@ -31,5 +32,5 @@ static __device__ uint64_t g_trace[kTraceBlocks][kTraceWaves][kTraceEvents];
 #define BTL_TRACE_AT(ev) \
   do {                   \
   } while (0)
-#define BTL_TRACE_READ_FN
+#define BTL_TRACE_READ_FN(name)
 #endif

@@ -132,7 +132,9 @@ int btl_rmsnorm(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint
 /* ---- the ternary GEMM ------------------------------------------------ */
 
 /* acc[m,n] = sum_k q[m,k] * w[k,n] in int32 (exact), then the epilogue.
- * xa/a_dq as produced by btl_quant_absmax for the same M, K.
+ * xa/a_dq as produced by btl_quant_absmax for the same M, K; rowsum:
+ * optional [M] sum_k q, its rowsum output -- with it the M > 32 kernels skip
+ * summing the operand themselves (NULL: they do; M <= 32 ignores it).
  * seg_scale/seg_end: host arrays of nseg (1..4) weight scales and exclusive
  * column ends (multiples of 32, last == N) -- per-projection scales of the
  * fused QKV / gate||up weights (src/bitnet_tt/layers/attention.py:481-506,
@@ -142,7 +144,7 @@ int btl_rmsnorm(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint
  * splitk: 0 = library's choice.  workspace: btl_gemm_workspace_bytes(...)
  * bytes; its counters must be zero before the first call and are left zero
  * by every completed call.                                                 */
-int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, int64_t M, int64_t K, int64_t N, const uint32_t* wdev,
+int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, const int32_t* rowsum, int64_t M, int64_t K, int64_t N, const uint32_t* wdev,
                   const float* seg_scale, const int64_t* seg_end, int nseg, int epilogue, const uint16_t* residual, uint16_t* out, int32_t* acc_out, void* workspace,
                   size_t workspace_bytes, int splitk, btl_stream_t stream);
 

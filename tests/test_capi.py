@@ -75,12 +75,12 @@ def _p(x):
 
 
 def call_gemm(L, **kw):
-    a = dict(xa=_p(FAKE), a_dq=_p(FAKE), M=32, K=256, N=64, wdev=_p(FAKE), nseg=1, epi=0,
+    a = dict(xa=_p(FAKE), a_dq=_p(FAKE), rowsum=None, M=32, K=256, N=64, wdev=_p(FAKE), nseg=1, epi=0,
              residual=None, out=_p(FAKE), acc=None, ws=None, ws_bytes=0, splitk=1)
     a.update(kw)
     sc = (ctypes.c_float * 4)(1.0, 1.0, 1.0, 1.0)
     en = (ctypes.c_int64 * 4)(*(kw.get("ends") or (a["N"], a["N"], a["N"], a["N"])))
-    return L.btl_gemm_i8t2(a["xa"], a["a_dq"], a["M"], a["K"], a["N"], a["wdev"], sc, en, a["nseg"],
+    return L.btl_gemm_i8t2(a["xa"], a["a_dq"], a["rowsum"], a["M"], a["K"], a["N"], a["wdev"], sc, en, a["nseg"],
                            a["epi"], a["residual"], a["out"], a["acc"], a["ws"], a["ws_bytes"], a["splitk"], None)
 
 
@@ -100,6 +100,8 @@ def test_gemm_argument_checks(L):
     assert "16-byte" in N.last_error()
     assert call_gemm(L, xa=_p(FAKE + 8)) == 3
     assert "misaligned" in N.last_error()
+    assert call_gemm(L, M=64, rowsum=_p(FAKE + 2)) == 3
+    assert "rowsum" in N.last_error()
     # split-K needs a workspace of the advertised size
     assert call_gemm(L, M=32, K=2560, N=3840, splitk=2, ws=None) == 1
     assert call_gemm(L, M=32, K=2560, N=3840, splitk=2, ws=_p(FAKE), ws_bytes=16) == 4

@@ -21,9 +21,10 @@ def device_weight(orc, w_kn):
     return H.to_dev(dev.view(np.int32))
 
 
-def run_gemm(orc, q, w_kn, scales, ends=None, epi=0, splitk=0, residual_bits=None, wdev=None):
+def run_gemm(orc, q, w_kn, scales, ends=None, epi=0, splitk=0, residual_bits=None, wdev=None, rowsum=False):
     """int8 q [m,k] x ternary w [k,n] through btl_gemm_i8t2 with a random
-    per-row dequantisation factor a_dq (the row sums come from the operand)."""
+    per-row dequantisation factor a_dq.  rowsum=True hands the kernel the row
+    sums sum_k q (as btl_quant_absmax writes them); else it sums the operand."""
     L = N.lib()
     d = H.dev()
     m, k = q.shape
@@ -46,7 +47,8 @@ def run_gemm(orc, q, w_kn, scales, ends=None, epi=0, splitk=0, residual_bits=Non
     ws_bytes = int(L.btl_gemm_workspace_bytes(m, k, n, epi, splitk))
     ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=d)
     a_dq_d = H.to_dev(a_dq)  # keep the tensor alive across the launch
-    N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(a_dq_d), m, k, n, N.ptr(wdev), sc, en,
+    rs_d = H.to_dev(q.astype(np.int32).sum(1, dtype=np.int64).astype(np.int32)) if rowsum else None
+    N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(a_dq_d), N.ptr(rs_d), m, k, n, N.ptr(wdev), sc, en,
                             nseg, epi, N.ptr(res), N.ptr(out), N.ptr(acc), N.ptr(ws), ws.numel(), splitk,
                             N.stream_of(d)), "btl_gemm_i8t2")
     torch.cuda.synchronize()
@@ -148,41 +150,44 @@ def test_relu2_epilogue(orc, m, k, f):
 
 
 @pytest.mark.parametrize("m,k,n", [(33, 256, 128), (64, 512, 96), (100, 640, 160), (512, 256, 64)])
-def test_prefill_gemm_bit_exact(orc, m, k, n):
-    print(f"prefill gemm m={m} k={k} n={n}", flush=True)
+@pytest.mark.parametrize("rowsum", [False, True])
+def test_prefill_gemm_bit_exact(orc, m, k, n, rowsum):
+    print(f"prefill gemm m={m} k={k} n={n} rowsum={rowsum}", flush=True)
     rng = np.random.default_rng(m + k + n)
     q = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
     w = H.ternary(k, n, seed=n)
-    acc, out, a_dq, _ = run_gemm(orc, q, w, [0.02])
+    acc, out, a_dq, _ = run_gemm(orc, q, w, [0.02], rowsum=rowsum)
     ref = orc.gemm_i8t(q, w)
     assert np.array_equal(acc, ref)
     assert np.array_equal(out, expected_out(orc, ref, a_dq, [0.02], [n], 0))
 
 
 @pytest.mark.parametrize("m,k,f", [(70, 384, 96), (512, 256, 160), (129, 640, 32)])
-def test_prefill_relu2_bit_exact(orc, m, k, f):
+@pytest.mark.parametrize("rowsum", [False, True])
+def test_prefill_relu2_bit_exact(orc, m, k, f, rowsum):
     """relu2 prefill with F not a multiple of the 4 gate tiles of a workgroup."""
-    print(f"prefill relu2 m={m} k={k} f={f}", flush=True)
+    print(f"prefill relu2 m={m} k={k} f={f} rowsum={rowsum}", flush=True)
     rng = np.random.default_rng(m * 7 + f)
     q = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
     w = H.ternary(k, 2 * f, seed=f + 1)
     scales, ends = [0.021, 0.017], [f, 2 * f]
-    acc, out, a_dq, _ = run_gemm(orc, q, w, scales, ends, epi=1)
+    acc, out, a_dq, _ = run_gemm(orc, q, w, scales, ends, epi=1, rowsum=rowsum)
     assert np.array_equal(acc, orc.gemm_i8t(q, w))
     assert np.array_equal(out, expected_out(orc, acc, a_dq, scales, ends, 1))
 
 
-@pytest.mark.parametrize("m,k,n,epi", [(512, 2560, 3840, 0), (512, 2560, 13824, 1), (2048, 2560, 6912, 0),
-                                       (2048, 6912, 2560, 0), (512, 2560, 2560, 0)])
-def test_prefill_full_size_properties(orc, m, k, n, epi):
+@pytest.mark.parametrize("m,k,n,epi,rowsum", [(512, 2560, 3840, 0, False), (512, 2560, 13824, 1, True),
+                                              (2048, 2560, 6912, 0, True), (2048, 6912, 2560, 0, False),
+                                              (2048, 6912, 2560, 0, True), (512, 2560, 2560, 0, True)])
+def test_prefill_full_size_properties(orc, m, k, n, epi, rowsum):
     """Full prefill shapes: sampled rows exact, row/column checksums exact."""
-    print(f"prefill full m={m} k={k} n={n} epi={epi}", flush=True)
+    print(f"prefill full m={m} k={k} n={n} epi={epi} rowsum={rowsum}", flush=True)
     rng = np.random.default_rng(m + n)
     q = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
     w = H.ternary(k, n, seed=k + n)
     scales = [0.02] if epi == 0 else [0.02, 0.03]
     ends = [n] if epi == 0 else [n // 2, n]
-    acc, out, a_dq, _ = run_gemm(orc, q, w, scales, ends, epi=epi)
+    acc, out, a_dq, _ = run_gemm(orc, q, w, scales, ends, epi=epi, rowsum=rowsum)
     rows = np.sort(rng.choice(m, 6, replace=False))
     ref_rows = orc.gemm_i8t(np.ascontiguousarray(q[rows]), w)
     assert np.array_equal(acc[rows], ref_rows)
@@ -193,22 +198,25 @@ def test_prefill_full_size_properties(orc, m, k, n, epi):
     assert np.array_equal(out[rows], exp_rows)
 
 
-def test_fused_entry_matches_split_path(orc):
-    """btl_bitlinear_fused == btl_quant_absmax + btl_gemm_i8t2, and == oracle."""
+@pytest.mark.parametrize("m", [32, 100])
+def test_fused_entry_matches_split_path(orc, m):
+    """btl_bitlinear_fused == oracle: one launch at M = 32; at M = 100 the
+    activation kernel and the prefill GEMM, which takes its row sums."""
     from bitnet_tt.ternary_matmul import PackedTernaryWeight, ternary_matmul
 
-    m, k, n = 32, 2560, 3840
+    print(f"fused entry m={m}", flush=True)
+    k, n = 2560, 3840
     xb = H.activations(orc, m, k, seed=21)
     gb = H.gamma(orc, k, seed=22)
     w = H.ternary(k, n, seed=23)
     pw = PackedTernaryWeight(device_weight(orc, w), k, n, (0.017, 0.019, 0.023), (2560, 3200, 3840))
     acc = torch.empty((m, n), dtype=torch.int32, device=H.dev())
     xq = torch.empty((m, k), dtype=torch.int8, device=H.dev())
+    ref = orc.bitlinear(xb, w, [0.017, 0.019, 0.023], [2560, 3200, 3840], gamma_bf16=gb, norm_eps=1e-5)
     for splitk in (0, 1, 2, 4):
         out = ternary_matmul(H.to_dev_bf16(xb), pw, norm_weight=H.to_dev_bf16(gb), norm_epsilon=1e-5,
                              splitk=splitk, acc_out=acc, xq_out=xq)
         torch.cuda.synchronize()
-        ref = orc.bitlinear(xb, w, [0.017, 0.019, 0.023], [2560, 3200, 3840], gamma_bf16=gb, norm_eps=1e-5)
         assert np.array_equal(xq.cpu().numpy(), ref["q"])
         assert np.array_equal(acc.cpu().numpy(), ref["acc"])
         assert np.array_equal(H.bits_of(out), ref["out"])
