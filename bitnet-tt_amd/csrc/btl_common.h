@@ -25,6 +25,18 @@ __host__ __device__ __forceinline__ uint16_t f2bf(float f) {
 #endif
 }
 
+// Two values at once, f2bf of each: lo in bits 15:0, hi in bits 31:16 (one
+// v_cvt_pk_bf16_f32 on the device).
+__host__ __device__ __forceinline__ uint32_t f2bf_pair(float lo, float hi) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
+#else
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+#endif
+}
+
 // ---- errors -------------------------------------------------------------
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();

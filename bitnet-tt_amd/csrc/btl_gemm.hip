@@ -353,10 +353,11 @@ __global__ __launch_bounds__(512) void k_bitlinear_decode(GemmArgs p, ActArgs a,
 // activation tile (16 KiB: 4 row blocks x 4 k-steps) and of the packed
 // weights (8 KiB: 8 tiles) is staged in LDS as 24 chunks of 1 KiB, six per
 // wave, each one global_load_lds_dwordx4 (lane i's 16 bytes land at chunk +
-// 16i), so staging costs no registers.  kPfStages superblocks are in flight:
-// a stage is waited for (vmcnt of the wave's own loads, then a barrier), its
-// MFMAs run, and after a second barrier the freed buffer is refilled with the
-// superblock kPfStages ahead.  The four waves form a WR x (4/WR) grid: wave
+// 16i), so staging costs no registers.  ST stages rotate (3 for 128-row
+// tiles, 4 for 64-row tiles): one barrier per superblock, after the wave's
+// own loads of it have landed (vmcnt), also marks the previous stage as read
+// by every wave, and that stage is refilled right after it with the
+// superblock ST - 1 ahead.  The four waves form a WR x (4/WR) grid: wave
 // (wm, wn) = (wv % WR, wv / WR) computes the RB/WR row blocks from
 // (RB/WR)*wm against US = 2*WR column slots: US*wn.. (scale), or US/2 gate
 // slots from (US/2)*wn with the up slots 4 above them (relu2: a column's gate
@@ -371,7 +372,6 @@ __global__ __launch_bounds__(512) void k_bitlinear_decode(GemmArgs p, ActArgs a,
 constexpr int kPfXcds = 8;
 constexpr int kPfGroupRows = 4;
 constexpr int kPfCT = 8;      // column tiles of 32 per workgroup
-constexpr int kPfStages = 3;
 // Row blocks of 32 per workgroup: 4 (128 rows), or 2 (64 rows, each wave one
 // row block) when 128-row tiles would leave CUs idle.
 
@@ -406,11 +406,15 @@ __device__ __forceinline__ void pf_wait(int later) {
   }
 }
 
-// Workgroup barrier without the memory fence of __syncthreads (whose release
-// part would wait for every load in flight, the LDS-direct ones included);
-// the compiler fences keep LDS accesses on their side of it.
-__device__ __forceinline__ void barrier_only() {
+// Workgroup barrier after this wave's LDS accesses have completed
+// (lgkmcnt(0)), without the memory fence of __syncthreads, whose release part
+// would also wait for every global load in flight, the LDS-direct ones
+// included.  The compiler fences keep LDS instructions on their side of it;
+// the explicit wait covers their results, which the compiler would otherwise
+// be free to collect after the barrier.
+__device__ __forceinline__ void lds_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt unconstrained
   __builtin_amdgcn_s_barrier();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
@@ -424,14 +428,17 @@ struct PfShape {
   static constexpr int us = 2 * WR;              // column slots per wave
   static constexpr int chunks = RB * 4 + kPfCT;  // 1 KiB chunks per stage
   static constexpr int per_wave = chunks / 4;
+  // Stages in flight: the 128-row tile's 24 KiB stages fit three times for two
+  // workgroups per CU; the 64-row tile's 16 KiB stages four times.
+  static constexpr int stages = RB == 4 ? 3 : 4;
 };
 
 // Issues this wave's direct-to-LDS loads of superblock ks (a plain function:
 // a lambda here keeps the host compiler from emitting the kernel's stub).
-template <int NC>
+template <int NC, int ST>
 __device__ __forceinline__ void pf_issue(int8_t* stage_base, int stage_bytes, const int8_t* const* src, const int* step,
                                          int ks, int wv) {
-  int8_t* dst = stage_base + (ks % kPfStages) * stage_bytes + wv * NC * 1024;
+  int8_t* dst = stage_base + (ks % ST) * stage_bytes + wv * NC * 1024;
 #pragma unroll
   for (int i = 0; i < NC; ++i) __builtin_amdgcn_global_load_lds(src[i] + (int64_t)ks * step[i], dst + i * 1024, 16, 0, 0);
 }
@@ -440,6 +447,7 @@ __device__ __forceinline__ void pf_issue(int8_t* stage_base, int stage_bytes, co
 // one wave per row block sums that block's operand bytes in the loop.
 template <int EPI, int RB, int WR, bool PRS>
 __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, int ngn) {
+  constexpr int ST = PfShape<RB, WR>::stages;
   constexpr int kPfRB = PfShape<RB, WR>::rb;
   constexpr int XR = PfShape<RB, WR>::xr;
   constexpr int US = PfShape<RB, WR>::us;
@@ -448,10 +456,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   constexpr int kPfChunksPerWave = PfShape<RB, WR>::per_wave;
   // One LDS object: the stage buffers, then a_dq and the row sums of the
   // tile's rows.
-  __shared__ __attribute__((aligned(16))) int8_t lds[kPfStages * kPfChunks * 1024 + kPfRB * 32 * 8];
+  __shared__ __attribute__((aligned(16))) int8_t lds[ST * kPfChunks * 1024 + kPfRB * 32 * 8];
   int8_t (*stage)[kPfChunks * 1024] = reinterpret_cast<int8_t (*)[kPfChunks * 1024]>(lds);
-  float* s_adq = reinterpret_cast<float*>(lds + kPfStages * kPfChunks * 1024);
-  int32_t* s_rs = reinterpret_cast<int32_t*>(lds + kPfStages * kPfChunks * 1024 + kPfRB * 32 * 4);
+  float* s_adq = reinterpret_cast<float*>(lds + ST * kPfChunks * 1024);
+  int32_t* s_rs = reinterpret_cast<int32_t*>(lds + ST * kPfChunks * 1024 + kPfRB * 32 * 4);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   // wave-uniform as far as the compiler knows (a branch on wn then costs no
   // select over both sides)
@@ -502,17 +510,22 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   const float adq_mine = p.a_dq[min(row_mine, p.Mb * 32 - 1)];
   if (PRS) rs_lane = p.rowsum[min(row_mine, p.M - 1)];  // rows past M are not stored
 #pragma unroll
-  for (int k = 0; k < kPfStages; ++k)
-    if (k < KS) pf_issue<kPfChunksPerWave>(lds, kPfChunks * 1024, src, step, k, wv);
+  for (int k = 0; k < ST; ++k)
+    if (k < KS) pf_issue<kPfChunksPerWave, ST>(lds, kPfChunks * 1024, src, step, k, wv);
   BTL_TRACE_AT(0);
   for (int ks = 0; ks < KS; ++ks) {
-    // this wave's loads of superblock ks are done once at most the loads of
-    // the (up to kPfStages - 1) later superblocks are outstanding
-    pf_wait<kPfChunksPerWave, kPfStages>(KS - 1 - ks);
-    if (ks < 6) BTL_TRACE_AT(1 + 2 * ks);
-    barrier_only();
-    if (ks < 6) BTL_TRACE_AT(2 + 2 * ks);
-    const int8_t* buf = stage[ks % kPfStages];
+    // Superblocks of this wave in flight: ks .. ks + ST - 1 at ks = 0, then
+    // ks .. ks + ST - 2 (the refill of a freed stage is issued one iteration
+    // after its reads); ks has landed once the rest are all that is left.
+    pf_wait<kPfChunksPerWave, ST>(min(ks == 0 ? ST - 1 : ST - 2, KS - 1 - ks));
+    if (ks < 5) BTL_TRACE_AT(1 + 2 * ks);
+    // every wave's loads of ks have landed and every wave is done reading
+    // stage (ks - 1) % ST, which is refilled with superblock ks - 1 + ST
+    lds_barrier();
+    if (ks < 5) BTL_TRACE_AT(2 + 2 * ks);
+    if (ks >= 1 && ks - 1 + ST < KS)
+      pf_issue<kPfChunksPerWave, ST>(lds, kPfChunks * 1024, src, step, ks - 1 + ST, wv);
+    const int8_t* buf = stage[ks % ST];
     v4i bw[US];
 #pragma unroll
     for (int u = 0; u < US; ++u) bw[u] = *reinterpret_cast<const v4i*>(buf + (kPfRB * 4 + slot[u]) * 1024 + lane * 16);
@@ -534,8 +547,6 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
       }
     }
     if (ks == KS - 1) BTL_TRACE_AT(13);
-    barrier_only();  // every wave's reads of this buffer are done (their values fed the MFMAs)
-    if (ks + kPfStages < KS) pf_issue<kPfChunksPerWave>(lds, kPfChunks * 1024, src, step, ks + kPfStages, wv);
   }
 
   // Epilogue in two passes through LDS (the stage buffers are free now):
@@ -553,7 +564,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   int8_t* tile_lds = &stage[0][0];
   constexpr int kOutCols = (EPI == EPI_RELU2) ? kPfCT * 16 : kPfCT * 32;  // output columns of the tile
   constexpr int kPitch = kOutCols * 2 + 16;  // bytes per row; halves of a wave land 16 banks apart
-  static_assert(kPfRB * 32 * kPitch <= kPfStages * kPfChunks * 1024, "output tile fits in the stage buffers");
+  static_assert(kPfRB * 32 * kPitch <= ST * kPfChunks * 1024, "output tile fits in the stage buffers");
   const int j = lane & 31;
   // weight scale per slot: segment ends are multiples of 32, so one per tile
   float sw[US];
@@ -594,29 +605,42 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
         }
       }
     }
+    // Row block x of this wave: lane l holds column j of rows acc_row(r, l)
+    // = 8*(r/4) + 4*(l/32) + r%4, so a column's rows sit at constant offsets
+    // from one base per slot, and rows r, r + 1 share one conversion.
+    int8_t* const base_x = tile_lds + ((XR * wm + x) * 32 + 4 * (lane >> 5)) * kPitch + j * 2;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int32_t rs = rsr[r];
-      const int il = (XR * wm + x) * 32 + acc_row(r, lane);  // row within the tile
+    for (int r = 0; r < 16; r += 2) {
+      const int off0 = (8 * (r >> 2) + (r & 3)) * kPitch, off1 = off0 + kPitch;
       if (EPI == EPI_RELU2) {
 #pragma unroll
         for (int u = 0; u < HU; ++u) {
-          const int32_t ag = acc[x][u][r] - rs, au = acc[x][u + HU][r] - rs;
-          const float gg = bf2f(f2bf((float)ag * (sw[u] * ad[r])));
-          const float uu = bf2f(f2bf((float)au * (sw[u + HU] * ad[r])));
-          const float gr = gg > 0.0f ? gg : 0.0f;
-          *reinterpret_cast<uint16_t*>(tile_lds + il * kPitch + ((HU * wn + u) * 32 + j) * 2) = f2bf(bf2f(f2bf(gr * gr)) * uu);
+          int8_t* const bu = base_x + (HU * wn + u) * 64;
+          const uint32_t g2 = f2bf_pair((float)(acc[x][u][r] - rsr[r]) * (sw[u] * ad[r]),
+                                        (float)(acc[x][u][r + 1] - rsr[r + 1]) * (sw[u] * ad[r + 1]));
+          const uint32_t u2 = f2bf_pair((float)(acc[x][u + HU][r] - rsr[r]) * (sw[u + HU] * ad[r]),
+                                        (float)(acc[x][u + HU][r + 1] - rsr[r + 1]) * (sw[u + HU] * ad[r + 1]));
+          const float g0 = fmaxf(bf2f((uint16_t)g2), 0.0f), g1 = fmaxf(bf2f((uint16_t)(g2 >> 16)), 0.0f);
+          const uint32_t sq = f2bf_pair(g0 * g0, g1 * g1);
+          const uint32_t o = f2bf_pair(bf2f((uint16_t)sq) * bf2f((uint16_t)u2),
+                                       bf2f((uint16_t)(sq >> 16)) * bf2f((uint16_t)(u2 >> 16)));
+          *reinterpret_cast<uint16_t*>(bu + off0) = (uint16_t)o;
+          *reinterpret_cast<uint16_t*>(bu + off1) = (uint16_t)(o >> 16);
         }
       } else {
 #pragma unroll
         for (int u = 0; u < US; ++u) {
-          const int32_t v = acc[x][u][r] - rs;
-          *reinterpret_cast<uint16_t*>(tile_lds + il * kPitch + (slot[u] * 32 + j) * 2) = f2bf((float)v * (sw[u] * ad[r]));
+          int8_t* const bu = base_x + slot[u] * 64;
+          const uint32_t o = f2bf_pair((float)(acc[x][u][r] - rsr[r]) * (sw[u] * ad[r]),
+                                       (float)(acc[x][u][r + 1] - rsr[r + 1]) * (sw[u] * ad[r + 1]));
+          *reinterpret_cast<uint16_t*>(bu + off0) = (uint16_t)o;
+          *reinterpret_cast<uint16_t*>(bu + off1) = (uint16_t)(o >> 16);
         }
       }
     }
   }
-  barrier_only();
+  BTL_TRACE_AT(11);
+  lds_barrier();  // the output tile is complete
   constexpr int kChunksPerRow = kOutCols / 8;
   constexpr int kPerThread = kPfRB * 32 * kChunksPerRow / 256;
   const int col_base = gn * kOutCols;
@@ -652,6 +676,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
     }
     *reinterpret_cast<uint4*>(p.out + (int64_t)i * p.n_out + col) = o;
   }
+  BTL_TRACE_AT(14);
 }
 
 // ------------------------------------------------------------- planning --
