@@ -16,8 +16,7 @@ static void launch_rows(unsigned rows, hipStream_t s, const ActArgs& p) {
   switch (act_cpt(p.K)) {
     case 1: hipLaunchKernelGGL((k_act_rows<NORM, QUANT, 1>), dim3(rows), dim3(kActThreads), 0, s, p); break;
     case 2: hipLaunchKernelGGL((k_act_rows<NORM, QUANT, 2>), dim3(rows), dim3(kActThreads), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((k_act_rows<NORM, QUANT, 4>), dim3(rows), dim3(kActThreads), 0, s, p); break;
-    default: hipLaunchKernelGGL((k_act_rows<NORM, QUANT, 8>), dim3(rows), dim3(kActThreads), 0, s, p); break;
+    default: hipLaunchKernelGGL((k_act_rows<NORM, QUANT, 4>), dim3(rows), dim3(kActThreads), 0, s, p); break;
   }
 }
 

@@ -9,12 +9,13 @@
 //   quant    (src/bitnet_tt/utils/quantization.py:60-91):
 //            a = max(max|y|, 1e-5); q = clip(rne(y * (127/a)), -128, 127)
 //
-// 256 threads (4 waves) work on a row.  The sum of squares follows a fixed
+// 512 threads (8 waves) work on a row.  The sum of squares follows a fixed
 // order so the statistic is reproducible bit for bit: thread t accumulates
-// x^2 over the 8-element chunks t, t+256, ... in order, the 64 lanes of a wave
-// combine by an xor butterfly (offsets 32..1), and the four wave sums combine
-// as (w0+w1)+(w2+w3).  Multiplies and adds are separately rounded (built with
-// -ffp-contract=off); division and sqrt are correctly rounded.
+// x^2 over the 8-element chunks t, t+512, ... in order, the 64 lanes of a wave
+// combine by an xor butterfly (offsets 32..1), and the eight wave sums
+// combine as ((w0+w1)+(w2+w3))+((w4+w5)+(w6+w7)).  Multiplies and adds are
+// separately rounded (built with -ffp-contract=off); division and sqrt are
+// correctly rounded.
 //
 // Quantised output layout (per 32-row block mb, 128-column superblock ks):
 // byte (((mb*KS + ks)*4 + q)*64 + lane)*16 + p holds q[mb*32 + (lane & 31)]
@@ -29,14 +30,21 @@
 
 namespace btl {
 
-constexpr int kActThreads = 256;
-constexpr int kActMaxChunks = BTL_MAX_K / 8 / kActThreads;  // 8 chunks of 8 per thread
+constexpr int kActThreads = 512;
+constexpr int kActWaves = kActThreads / 64;
+constexpr int kActMaxChunks = BTL_MAX_K / 8 / kActThreads;  // 4 chunks of 8 per thread
 
-// Chunks of 8 elements per thread for a row of K (1, 2, 4 or 8): the row code
+// Chunks of 8 elements per thread for a row of K (1, 2 or 4): the row code
 // is instantiated per bucket so a thread's loops cover only chunks it can own.
 inline int act_cpt(int64_t K) {
   const int64_t c = (K / 8 + kActThreads - 1) / kActThreads;
-  return c <= 1 ? 1 : c <= 2 ? 2 : c <= 4 ? 4 : 8;
+  return c <= 1 ? 1 : c <= 2 ? 2 : 4;
+}
+
+// Fixed combination order of the 8 wave partials (part of the numerics
+// contract: the oracle restates it).
+__device__ __forceinline__ float sum8_fixed(const float* s) {
+  return ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
 }
 
 struct ActArgs {
@@ -162,34 +170,22 @@ __device__ __forceinline__ void store8(int8_t* p, uint32_t lo, uint32_t hi) {
     *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
 }
 
-// 16-byte device-coherent store (write-through to the memory side, like the
-// agent-scope atomic stores above; there is no 128-bit atomic store type).
-// Completion is covered by wait_memory().
-__device__ __forceinline__ void store16_coherent(void* p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-  const u4 v = {a, b, c, d};
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
-}
-
 // Stores the quantised chunk c (8 bytes lo|hi) of row m.  Chunks c and c^1
-// (lanes t and t^1 of the same wave, both active) fill one 16-byte slot of the
-// operand layout: with COHERENT the even lane takes its neighbour's 8 bytes
-// and writes the slot with one 16-byte coherent store.
+// (lanes t and t^1 of one wave) fill one 16-byte slot of the operand layout,
+// so a wave's store instruction writes whole slots.  With COHERENT the store
+// is an agent-scope atomic one (write-through to the memory side), emitted by
+// the compiler, whose hazard checks cover its data registers (a hand-written
+// 16-byte store in inline asm is invisible to them: a VALU write of the store
+// data right after it corrupted the last lanes' bytes).
 template <bool COHERENT>
 __device__ __forceinline__ void store_chunk(int8_t* xa, int m, int c, int KS, uint32_t lo, uint32_t hi) {
-  if (COHERENT) {
-    const uint32_t lo_n = dpp_mov<0xB1>(lo);  // lane ^ 1
-    const uint32_t hi_n = dpp_mov<0xB1>(hi);
-    if ((c & 1) == 0) store16_coherent(xa + xa_offset(m, 8 * c, KS), lo, hi, lo_n, hi_n);
-  } else {
-    store8<false>(xa + xa_offset(m, 8 * c, KS), lo, hi);
-  }
+  store8<COHERENT>(xa + xa_offset(m, 8 * c, KS), lo, hi);
 }
 
 // ---- pieces of the row prologue shared by every kernel that runs it -------
 // A row lives in registers as v[i][0..7] = elements 8c..8c+7 of chunk
-// c = tid + 256*i; only chunks c < nch hold data.  Threads >= 256 of a block
-// hold nothing and only join the barriers.
+// c = tid + kActThreads*i (512 threads: all eight waves of the row's block);
+// only chunks c < nch hold data.
 
 // 1/sqrt(sum(v^2)/K + eps) in the fixed order described above (one barrier).
 template <int CPT>
@@ -210,7 +206,7 @@ __device__ __forceinline__ float row_rms_inv(const float (&v)[CPT][8], int nch, 
   s = wave_xor_sum(s);
   if (active && lane == 0) s_sum[wv] = s;
   __syncthreads();
-  const float ss = (s_sum[0] + s_sum[1]) + (s_sum[2] + s_sum[3]);
+  const float ss = sum8_fixed(s_sum);
   const float var = ss / (float)K;
   return 1.0f / sqrtf(var + eps);
 }
@@ -254,7 +250,9 @@ __device__ __forceinline__ float row_absmax(const float (&v)[CPT][8], int nch, f
   amax = wave_xor_max(amax);
   if (active && lane == 0) s_max[wv] = amax;
   __syncthreads();
-  const float a = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+  float a = s_max[0];
+#pragma unroll
+  for (int w = 1; w < kActWaves; ++w) a = fmaxf(a, s_max[w]);
   return a > act_eps ? a : act_eps;
 }
 
@@ -285,9 +283,9 @@ __device__ void act_row(const ActArgs& p, int m, int tid) {
   static_assert(CPT >= 1 && CPT <= kActMaxChunks, "chunks per thread");
   const bool active = tid < kActThreads;
   const int lane = tid & 63, wv = tid >> 6;
-  __shared__ float s_sum[4];
-  __shared__ float s_max[4];
-  __shared__ int s_int[4];
+  __shared__ float s_sum[kActWaves];
+  __shared__ float s_max[kActWaves];
+  __shared__ int s_int[kActWaves];
 
   if (p.zero_words && m == 0 && active)
     for (int i = tid; i < p.n_zero_words; i += kActThreads) {
@@ -393,7 +391,9 @@ __device__ void act_row(const ActArgs& p, int m, int tid) {
   if (active && lane == 0) s_int[wv] = rs;
   __syncthreads();
   if (tid == 0) {
-    const int32_t total = s_int[0] + s_int[1] + s_int[2] + s_int[3];
+    int32_t total = 0;
+#pragma unroll
+    for (int w = 0; w < kActWaves; ++w) total += s_int[w];
     if (COHERENT)
       st_coherent(p.rowsum + m, total);
     else

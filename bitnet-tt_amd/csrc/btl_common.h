@@ -60,6 +60,7 @@ struct GemmPlan {
   int waves;      // decode: waves per workgroup (4 or 8), splitting the slice's K
   int ngroups;    // decode: workgroups along N
   int splitk;     // decode: workgroups along K
+  int mh;         // fused decode: workgroups along M (2: 16 rows each)
   int64_t ws_bytes;
 };
 GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req);

@@ -446,8 +446,8 @@ template <int CQ, int CH, int CF>
 __global__ __launch_bounds__(512) void k_decode_layer(LayerArgs p) {
   __shared__ int32_t red[kLayerWaves * 2 * 16 * 64];
   __shared__ int32_t red_rs[kLayerWaves][32];
-  __shared__ float s_sum[4];
-  __shared__ float s_max[4];
+  __shared__ float s_sum[kActWaves];
+  __shared__ float s_max[kActWaves];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, b = blockIdx.x;
   const uint32_t E = p.epoch[b];
   const bool row_block = b < p.M;
@@ -653,9 +653,11 @@ int btl_decode_layer(int64_t M, int64_t H, int64_t Q, int64_t F, int64_t NQKV, c
     return set_error(BTL_ERR_WORKSPACE, "btl_decode_layer: workspace %zu < %lld bytes", workspace_bytes,
                      (long long)z.total);
   const int cq = act_cpt(Q), ch = act_cpt(H), cf = act_cpt(F);
+  // instances: small shapes, the 2B shapes (F = 6912), and K up to 16384
   const bool inst_small = cq == 1 && ch == 1 && cf == 1;
-  const bool inst_2b = cq == 2 && ch == 2 && cf == 4;
-  if (!inst_small && !inst_2b)
+  const bool inst_2b = cq == 1 && ch == 1 && cf == 2;
+  const bool inst_big = cq <= 2 && ch <= 2 && cf <= 4 && !inst_small && !inst_2b;
+  if (!inst_small && !inst_2b && !inst_big)
     return set_error(BTL_ERR_SHAPE, "btl_decode_layer: no kernel instance for H=%lld Q=%lld F=%lld", (long long)H,
                      (long long)Q, (long long)F);
   const btl_layer_weight_t* ws_in[kLayerOps] = {o_proj, gate_up, down, next_qkv};
@@ -703,6 +705,8 @@ int btl_decode_layer(int64_t M, int64_t H, int64_t Q, int64_t F, int64_t NQKV, c
   a.spin_limit = 1u << 17;
   hipStream_t s = (hipStream_t)stream;
   if (inst_2b)
+    launch_layer<1, 1, 2>(grid, s, a);
+  else if (inst_big)
     launch_layer<2, 2, 4>(grid, s, a);
   else
     launch_layer<1, 1, 1>(grid, s, a);

@@ -236,18 +236,19 @@ void orc_act_quant_absmax(const float* x, int64_t rows, int64_t k, float eps, in
 /* inference/generator_batch32.py:721-727):                             */
 /*   r = 1/sqrt(mean(x^2) + eps);  y = bf16(gamma * bf16(x * r)).       */
 /* order 0: sum of squares in double, r rounded once to float32.        */
-/* order 1: this build's fixed fp32 order -- 256 partial sums, partial  */
-/* t adding x^2 (rounded) over 8-element chunks c = t, t+256, ...;      */
+/* order 1: this build's fixed fp32 order -- 512 partial sums, partial  */
+/* t adding x^2 (rounded) over 8-element chunks c = t, t+512, ...;      */
 /* partials combined by the xor butterfly over 64 lanes (offsets        */
-/* 32..1) inside each of 4 groups, then (g0+g1)+(g2+g3);                 */
+/* 32..1) inside each of 8 groups, then                                 */
+/* ((g0+g1)+(g2+g3))+((g4+g5)+(g6+g7));                                 */
 /* var = ss / K, r = 1/sqrt(var + eps) with correctly rounded ops.      */
 /* ------------------------------------------------------------------ */
 static float rms_inv_blocked(const float* x, int64_t k, float eps) {
-  float part[256];
+  float part[512];
   int64_t nchunk = k / 8;
-  for (int t = 0; t < 256; ++t) {
+  for (int t = 0; t < 512; ++t) {
     float s = 0.0f;
-    for (int64_t c = t; c < nchunk; c += 256)
+    for (int64_t c = t; c < nchunk; c += 512)
       for (int j = 0; j < 8; ++j) {
         float v = x[c * 8 + j];
         float sq = v * v;
@@ -255,8 +256,8 @@ static float rms_inv_blocked(const float* x, int64_t k, float eps) {
       }
     part[t] = s;
   }
-  float grp[4];
-  for (int g = 0; g < 4; ++g) {
+  float grp[8];
+  for (int g = 0; g < 8; ++g) {
     float v[64], nv[64];
     for (int l = 0; l < 64; ++l) v[l] = part[g * 64 + l];
     for (int off = 32; off >= 1; off >>= 1) {
@@ -265,7 +266,7 @@ static float rms_inv_blocked(const float* x, int64_t k, float eps) {
     }
     grp[g] = v[0];
   }
-  float ss = (grp[0] + grp[1]) + (grp[2] + grp[3]);
+  float ss = ((grp[0] + grp[1]) + (grp[2] + grp[3])) + ((grp[4] + grp[5]) + (grp[6] + grp[7]));
   float var = ss / (float)k;
   float d = sqrtf(var + eps);
   return 1.0f / d;

@@ -234,12 +234,13 @@ def test_fused_decode_handshake_clean(orc):
         w = H.ternary(k, n, seed=n)
         ends = (n // 2, n) if epi == "relu2_mul" else (n,)
         pw = PackedTernaryWeight(device_weight(orc, w), k, n, (0.02,) * len(ends), ends)
-        for _ in range(3):
-            out = ternary_matmul(H.to_dev_bf16(xb), pw, epilogue=epi)
-        torch.cuda.synchronize()
         ref = orc.bitlinear(xb, w, [0.02] * len(ends), list(ends))
         exp = ref["out"] if epi == "none" else orc.relu2_mul_bf16(ref["out"][:, : n // 2], ref["out"][:, n // 2:])
-        assert np.array_equal(H.bits_of(out), exp)
+        for rep in range(6):  # every call checked: a row published before its stores landed shows up as one bad call
+            out = ternary_matmul(H.to_dev_bf16(xb), pw, epilogue=epi)
+            torch.cuda.synchronize()
+            bad = [i for i in range(m) if not np.array_equal(H.bits_of(out)[i], exp[i])]
+            assert not bad, f"m={m} k={k} n={n} call {rep}: rows {bad} differ"
     err = int(N.lib().btl_fused_error_offset())
     for key, ws in N._workspaces.items():
         if key[0] != "bitlinear":
