@@ -203,10 +203,12 @@ def prefill_mfma(torch, N, dev):
         o = torch.empty((M, Nf), dtype=torch.bfloat16, device=dev)
         sc, en, nseg = N.segments_arrays([0.02], [Nf])
         stream = N.stream_of(dev)
+        # split-K partials and counters (zero-filled once; every call leaves them clean)
+        ws = torch.zeros(max(int(L.btl_gemm_workspace_bytes(M, K, Nf, 0, 0)), 256), dtype=torch.uint8, device=dev)
 
         def launch(i):
             N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(a_dq), N.ptr(rowsum), M, K, Nf, N.ptr(wd[i % copies]), sc, en,
-                                    nseg, 0, None, N.ptr(o), None, None, 0, 1, stream), "prefill gemm")
+                                    nseg, 0, None, N.ptr(o), None, N.ptr(ws), ws.numel(), 0, stream), "prefill gemm")
 
         reps = 20
         s = torch.cuda.Stream(device=dev)

@@ -453,8 +453,18 @@ __device__ __forceinline__ void pf_issue(int8_t* stage_base, int stage_bytes, co
 
 // PRS: the row sums come in p.rowsum (the activation kernel's); without it
 // one wave per row block sums that block's operand bytes in the loop.
-template <int EPI, int RB, int WR, bool PRS>
+// SK (with PRS): p.splitk workgroups share each tile, superblocks split
+// evenly; each publishes its raw partial sums (coherent stores, then a
+// per-tile arrival counter) and the last to arrive adds the others' partials
+// -- integers, so any order gives the same result -- and runs the epilogue.
+// Nothing waits on another workgroup.
+template <int RB, int WR>
+constexpr int pf_partial_qwords() {  // 64-bit words of one workgroup's partial tile
+  return 4 * PfShape<RB, WR>::xr * PfShape<RB, WR>::us * 8 * 64;
+}
+template <int EPI, int RB, int WR, bool PRS, bool SK>
 __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, int ngn) {
+  static_assert(!SK || PRS, "split-K sums raw partials and subtracts the given row sums once");
   constexpr int ST = PfShape<RB, WR>::stages;
   constexpr int kPfRB = PfShape<RB, WR>::rb;
   constexpr int XR = PfShape<RB, WR>::xr;
@@ -463,8 +473,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   constexpr int kPfChunks = PfShape<RB, WR>::chunks;
   constexpr int kPfChunksPerWave = PfShape<RB, WR>::per_wave;
   // One LDS object: the stage buffers, then a_dq and the row sums of the
-  // tile's rows.
-  __shared__ __attribute__((aligned(16))) int8_t lds[ST * kPfChunks * 1024 + kPfRB * 32 * 8];
+  // tile's rows, then the split-K arrival flag.
+  __shared__ __attribute__((aligned(16))) int8_t lds[ST * kPfChunks * 1024 + kPfRB * 32 * 8 + 16];
+  int* s_last = reinterpret_cast<int*>(lds + ST * kPfChunks * 1024 + kPfRB * 32 * 8);
   int8_t (*stage)[kPfChunks * 1024] = reinterpret_cast<int8_t (*)[kPfChunks * 1024]>(lds);
   float* s_adq = reinterpret_cast<float*>(lds + ST * kPfChunks * 1024);
   int32_t* s_rs = reinterpret_cast<int32_t*>(lds + ST * kPfChunks * 1024 + kPfRB * 32 * 4);
@@ -473,15 +484,21 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   // select over both sides)
   const int wm = __builtin_amdgcn_readfirstlane(wv % WR), wn = __builtin_amdgcn_readfirstlane(wv / WR);
   const int ntiles = ngm * ngn;
-  const int per = (ntiles + kPfXcds - 1) / kPfXcds;
-  const int t = (int)(blockIdx.x % kPfXcds) * per + (int)(blockIdx.x / kPfXcds);
-  if (t >= ntiles) return;
+  const int nsplit = SK ? p.splitk : 1;
+  const int nunits = ntiles * nsplit;  // a tile's splits are consecutive units
+  const int per = (nunits + kPfXcds - 1) / kPfXcds;
+  const int unit = (int)(blockIdx.x % kPfXcds) * per + (int)(blockIdx.x / kPfXcds);
+  if (unit >= nunits) return;
+  const int t = unit / nsplit, sp = unit % nsplit;
   const int grp = t / (kPfGroupRows * ngn);            // group of kPfGroupRows row tiles
   const int rows_in = min(kPfGroupRows, ngm - grp * kPfGroupRows);
   const int r = t - grp * kPfGroupRows * ngn;
   const int gm = grp * kPfGroupRows + r % rows_in;
   const int gn = r / rows_in;
-  const int KS = p.KS;
+  // this workgroup's superblocks [sb0, sb0 + KS) of the p.KS
+  const int sb0 = SK ? (sp * p.KS) / nsplit : 0;
+  const int KS = SK ? ((sp + 1) * p.KS) / nsplit - sb0 : p.KS;
+  const int KSall = p.KS;  // row stride of the operand layouts
 
   // Global source of this wave's chunks at superblock 0; a superblock
   // advances activation chunks by 4 KiB and weight chunks by 1 KiB.
@@ -493,11 +510,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
     if (c < kPfRB * 4) {
       int mb = gm * kPfRB + (c >> 2);
       mb = mb < p.Mb ? mb : p.Mb - 1;
-      src[i] = p.xa + ((((int64_t)mb * KS) * 4 + (c & 3)) * 64 + lane) * 16;
+      src[i] = p.xa + ((((int64_t)mb * KSall + sb0) * 4 + (c & 3)) * 64 + lane) * 16;
       step[i] = 4096;
     } else {
       const int tile = pf_tile<EPI>(p, gn, c - kPfRB * 4);
-      src[i] = reinterpret_cast<const int8_t*>(p.wdev) + (((int64_t)tile * KS) * 64 + lane) * 16;
+      src[i] = reinterpret_cast<const int8_t*>(p.wdev) + (((int64_t)tile * KSall + sb0) * 64 + lane) * 16;
       step[i] = 1024;
     }
   }
@@ -555,6 +572,44 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
       }
     }
     if (ks == KS - 1) BTL_TRACE_AT(13);
+  }
+
+  if (SK && nsplit > 1) {
+    // Publish this split's partial tile: lane-contiguous 64-bit words
+    // (registers r, r + 1 of accumulator (x, u)), one block per split.
+    constexpr int kQ = pf_partial_qwords<RB, WR>();
+    uint64_t* const part = reinterpret_cast<uint64_t*>(p.ws_part);
+    uint64_t* const mine = part + (int64_t)(t * nsplit + sp) * kQ;
+#pragma unroll
+    for (int x = 0; x < XR; ++x)
+#pragma unroll
+      for (int u = 0; u < US; ++u)
+#pragma unroll
+        for (int r2 = 0; r2 < 8; ++r2)
+          st_coherent(mine + (((wv * XR + x) * US + u) * 8 + r2) * 64 + lane,
+                      (uint64_t)(uint32_t)acc[x][u][2 * r2] | ((uint64_t)(uint32_t)acc[x][u][2 * r2 + 1] << 32));
+    wait_memory();
+    __syncthreads();  // the whole partial is out before the arrival is counted
+    if (tid == 0) *s_last = atomicAdd(p.ws_cnt + t, 1u) == (unsigned)(nsplit - 1);
+    __syncthreads();
+    if (!*s_last) return;
+    // Last to arrive: every other split's partial is out (its counter
+    // increment followed its acknowledged stores); add them.
+    for (int o = 0; o < nsplit; ++o) {
+      if (o == sp) continue;
+      const uint64_t* const other = part + (int64_t)(t * nsplit + o) * kQ;
+#pragma unroll
+      for (int x = 0; x < XR; ++x)
+#pragma unroll
+        for (int u = 0; u < US; ++u)
+#pragma unroll
+          for (int r2 = 0; r2 < 8; ++r2) {
+            const uint64_t v = ld_coherent(other + (((wv * XR + x) * US + u) * 8 + r2) * 64 + lane);
+            acc[x][u][2 * r2] += (int32_t)(uint32_t)v;
+            acc[x][u][2 * r2 + 1] += (int32_t)(uint32_t)(v >> 32);
+          }
+    }
+    if (tid == 0) st_coherent(p.ws_cnt + t, 0u);  // the workspace is left clean for the next call
   }
 
   // Epilogue in two passes through LDS (the stage buffers are free now):
@@ -759,11 +814,44 @@ static GemmPlan plan_decode(int64_t K, int64_t N, int epilogue, int splitk_req, 
   return pl;
 }
 
+// Prefill tiling: 128-row tiles unless they would leave CUs idle, then
+// 64-row tiles; a 64-row grid smaller than the CU count splits K (kernels
+// given row sums only) up to about one workgroup per CU, at least 4
+// superblocks each.  Measured on MI355X at M = 512: K = 6912, N = 2560
+// 32.7 -> 21.7 us (3 splits); two workgroups per CU instead is slower at
+// every shape (the finishing workgroup reads S - 1 partials of 64 KiB).
+struct PfGrid {
+  int rb, ngm, ngn, splitk;
+};
+static PfGrid pf_grid(int64_t M, int64_t K, int64_t N, int epilogue) {
+  PfGrid g;
+  const int Mb = (int)mblocks(M), NT = (int)(N / 32), KS = (int)ksb(K);
+  g.ngn = (epilogue == BTL_EPI_RELU2_MUL) ? (NT / 2 + 3) / 4 : (NT + kPfCT - 1) / kPfCT;
+  const int cus = device_cus();
+  g.rb = ((Mb + 3) / 4) * g.ngn >= cus ? 4 : 2;
+  g.ngm = (Mb + g.rb - 1) / g.rb;
+  const int ntiles = g.ngm * g.ngn;
+  g.splitk = 1;
+  if (g.rb == 2 && ntiles <= cus) {
+    int sk = cus / ntiles;
+    if (sk > KS / 4) sk = KS / 4;
+    if (sk > 8) sk = 8;
+    g.splitk = sk > 1 ? sk : 1;
+  }
+  return g;
+}
+
 GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req) {
   if (M > 32) {
     GemmPlan pl = {};
     pl.prefill = true;
-    pl.splitk = 1;
+    const PfGrid g = pf_grid(M, K, N, epilogue);
+    pl.splitk = g.splitk;
+    pl.ngroups = g.ngm * g.ngn;  // tiles: one arrival counter each
+    pl.ws_bytes = 0;
+    if (g.splitk > 1)
+      pl.ws_bytes = round_up((int64_t)pl.ngroups * 4, 256) +
+                    (int64_t)pl.ngroups * g.splitk * pf_partial_qwords<2, 1>() * 8;
     return pl;
   }
   return plan_decode(K, N, epilogue, splitk_req, decode_waves(), device_cus());
@@ -903,35 +991,40 @@ static GemmArgs gemm_args(const int8_t* xa, const float* a_dq, const int32_t* ro
   a.splitk = pl.splitk;
   a.mh = pl.mh == 2 ? 2 : 1;
   a.ngroups = pl.ngroups;
-  if (!pl.prefill && pl.splitk > 1) {
+  if (pl.splitk > 1) {  // decode split-K, or prefill split-K (per tile)
     a.ws_cnt = reinterpret_cast<uint32_t*>(ws);
     a.ws_part = reinterpret_cast<int32_t*>(ws + round_up((int64_t)pl.ngroups * 4, 256));
   }
   return a;
 }
 
-template <bool PRS>
-static void launch_prefill(int epilogue, int rb, dim3 grid, hipStream_t s, const GemmArgs& a, int ngm, int ngn) {
-  if (epilogue == BTL_EPI_RELU2_MUL) {
+template <int EPI>
+static void launch_prefill_epi(bool prs, int rb, bool sk, dim3 grid, hipStream_t s, const GemmArgs& a, int ngm,
+                               int ngn) {
+  if (!prs) {
     if (rb == 4)
-      hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2, 4, 2, PRS>), grid, dim3(256), 0, s, a, ngm, ngn);
+      hipLaunchKernelGGL((k_gemm_prefill<EPI, 4, 2, false, false>), grid, dim3(256), 0, s, a, ngm, ngn);
     else
-      hipLaunchKernelGGL((k_gemm_prefill<EPI_RELU2, 2, 1, PRS>), grid, dim3(256), 0, s, a, ngm, ngn);
+      hipLaunchKernelGGL((k_gemm_prefill<EPI, 2, 1, false, false>), grid, dim3(256), 0, s, a, ngm, ngn);
+  } else if (rb == 4) {
+    hipLaunchKernelGGL((k_gemm_prefill<EPI, 4, 2, true, false>), grid, dim3(256), 0, s, a, ngm, ngn);
+  } else if (sk) {
+    hipLaunchKernelGGL((k_gemm_prefill<EPI, 2, 1, true, true>), grid, dim3(256), 0, s, a, ngm, ngn);
   } else {
-    if (rb == 4)
-      hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE, 4, 2, PRS>), grid, dim3(256), 0, s, a, ngm, ngn);
-    else
-      hipLaunchKernelGGL((k_gemm_prefill<EPI_SCALE, 2, 1, PRS>), grid, dim3(256), 0, s, a, ngm, ngn);
+    hipLaunchKernelGGL((k_gemm_prefill<EPI, 2, 1, true, false>), grid, dim3(256), 0, s, a, ngm, ngn);
   }
 }
 
 static int launch_gemm(const GemmArgs& a, int epilogue, const GemmPlan& pl, hipStream_t s) {
   if (pl.prefill) {
-    const int ngn = (epilogue == BTL_EPI_RELU2_MUL) ? (a.NT / 2 + 3) / 4 : (a.NT + kPfCT - 1) / kPfCT;
-    // 128-row tiles unless they would leave CUs idle
-    const int rb = ((a.Mb + 3) / 4) * ngn >= device_cus() ? 4 : 2;
-    const int ngm = (a.Mb + rb - 1) / rb;
-    const int per = (ngm * ngn + kPfXcds - 1) / kPfXcds;
+    const PfGrid g = pf_grid(a.M, (int64_t)a.KS * 128, a.N, epilogue);
+    const int ngm = g.ngm, ngn = g.ngn, rb = g.rb;
+    // split-K runs with the given row sums (partials are raw sums; the row sum
+    // is subtracted once, by the workgroup that finishes the tile)
+    const bool sk = a.rowsum && a.splitk > 1;
+    GemmArgs b = a;
+    if (!sk) b.splitk = 1;
+    const int per = (ngm * ngn * b.splitk + kPfXcds - 1) / kPfXcds;
     dim3 grid((unsigned)(per * kPfXcds));
     // Every wave takes two row blocks, so each unpacked weight operand feeds
     // two MFMAs: 64-row tiles run the 1 x 4 wave grid (2 column slots per
@@ -939,10 +1032,10 @@ static int launch_gemm(const GemmArgs& a, int epilogue, const GemmPlan& pl, hipS
     // the 2B shapes, one row block per wave is 5-9 % slower (VALU unpacking
     // that does not overlap the MFMAs) and four per wave ~10 % slower (LDS
     // reads and 237 VGPRs).
-    if (a.rowsum)
-      launch_prefill<true>(epilogue, rb, grid, s, a, ngm, ngn);
+    if (epilogue == BTL_EPI_RELU2_MUL)
+      launch_prefill_epi<EPI_RELU2>(a.rowsum != nullptr, rb, sk, grid, s, b, ngm, ngn);
     else
-      launch_prefill<false>(epilogue, rb, grid, s, a, ngm, ngn);
+      launch_prefill_epi<EPI_SCALE>(a.rowsum != nullptr, rb, sk, grid, s, b, ngm, ngn);
     return check_launch("ternary gemm (prefill)");
   }
   const int nsb = decode_nsb(pl, a.KS, epilogue);

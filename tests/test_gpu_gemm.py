@@ -176,6 +176,44 @@ def test_prefill_relu2_bit_exact(orc, m, k, f, rowsum):
     assert np.array_equal(out, expected_out(orc, acc, a_dq, scales, ends, 1))
 
 
+@pytest.mark.parametrize("m,k,n,epi", [(64, 2048, 256, 0), (100, 1536, 160, 0), (70, 2048, 192, 1), (130, 992, 96, 0),
+                                       (33, 6912, 64, 0)])
+def test_prefill_splitk_bit_exact(orc, m, k, n, epi):
+    """Prefill grids smaller than the CU count split K between workgroups
+    (given row sums); the last workgroup of a tile adds the others' exact
+    partials.  Two calls in a row on one workspace, counters left at zero."""
+    L = N.lib()
+    assert int(L.btl_choose_splitk(m, k, n, epi)) > 1, "shape should take the split-K path"
+    print(f"prefill split-K m={m} k={k} n={n} epi={epi}", flush=True)
+    rng = np.random.default_rng(m * 3 + k)
+    q = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
+    w = H.ternary(k, n, seed=k + 7)
+    scales = [0.02] if epi == 0 else [0.021, 0.017]
+    ends = [n] if epi == 0 else [n // 2, n]
+    d = H.dev()
+    rows = 32 * ((m + 31) // 32)
+    a_dq = np.zeros(rows, np.float32)
+    a_dq[:m] = (0.005 + 0.03 * rng.random(m)).astype(np.float32)
+    xa, a_dq_d, wdev = H.to_dev(H.rowmajor_to_xa(q)), H.to_dev(a_dq), device_weight(orc, w)
+    rs_d = H.to_dev(q.astype(np.int64).sum(1).astype(np.int32))
+    sc, en, nseg = N.segments_arrays(scales, ends)
+    ws_bytes = int(L.btl_gemm_workspace_bytes(m, k, n, epi, 0))
+    assert ws_bytes > 0
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=d)
+    ref = orc.gemm_i8t(q, w)
+    for call in range(2):
+        n_out = n // 2 if epi == 1 else n
+        out = torch.empty((m, n_out), dtype=torch.bfloat16, device=d)
+        acc = torch.empty((m, n), dtype=torch.int32, device=d)
+        N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(a_dq_d), N.ptr(rs_d), m, k, n, N.ptr(wdev), sc, en, nseg, epi, None,
+                                N.ptr(out), N.ptr(acc), N.ptr(ws), ws.numel(), 0, N.stream_of(d)), "btl_gemm_i8t2")
+        torch.cuda.synchronize()
+        assert np.array_equal(acc.cpu().numpy(), ref), f"call {call}: accumulators"
+        assert np.array_equal(H.bits_of(out), expected_out(orc, ref, a_dq[:m], scales, ends, epi)), f"call {call}: out"
+        # the per-tile arrival counters lead the workspace (256 bytes here); the partials follow them
+        assert not ws[:256].cpu().numpy().any(), f"call {call}: arrival counters not back at zero"
+
+
 @pytest.mark.parametrize("m,k,n,epi,rowsum", [(512, 2560, 3840, 0, False), (512, 2560, 13824, 1, True),
                                               (2048, 2560, 6912, 0, True), (2048, 6912, 2560, 0, False),
                                               (2048, 6912, 2560, 0, True), (512, 2560, 2560, 0, True)])
