@@ -141,9 +141,11 @@ int btl_rmsnorm(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint
  * src/bitnet_tt/layers/ffn.py:22-34).  out: [M, N] (SCALE) or [M, N/2]
  * (RELU2_MUL) bf16; residual: optional [M, N] bf16 (SCALE only; may equal
  * out).  acc_out: optional [M, N] int32 copy of the exact accumulators.
- * splitk: 0 = library's choice.  workspace: btl_gemm_workspace_bytes(...)
- * bytes; its counters must be zero before the first call and are left zero
- * by every completed call.                                                 */
+ * splitk: 0 = library's choice (M <= 32); for M > 32 the library splits K
+ * itself when the tile grid is smaller than the CU count and rowsum is
+ * given.  workspace: btl_gemm_workspace_bytes(...) bytes (split-K partials
+ * and counters; 0 for shapes that never split); its counters must be zero
+ * before the first call and are left zero by every completed call.        */
 int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, const int32_t* rowsum, int64_t M, int64_t K, int64_t N, const uint32_t* wdev,
                   const float* seg_scale, const int64_t* seg_end, int nseg, int epilogue, const uint16_t* residual, uint16_t* out, int32_t* acc_out, void* workspace,
                   size_t workspace_bytes, int splitk, btl_stream_t stream);
