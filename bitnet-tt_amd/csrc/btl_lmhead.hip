@@ -6,12 +6,13 @@
 //
 // The head is 656 MB of bf16 at the 2B shape, more bytes than every BitLinear
 // of a step together, so the kernel is a weight stream:
-//  * the weights are repacked once into MFMA operand order: 32 vocab rows x
-//    16 k per KiB, lane l holding W[row l & 31][k0 + 8 (l >> 5) .. + 8], so a
+//  * the weights are repacked once into MFMA operand order: 16 vocab rows x
+//    32 k per KiB, lane l holding W[row l & 15][k0 + 8 (l >> 4) .. + 8], so a
 //    wave's operand is one coalesced 16-byte load per lane;
-//  * one workgroup per CU walks vocab tiles of 32 rows; its eight waves split
+//  * one workgroup per CU walks vocab tiles of 16 rows; its eight waves split
 //    K, each keeping its slice of the (up to 32) normalised rows in registers
-//    for the whole launch, and run v_mfma_f32_32x32x16_bf16;
+//    for the whole launch, and run v_mfma_f32_16x16x32_bf16 (one or two
+//    16-row blocks);
 //  * the loads of the next tile are issued before the previous tile's partial
 //    sums are reduced through LDS, so the reduction runs under them;
 //  * every thread keeps the best (value, first index) of its two rows; the
