@@ -134,6 +134,27 @@ __device__ __forceinline__ void epi_relu2(const GemmArgs& p, int i, int ng, int 
 enum { EPI_SCALE = BTL_EPI_SCALE, EPI_RELU2 = BTL_EPI_RELU2_MUL };
 
 // ------------------------------------------------------------- decode ----
+// Poll wave of a fused GEMM workgroup: wait until the activation rows this
+// workgroup reads (all of them, or row half h when mh = 2) carry this
+// launch's number, then record the number in the workgroup's seen slots.
+// A bounded spin: on time-out the error word is set and the wave goes on.
+__device__ __forceinline__ void wait_rows_ready(const FusedSync& fs, int bid, int mh, int h, int lane) {
+  const uint32_t e = ld_coherent(seen_word(fs, bid)) + 1u;  // this launch's number
+  unsigned n = 0;
+  for (;;) {
+    const bool mine = lane >= fs.nact || (mh == 2 && (lane >> 4) != h) ||
+                      (int32_t)(ld_coherent(ready_word(fs, lane)) - e) >= 0;
+    if (__all(mine)) break;
+    if (++n > fs.spin_limit) {
+      if (lane == 0) st_coherent(sync_word(fs, kErrorWord), 1u);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  // after the wait: stores count in the same wait counter as the polls
+  for (int j = bid + lane * fs.ngemm; j < kGemmSlots; j += 64 * fs.ngemm) st_coherent(seen_word(fs, j), e);
+}
+
 // GEMM workgroup of the decode path.  With FUSED the activations come from
 // workgroups of the same launch: wait for them after the weight loads of the
 // first pass are in flight, and read activations and scales coherently.
@@ -195,22 +216,7 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
   float ad_pre[RR];
   if (FUSED) {
     // Every thread of the workgroup reaches this barrier, with or without work.
-    if (wv == WAVES - 1) {
-      const uint32_t e = ld_coherent(seen_word(fs, bid)) + 1u;  // this launch's number
-      unsigned n = 0;
-      for (;;) {
-        const bool mine = lane >= fs.nact || (p.mh == 2 && (lane >> 4) != h) ||
-                          (int32_t)(ld_coherent(ready_word(fs, lane)) - e) >= 0;
-        if (__all(mine)) break;
-        if (++n > fs.spin_limit) {
-          if (lane == 0) st_coherent(sync_word(fs, kErrorWord), 1u);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-      }
-      // after the wait: stores count in the same wait counter as the polls
-      for (int j = bid + lane * fs.ngemm; j < kGemmSlots; j += 64 * fs.ngemm) st_coherent(seen_word(fs, j), e);
-    }
+    if (wv == WAVES - 1) wait_rows_ready(fs, bid, p.mh, h, lane);
     __syncthreads();
     // Scales of the rows this thread finishes, loaded with the activations.
 #pragma unroll
@@ -332,6 +338,98 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
   }
 }
 
+// GEMM workgroup of a fused row-half launch (mh = 2) with one column tile and
+// the scale epilogue: rows 16h..16h+15 of the token tile against the 32
+// columns of tile g, on v_mfma_i32_16x16x64_i8 (two MFMAs, columns 0-15 and
+// 16-31, per 64 k).  The 32-row MFMA would spend half its cycles on the other
+// half's zero rows.
+//  * A: lane l takes row 16h + (l & 15), k-group l >> 4 of a 64-k step
+//    straight from the MFMA-order tile: k-group G of step p is 32-k step
+//    2p + (G >> 1), half G & 1, i.e. tile lane 16h + (l & 15) + 32 (G & 1).
+//  * B: the device layout gives lane l column l & 31, half l >> 5 of each
+//    32-k step.  A 32-lane swap and then a 16-lane swap of the packed words
+//    of steps 2p and 2p+1 give, in 16-lane rows r of (step, lanes),
+//    [2p.r0 | 2p.r2 | 2p+1.r0 | 2p+1.r2] (columns 0-15) and
+//    [2p.r1 | 2p.r3 | 2p+1.r1 | 2p+1.r3] (columns 16-31): lane l then holds
+//    column (l & 15) (+16) with the k-group of its A operand.
+//  * C: lane l, element j is row 4 (l >> 4) + j, column l & 15.
+template <int NSB, int WAVES>
+__device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs) {
+  __shared__ int32_t red[WAVES][8][64];
+  __shared__ int32_t red_rs[WAVES][16];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tile = bid % p.ngroups;
+  const int h = bid / p.ngroups;
+  // the last wave only polls (as in gemm_decode_wg); the others share K
+  constexpr int KW = WAVES - 1;
+  const int wb = wv < KW ? (wv * p.KS) / KW : p.KS;
+  const int we = wv < KW ? ((wv + 1) * p.KS) / KW : p.KS;
+
+  v4i b[NSB];
+  auto load_b = [&](int base, int cnt) {
+#pragma unroll
+    for (int i = 0; i < NSB; ++i) {
+      const int sb = base + (i < cnt ? i : cnt - 1);
+      b[i] = ld128(p.wdev + (((int64_t)tile * p.KS + sb) * 64 + lane) * 4);
+    }
+  };
+  if (wb < we) load_b(wb, (we - wb) < NSB ? (we - wb) : NSB);
+
+  // the output element this thread finishes: row 16h + er, column tile*32 + ec
+  const int er = tid >> 5, ec = tid & 31;
+  const int row = 16 * h + er, col = tile * 32 + ec;
+  const uint16_t res = residual_at(p, row, col);
+  if (wv == WAVES - 1) wait_rows_ready(fs, bid, 2, h, lane);
+  __syncthreads();
+  const float ad = ld_coherent(p.a_dq + row);
+
+  v4i acc0 = (v4i){0, 0, 0, 0}, acc1 = (v4i){0, 0, 0, 0};
+  int32_t rs_lane = 0;  // sum of this lane's A bytes (row 16h + (l & 15))
+  const int a_lane = 16 * h + (lane & 15) + 32 * ((lane >> 4) & 1);
+  const int a_step = lane >> 5;
+  for (int base = wb; base < we; base += NSB) {
+    const int cnt = (we - base) < NSB ? (we - base) : NSB;
+    if (base != wb) load_b(base, cnt);
+    v4i a[NSB][2];
+#pragma unroll
+    for (int i = 0; i < NSB; ++i) {
+      const int sb = base + (i < cnt ? i : cnt - 1);
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) a[i][pp] = ld128(p.xa + ((sb * 4 + 2 * pp + a_step) * 64 + a_lane) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < NSB; ++i) {
+      if (i < cnt) {
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+          const auto s32 = __builtin_amdgcn_permlane32_swap((uint32_t)b[i][2 * pp], (uint32_t)b[i][2 * pp + 1], false, false);
+          const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
+          acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[0]), acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[1]), acc1, 0, 0, 0);
+          rs_lane = bytes_sum(a[i][pp], rs_lane);
+        }
+      }
+    }
+  }
+  {
+    // a row's bytes are spread over lanes l, l ^ 16, l ^ 32, l ^ 48
+    int32_t rs = rs_lane + (int32_t)xor_partner_u<16>((uint32_t)rs_lane);
+    rs += (int32_t)xor_partner_u<32>((uint32_t)rs);
+    if (lane < 16) red_rs[wv][lane] = rs;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    red[wv][j][lane] = acc0[j];
+    red[wv][4 + j][lane] = acc1[j];
+  }
+  __syncthreads();
+  const int reg = 4 * (ec >> 4) + (er & 3), src = 16 * (er >> 2) + (ec & 15);
+  int32_t v = 0;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) v += red[w][reg][src] - red_rs[w][er];
+  if (row < p.M) epi_scale(p, row, col, v, ad, res);
+}
+
 template <int TPW, int NSB, int EPI, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void k_gemm_decode(GemmArgs p) {
   gemm_decode_wg<TPW, NSB, EPI, WAVES, false>(p, blockIdx.x, FusedSync{});
@@ -350,6 +448,12 @@ __global__ __launch_bounds__(512) void k_bitlinear_decode(GemmArgs p, ActArgs a,
     __syncthreads();
     if (threadIdx.x == 0) st_coherent(ready, e);
     return;
+  }
+  if constexpr (TPW == 1 && EPI == EPI_SCALE) {
+    if (p.mh == 2) {
+      gemm_decode_half<NSB, 8>(p, blockIdx.x - fs.nact, fs);
+      return;
+    }
   }
   gemm_decode_wg<TPW, NSB, EPI, 8, true>(p, blockIdx.x - fs.nact, fs);
 }
