@@ -167,13 +167,7 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
   __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int g = bid % p.ngroups;
-  const int s = (bid / p.ngroups) % p.splitk;
-  // Row half of this workgroup (mh = 2): it loads and finishes rows
-  // 16h..16h+15 only.  The MFMA keeps its 32-row shape with the other
-  // half's operand lanes zero, so each workgroup reads half the activation
-  // tile (lane l holds row l & 31).
-  const int h = bid / (p.ngroups * p.splitk);
-  const bool rows_mine = p.mh == 1 || ((lane & 31) >> 4) == h;
+  const int s = bid / p.ngroups;
 
   int tile[TPW];
 #pragma unroll
@@ -216,7 +210,7 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
   float ad_pre[RR];
   if (FUSED) {
     // Every thread of the workgroup reaches this barrier, with or without work.
-    if (wv == WAVES - 1) wait_rows_ready(fs, bid, p.mh, h, lane);
+    if (wv == WAVES - 1) wait_rows_ready(fs, bid, 1, 0, lane);
     __syncthreads();
     // Scales of the rows this thread finishes, loaded with the activations.
 #pragma unroll
@@ -238,7 +232,7 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
         // (by this launch's activation blocks, before their ready flags) and
         // caches start clean at every kernel boundary, so each XCD's L2
         // fetches it once for all of its CUs
-        a[i][q] = rows_mine ? ld128(p.xa + off) : (v4i){0, 0, 0, 0};
+        a[i][q] = ld128(p.xa + off);
       }
     }
 #pragma unroll
@@ -327,7 +321,7 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
 #pragma unroll
   for (int rr = 0; rr < RR; ++rr) {
     const int i = acc_row(wv + WAVES * rr, lane);
-    if (i >= p.M || (p.mh == 2 && (i >> 4) != h)) continue;
+    if (i >= p.M) continue;
     const float ad = ad_row[rr];
     if (EPI == EPI_RELU2) {
       epi_relu2(p, i, tile[0] * 32 + j, tile[1] * 32 + j, v[0][rr], v[1][rr], ad);
@@ -338,11 +332,11 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
   }
 }
 
-// GEMM workgroup of a fused row-half launch (mh = 2) with one column tile and
-// the scale epilogue: rows 16h..16h+15 of the token tile against the 32
-// columns of tile g, on v_mfma_i32_16x16x64_i8 (two MFMAs, columns 0-15 and
-// 16-31, per 64 k).  The 32-row MFMA would spend half its cycles on the other
-// half's zero rows.
+// GEMM workgroup of a fused row-half launch (mh = 2): rows 16h..16h+15 of
+// the token tile against TPW column tiles of 32 (scale epilogue: tiles
+// g*TPW ..; relu2: gate tile g and its up tile), on
+// v_mfma_i32_16x16x64_i8, two MFMAs (columns 0-15 and 16-31) per tile and
+// 64 k.  A 32-row MFMA would spend half its cycles on the other half's rows.
 //  * A: lane l takes row 16h + (l & 15), k-group l >> 4 of a 64-k step
 //    straight from the MFMA-order tile: k-group G of step p is 32-k step
 //    2p + (G >> 1), half G & 1, i.e. tile lane 16h + (l & 15) + 32 (G & 1).
@@ -353,37 +347,50 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
 //    [2p.r1 | 2p.r3 | 2p+1.r1 | 2p+1.r3] (columns 16-31): lane l then holds
 //    column (l & 15) (+16) with the k-group of its A operand.
 //  * C: lane l, element j is row 4 (l >> 4) + j, column l & 15.
-template <int NSB, int WAVES>
+template <int TPW, int NSB, int EPI, int WAVES>
 __device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs) {
-  __shared__ int32_t red[WAVES][8][64];
+  static_assert(EPI == EPI_SCALE ? (TPW == 1 || TPW == 2) : TPW == 2, "tiles per workgroup");
+  static_assert(WAVES * 64 == 512, "one output element per thread and tile");
+  __shared__ int32_t red[WAVES][TPW][8][64];
   __shared__ int32_t red_rs[WAVES][16];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int tile = bid % p.ngroups;
+  const int g = bid % p.ngroups;
   const int h = bid / p.ngroups;
+  int tile[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    constexpr int HP = TPW / 2;  // relu2: gate tiles t < HP, up tiles t >= HP
+    tile[t] = EPI == EPI_RELU2 ? (t < HP ? g * HP + t : (p.NT >> 1) + g * HP + (t - HP)) : g * TPW + t;
+  }
   // the last wave only polls (as in gemm_decode_wg); the others share K
   constexpr int KW = WAVES - 1;
   const int wb = wv < KW ? (wv * p.KS) / KW : p.KS;
   const int we = wv < KW ? ((wv + 1) * p.KS) / KW : p.KS;
 
-  v4i b[NSB];
+  v4i b[TPW][NSB];
   auto load_b = [&](int base, int cnt) {
 #pragma unroll
     for (int i = 0; i < NSB; ++i) {
       const int sb = base + (i < cnt ? i : cnt - 1);
-      b[i] = ld128(p.wdev + (((int64_t)tile * p.KS + sb) * 64 + lane) * 4);
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) b[t][i] = ld128(p.wdev + (((int64_t)tile[t] * p.KS + sb) * 64 + lane) * 4);
     }
   };
   if (wb < we) load_b(wb, (we - wb) < NSB ? (we - wb) : NSB);
 
-  // the output element this thread finishes: row 16h + er, column tile*32 + ec
+  // the output elements this thread finishes: row 16h + er, column ec of every tile
   const int er = tid >> 5, ec = tid & 31;
-  const int row = 16 * h + er, col = tile * 32 + ec;
-  const uint16_t res = residual_at(p, row, col);
+  const int row = 16 * h + er;
+  uint16_t res[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) res[t] = EPI == EPI_SCALE ? residual_at(p, row, tile[t] * 32 + ec) : 0;
   if (wv == WAVES - 1) wait_rows_ready(fs, bid, 2, h, lane);
   __syncthreads();
   const float ad = ld_coherent(p.a_dq + row);
 
-  v4i acc0 = (v4i){0, 0, 0, 0}, acc1 = (v4i){0, 0, 0, 0};
+  v4i acc[TPW][2];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) acc[t][0] = acc[t][1] = (v4i){0, 0, 0, 0};
   int32_t rs_lane = 0;  // sum of this lane's A bytes (row 16h + (l & 15))
   const int a_lane = 16 * h + (lane & 15) + 32 * ((lane >> 4) & 1);
   const int a_step = lane >> 5;
@@ -402,10 +409,14 @@ __device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs
       if (i < cnt) {
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
-          const auto s32 = __builtin_amdgcn_permlane32_swap((uint32_t)b[i][2 * pp], (uint32_t)b[i][2 * pp + 1], false, false);
-          const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
-          acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[0]), acc0, 0, 0, 0);
-          acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[1]), acc1, 0, 0, 0);
+#pragma unroll
+          for (int t = 0; t < TPW; ++t) {
+            const auto s32 =
+                __builtin_amdgcn_permlane32_swap((uint32_t)b[t][i][2 * pp], (uint32_t)b[t][i][2 * pp + 1], false, false);
+            const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
+            acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[0]), acc[t][0], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[1]), acc[t][1], 0, 0, 0);
+          }
           rs_lane = bytes_sum(a[i][pp], rs_lane);
         }
       }
@@ -418,16 +429,33 @@ __device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs
     if (lane < 16) red_rs[wv][lane] = rs;
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    red[wv][j][lane] = acc0[j];
-    red[wv][4 + j][lane] = acc1[j];
-  }
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      red[wv][t][j][lane] = acc[t][0][j];
+      red[wv][t][4 + j][lane] = acc[t][1][j];
+    }
   __syncthreads();
   const int reg = 4 * (ec >> 4) + (er & 3), src = 16 * (er >> 2) + (ec & 15);
-  int32_t v = 0;
+  int32_t rs = 0;
 #pragma unroll
-  for (int w = 0; w < WAVES; ++w) v += red[w][reg][src] - red_rs[w][er];
-  if (row < p.M) epi_scale(p, row, col, v, ad, res);
+  for (int w = 0; w < WAVES; ++w) rs += red_rs[w][er];
+  int32_t v[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    int32_t sum = -rs;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) sum += red[w][t][reg][src];
+    v[t] = sum;
+  }
+  if (row >= p.M) return;
+  if constexpr (EPI == EPI_RELU2) {
+#pragma unroll
+    for (int u = 0; u < TPW / 2; ++u) epi_relu2(p, row, tile[u] * 32 + ec, tile[u + TPW / 2] * 32 + ec, v[u], v[u + TPW / 2], ad);
+  } else {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) epi_scale(p, row, tile[t] * 32 + ec, v[t], ad, res[t]);
+  }
 }
 
 template <int TPW, int NSB, int EPI, int WAVES>
@@ -438,7 +466,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_decode(GemmArgs p) {
 // One launch per decode BitLinear: blocks [0, nact) quantise the token rows,
 // blocks [nact, nact + ngemm) run the GEMM.  Activation blocks come first in
 // dispatch order, so they never wait behind GEMM blocks.
-template <int TPW, int NSB, int EPI, bool NORM, int CPT>
+template <int TPW, int NSB, int EPI, bool NORM, int CPT, bool HALF>
 __global__ __launch_bounds__(512) void k_bitlinear_decode(GemmArgs p, ActArgs a, FusedSync fs) {
   if ((int)blockIdx.x < fs.nact) {
     uint32_t* ready = ready_word(fs, (int)blockIdx.x);
@@ -449,13 +477,10 @@ __global__ __launch_bounds__(512) void k_bitlinear_decode(GemmArgs p, ActArgs a,
     if (threadIdx.x == 0) st_coherent(ready, e);
     return;
   }
-  if constexpr (TPW == 1 && EPI == EPI_SCALE) {
-    if (p.mh == 2) {
-      gemm_decode_half<NSB, 8>(p, blockIdx.x - fs.nact, fs);
-      return;
-    }
-  }
-  gemm_decode_wg<TPW, NSB, EPI, 8, true>(p, blockIdx.x - fs.nact, fs);
+  if constexpr (HALF)
+    gemm_decode_half<TPW, NSB, EPI, 8>(p, blockIdx.x - fs.nact, fs);
+  else
+    gemm_decode_wg<TPW, NSB, EPI, 8, true>(p, blockIdx.x - fs.nact, fs);
 }
 
 // ------------------------------------------------------------ prefill ----
@@ -973,11 +998,28 @@ static GemmPlan plan_fused(int64_t M, int64_t K, int64_t N, int epilogue, int sp
   if (splitk_req <= 0) splitk_req = 1;
   GemmPlan pl = plan_decode(K, N, epilogue, splitk_req, 8, max_wgs);
   pl.fused = (int64_t)pl.ngroups * pl.splitk <= max_wgs && pl.ngroups * pl.splitk <= kGemmSlots && act_cpt(K) <= 4;
-  // Two workgroups per column group, one per 16-row half, where both fit:
-  // each reads half of the activation tile after the hand-off (measured on
-  // MI355X: down 11.45 -> 11.2 us, o_proj 8.08 -> 8.0 us).
-  pl.mh = (pl.fused && M > 16 && pl.splitk == 1 && 2 * pl.ngroups <= max_wgs &&
-           2 * pl.ngroups <= kGemmSlots) ? 2 : 1;
+  // Two workgroups per column group, one per 16-row half, where both fit
+  // (for the scale epilogue, doubling the column tiles of a group if that
+  // makes them fit): each reads half of the activation tile after the
+  // hand-off and runs 16-row MFMAs.  Measured on MI355X at the 2B shapes:
+  // down 11.05 -> 9.6 us, o_proj 7.95 -> 7.1 us, QKV (two tiles a group)
+  // 7.98 -> 7.62 us.
+  pl.mh = 1;
+  if (pl.fused && M > 16 && pl.splitk == 1) {
+    const int NT = (int)(N / 32);
+    auto fits = [&](int ng) { return 2 * ng <= max_wgs && 2 * ng <= kGemmSlots; };
+    if (fits(pl.ngroups)) {
+      pl.mh = 2;
+    } else if (epilogue == BTL_EPI_SCALE && pl.tpw == 1 && NT % 2 == 0 && fits(NT / 2)) {
+      pl.tpw = 2;
+      pl.ngroups = NT / 2;
+      pl.mh = 2;
+    }
+    // Not for gate||up: four tiles a workgroup (two gate/up pairs) measured
+    // 9.9 us against 8.95 us for the whole-tile workgroups at 2560 -> 2 x 6912.
+    // The 16-row MFMA halves the MFMA time per unpacked weight dword, so the
+    // 2-bit unpack on the VALU then sets the pace.
+  }
   return pl;
 }
 
@@ -1007,16 +1049,17 @@ static void launch_decode_nsb(int nsb, dim3 grid, hipStream_t s, const GemmArgs&
   }
 }
 
-template <int TPW, int EPI, bool NORM, int CPT>
+template <int TPW, int EPI, bool NORM, int CPT, bool HALF>
 static void launch_fused_nsb(int nsb, dim3 grid, hipStream_t s, const GemmArgs& g, const ActArgs& a,
                              const FusedSync& fs) {
   const dim3 block(512);
   switch (nsb) {
-    case 2: hipLaunchKernelGGL((k_bitlinear_decode<TPW, 2, EPI, NORM, CPT>), grid, block, 0, s, g, a, fs); break;
-    case 4: hipLaunchKernelGGL((k_bitlinear_decode<TPW, 4, EPI, NORM, CPT>), grid, block, 0, s, g, a, fs); break;
-    case 6: hipLaunchKernelGGL((k_bitlinear_decode<TPW, 6, EPI, NORM, CPT>), grid, block, 0, s, g, a, fs); break;
+    case 2: hipLaunchKernelGGL((k_bitlinear_decode<TPW, 2, EPI, NORM, CPT, HALF>), grid, block, 0, s, g, a, fs); break;
+    case 4: hipLaunchKernelGGL((k_bitlinear_decode<TPW, 4, EPI, NORM, CPT, HALF>), grid, block, 0, s, g, a, fs); break;
+    case 6: hipLaunchKernelGGL((k_bitlinear_decode<TPW, 6, EPI, NORM, CPT, HALF>), grid, block, 0, s, g, a, fs); break;
     default:
-      hipLaunchKernelGGL((k_bitlinear_decode<TPW, TPW == 2 ? 6 : 8, EPI, NORM, CPT>), grid, block, 0, s, g, a, fs);
+      hipLaunchKernelGGL((k_bitlinear_decode<TPW, TPW == 2 ? 6 : 8, EPI, NORM, CPT, HALF>), grid, block, 0, s, g, a,
+                         fs);
       break;
   }
 }
@@ -1165,12 +1208,21 @@ static int launch_gemm(const GemmArgs& a, int epilogue, const GemmPlan& pl, hipS
 template <bool NORM, int CPT>
 static void launch_fused_epi(int epilogue, const GemmPlan& pl, int nsb, dim3 grid, hipStream_t s, const GemmArgs& g,
                              const ActArgs& a, const FusedSync& fs) {
-  if (epilogue == BTL_EPI_RELU2_MUL)
-    launch_fused_nsb<2, EPI_RELU2, NORM, CPT>(nsb, grid, s, g, a, fs);
-  else if (pl.tpw == 2)
-    launch_fused_nsb<2, EPI_SCALE, NORM, CPT>(nsb, grid, s, g, a, fs);
-  else
-    launch_fused_nsb<1, EPI_SCALE, NORM, CPT>(nsb, grid, s, g, a, fs);
+  if (pl.mh == 2) {
+    if (epilogue == BTL_EPI_RELU2_MUL) {
+      launch_fused_nsb<2, EPI_RELU2, NORM, CPT, true>(nsb, grid, s, g, a, fs);
+    } else if (pl.tpw == 2) {
+      launch_fused_nsb<2, EPI_SCALE, NORM, CPT, true>(nsb, grid, s, g, a, fs);
+    } else {
+      launch_fused_nsb<1, EPI_SCALE, NORM, CPT, true>(nsb, grid, s, g, a, fs);
+    }
+  } else if (epilogue == BTL_EPI_RELU2_MUL) {
+    launch_fused_nsb<2, EPI_RELU2, NORM, CPT, false>(nsb, grid, s, g, a, fs);
+  } else if (pl.tpw == 2) {
+    launch_fused_nsb<2, EPI_SCALE, NORM, CPT, false>(nsb, grid, s, g, a, fs);
+  } else {
+    launch_fused_nsb<1, EPI_SCALE, NORM, CPT, false>(nsb, grid, s, g, a, fs);
+  }
 }
 
 // Rows of 1, 2 or 4 chunks of 8 per thread (K <= 4096, 8192, 16384).

@@ -295,31 +295,45 @@ def test_fused_decode_handshake_clean(orc):
         assert not rest.any(), "stray handshake words"
 
 
-@pytest.mark.parametrize("m,k,n", [(32, 2560, 2560), (17, 6912, 2560), (24, 2560, 640), (32, 6912, 96)])
-def test_fused_row_halves_bit_exact(orc, m, k, n):
-    """Single-launch BitLinear with more than 16 rows and a narrow enough grid
-    that two GEMM workgroups take each column tile, one per 16-row half (the
-    o_proj and down shapes of the 2B model): int8 rows, int32 accumulators and
-    bf16 outputs with the scale and residual epilogue equal the oracle's, also
-    for the rows of a half that stops at M."""
+@pytest.mark.parametrize("m,k,n,epi", [(32, 2560, 2560, "none"), (17, 6912, 2560, "none"), (24, 2560, 640, "none"),
+                                        (32, 6912, 96, "none"), (32, 2560, 3840, "qkv"), (32, 2560, 13824, "relu2_mul"),
+                                        (19, 2560, 13824, "relu2_mul"), (32, 2560, 1024, "relu2_mul")])
+def test_fused_row_halves_bit_exact(orc, m, k, n, epi):
+    """Single-launch BitLinear with more than 16 rows.  Two GEMM workgroups
+    take each column group, one per 16-row half, in these cases:
+    - the o_proj and down shapes of the 2B model (one column tile a group,
+      scale and residual epilogue);
+    - fused QKV (two tiles a group, three scale segments);
+    - gate||up at 1024 (one gate/up pair a group, relu2 epilogue).
+    The 2B gate||up shape keeps whole-tile workgroups.  In every case the int8
+    rows, int32 accumulators and bf16 outputs equal the oracle's, also for the
+    rows of a half that stops at M."""
     from bitnet_tt.ternary_matmul import PackedTernaryWeight, ternary_matmul
 
-    print(f"row halves m={m} k={k} n={n}", flush=True)
+    print(f"row halves m={m} k={k} n={n} {epi}", flush=True)
     xb = H.activations(orc, m, k, seed=m + k + 7)
     gb = H.gamma(orc, k, seed=n + 3)
-    res = H.activations(orc, m, n, seed=n + 11)
     w = H.ternary(k, n, seed=k + 5)
-    pw = PackedTernaryWeight(device_weight(orc, w), k, n, (0.0173,), (n,))
+    if epi == "relu2_mul":
+        scales, ends = [0.0173, 0.0191], [n // 2, n]
+    elif epi == "qkv":
+        scales, ends = [0.0173, 0.0191, 0.0229], [2560, 3200, 3840]
+    else:
+        scales, ends = [0.0173], [n]
+    res = H.activations(orc, m, n, seed=n + 11) if epi == "none" else None
+    pw = PackedTernaryWeight(device_weight(orc, w), k, n, tuple(scales), tuple(ends))
     acc = torch.empty((m, n), dtype=torch.int32, device=H.dev())
     xq = torch.empty((m, k), dtype=torch.int8, device=H.dev())
-    ref = orc.bitlinear(xb, w, [0.0173], [n], gamma_bf16=gb, norm_eps=1e-5, residual_bf16=res)
+    ref = orc.bitlinear(xb, w, scales, ends, gamma_bf16=gb, norm_eps=1e-5, residual_bf16=res)
+    exp = ref["out"] if epi != "relu2_mul" else orc.relu2_mul_bf16(ref["out"][:, : n // 2], ref["out"][:, n // 2:])
+    kw = dict(residual=H.to_dev_bf16(res)) if res is not None else {}
     for rep in range(2):
         out = ternary_matmul(H.to_dev_bf16(xb), pw, norm_weight=H.to_dev_bf16(gb), norm_epsilon=1e-5,
-                             residual=H.to_dev_bf16(res), acc_out=acc, xq_out=xq)
+                             epilogue="relu2_mul" if epi == "relu2_mul" else "none", acc_out=acc, xq_out=xq, **kw)
         torch.cuda.synchronize()
         assert np.array_equal(xq.cpu().numpy(), ref["q"]), f"call {rep}: int8 rows differ"
         assert np.array_equal(acc.cpu().numpy(), ref["acc"]), f"call {rep}: accumulators differ"
-        assert np.array_equal(H.bits_of(out), ref["out"]), f"call {rep}: outputs differ"
+        assert np.array_equal(H.bits_of(out), exp), f"call {rep}: outputs differ"
 
 
 def test_fused_workspace_shared_across_shapes(orc):
