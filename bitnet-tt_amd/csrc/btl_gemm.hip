@@ -391,7 +391,11 @@ __device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs
   v4i acc[TPW][2];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) acc[t][0] = acc[t][1] = (v4i){0, 0, 0, 0};
-  int32_t rs_lane = 0;  // sum of this lane's A bytes (row 16h + (l & 15))
+  // Row sums on the matrix pipe, which has room here (the 2-bit unpack keeps
+  // the VALU busier): A against an all-ones operand, every column of row r
+  // holding sum_k q[r][k].
+  const v4i ones = (v4i){0x01010101, 0x01010101, 0x01010101, 0x01010101};
+  v4i acc_rs = (v4i){0, 0, 0, 0};
   const int a_lane = 16 * h + (lane & 15) + 32 * ((lane >> 4) & 1);
   const int a_step = lane >> 5;
   for (int base = wb; base < we; base += NSB) {
@@ -417,17 +421,14 @@ __device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs
             acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[0]), acc[t][0], 0, 0, 0);
             acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[1]), acc[t][1], 0, 0, 0);
           }
-          rs_lane = bytes_sum(a[i][pp], rs_lane);
+          acc_rs = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], ones, acc_rs, 0, 0, 0);
         }
       }
     }
   }
-  {
-    // a row's bytes are spread over lanes l, l ^ 16, l ^ 32, l ^ 48
-    int32_t rs = rs_lane + (int32_t)xor_partner_u<16>((uint32_t)rs_lane);
-    rs += (int32_t)xor_partner_u<32>((uint32_t)rs);
-    if (lane < 16) red_rs[wv][lane] = rs;
-  }
+  if ((lane & 15) == 0)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red_rs[wv][4 * (lane >> 4) + j] = acc_rs[j];
 #pragma unroll
   for (int t = 0; t < TPW; ++t)
 #pragma unroll
