@@ -354,8 +354,19 @@ __device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs
   __shared__ int32_t red[WAVES][TPW][8][64];
   __shared__ int32_t red_rs[WAVES][16];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int g = bid % p.ngroups;
-  const int h = bid / p.ngroups;
+  // The two halves of a group are 8 workgroups apart, so that round-robin
+  // dispatch puts them on one XCD and its L2 fetches the group's weights
+  // once.  Past the last whole block of 8 groups they pair up r apart.
+  const int g8 = p.ngroups & ~7;
+  int g, h;
+  if (bid < 2 * g8) {
+    g = ((bid >> 4) << 3) | (bid & 7);
+    h = (bid >> 3) & 1;
+  } else {
+    const int i = bid - 2 * g8, r = p.ngroups - g8;
+    g = g8 + i % r;
+    h = i / r;
+  }
   int tile[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
