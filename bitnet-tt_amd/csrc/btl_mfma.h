@@ -1,5 +1,6 @@
 // Operand helpers of the int8 x ternary MFMA (v_mfma_i32_32x32x32_i8) shared
-// by the GEMM kernels.
+// by the GEMM kernels.  The row-half decode body regroups the packed words
+// across lanes for v_mfma_i32_16x16x64_i8 before unpacking them here.
 //
 // Weights are stored as offset codes u = w + 1 in {0,1,2}, 2 bits each, in
 // MFMA operand order: dword q of lane `lane` in superblock ks of column tile
