@@ -14,7 +14,8 @@ Printed JSON (one line): value = algorithmic HBM bytes of a step / step time
 (GB/s), ms_per_step = BitLinear ms per decode step, plus the roofline of the
 dominant kernel (the BitLinear kind with the longest launch) measured with HIP
 events on the launch stream, the prefill MFMA-i8 utilisation, and the CPU
-oracle timed on the host as a reported baseline.  ``--pmc-pass`` runs only
+reference CPU path (numpy absmax quantisation + torch fp32 GEMM of the same
+step) timed on the host as a reported baseline.  ``--pmc-pass`` runs only
 the workload of the rocprofv3 --pmc traffic measurement.
 """
 
@@ -51,7 +52,7 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-lm-head", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="approximate CPU-baseline sample length")
+    ap.add_argument("--cpu-reps", type=int, default=20, help="timed CPU-baseline steps (after 3 warm-ups)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="run only the workload of the rocprofv3 --pmc traffic runs and exit")
     return ap.parse_args()
@@ -61,57 +62,86 @@ def parse():
 KINDS = ("qkv", "o_proj", "gate_up", "down")
 
 
+KIND_ATTR = {"qkv": "qkv", "o_proj": "o_proj", "gate_up": "gate_up", "down": "down"}
+ROTATION_BYTES = 512 << 20  # distinct weight bytes a per-kind pass cycles through (> 256 MB last-level cache)
+
+
 def kind_launcher(step, kind):
-    """(launch(layer_index), description) of one BitLinear kind of the step,
-    with exactly the arguments the step's own chain passes."""
+    """launch(layer_index, weight=None) of one BitLinear kind of the step, with
+    exactly the arguments the step's own chain passes (``weight`` replaces the
+    layer's weight by a copy with the same values)."""
     from bitnet_tt.ternary_matmul import ternary_matmul_into
 
     eps = step.eps
+    attr = KIND_ATTR[kind]
+
+    def wt(i, w):
+        return getattr(step.layers[i], attr) if w is None else w
+
     if kind == "qkv":
-        def launch(i):
-            w = step.layers[i]
-            ternary_matmul_into(step.hidden, w.qkv, step.qkv_out, norm_weight=w.input_layernorm, norm_epsilon=eps)
+        def launch(i, w=None):
+            L_ = step.layers[i]
+            ternary_matmul_into(step.hidden, wt(i, w), step.qkv_out, norm_weight=L_.input_layernorm, norm_epsilon=eps)
     elif kind == "o_proj":
-        def launch(i):
-            w = step.layers[i]
-            ternary_matmul_into(step.attn_out, w.o_proj, step.hidden, norm_weight=w.attn_sub_norm,
+        def launch(i, w=None):
+            L_ = step.layers[i]
+            ternary_matmul_into(step.attn_out, wt(i, w), step.hidden, norm_weight=L_.attn_sub_norm,
                                 norm_epsilon=eps, residual=step.hidden)
     elif kind == "gate_up":
-        def launch(i):
-            w = step.layers[i]
-            ternary_matmul_into(step.hidden, w.gate_up, step.ffn_h, norm_weight=w.post_attention_layernorm,
+        def launch(i, w=None):
+            L_ = step.layers[i]
+            ternary_matmul_into(step.hidden, wt(i, w), step.ffn_h, norm_weight=L_.post_attention_layernorm,
                                 norm_epsilon=eps, epilogue="relu2_mul")
     else:
-        def launch(i):
-            w = step.layers[i]
-            ternary_matmul_into(step.ffn_h, w.down, step.hidden, norm_weight=w.ffn_sub_norm, norm_epsilon=eps,
+        def launch(i, w=None):
+            L_ = step.layers[i]
+            ternary_matmul_into(step.ffn_h, wt(i, w), step.hidden, norm_weight=L_.ffn_sub_norm, norm_epsilon=eps,
                                 residual=step.hidden)
     return launch
+
+
+def rotation_plan(step, kind):
+    """[(layer, weight)] covering every layer's weight of a kind, repeated with
+    device copies until the distinct weight bytes reach ROTATION_BYTES, so a
+    pass cannot run out of the 256 MB last-level cache."""
+    import dataclasses
+
+    attr = KIND_ATTR[kind]
+    n = len(step.layers)
+    per_pass = sum(getattr(L_, attr).nbytes for L_ in step.layers)
+    copies = max(1, -(-ROTATION_BYTES // per_pass))
+    plan = [(i, None) for i in range(n)]
+    for _ in range(copies - 1):
+        for i in range(n):
+            w = getattr(step.layers[i], attr)
+            plan.append((i, dataclasses.replace(w, data=w.data.clone())))
+    return plan, per_pass * copies
 
 
 def kernel_event_timing(step, torch, reps):
     """Average duration of each BitLinear kind's single-launch decode kernel,
     measured with HIP events on the launch stream.  For every kind the 30
-    layers' launches (distinct weights: 265 MB for gate||up, more than the
-    256 MB last-level cache) are recorded into a graph; a replay is bracketed
-    by two events on that stream and divided by the number of launches."""
+    layers' launches, over copies of their weights until at least 512 MB of
+    distinct weights are cycled (more than the 256 MB last-level cache), are
+    recorded into a graph; a replay is bracketed by two events on that stream
+    and divided by the number of launches."""
     dev = step.device
     res = {}
     s = torch.cuda.Stream(device=dev)
-    n = len(step.layers)
     for kind in KINDS:
         launch = kind_launcher(step, kind)
+        plan, wbytes = rotation_plan(step, kind)
         step.reset_hidden()
         torch.cuda.synchronize()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
-            for i in range(n):  # eager pass: workspace allocation happens outside capture
-                launch(i)
+            for i, w in plan:  # eager pass: workspace allocation happens outside capture
+                launch(i, w)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=s):
-            for i in range(n):
-                launch(i)
+            for i, w in plan:
+                launch(i, w)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         times = []
@@ -123,11 +153,12 @@ def kernel_event_timing(step, torch, reps):
                 g.replay()
                 e1.record(s)
                 e1.synchronize()
-                times.append(e0.elapsed_time(e1) * 1e3 / n)  # us per launch
+                times.append(e0.elapsed_time(e1) * 1e3 / len(plan))  # us per launch
         torch.cuda.synchronize()
         times.sort()
-        res[kind] = {"us_per_launch_median": times[len(times) // 2], "us_per_launch_min": times[0]}
-        del g
+        res[kind] = {"us_per_launch_median": times[len(times) // 2], "us_per_launch_min": times[0],
+                     "launches_per_replay": len(plan), "distinct_weight_bytes": wbytes}
+        del g, plan
     step.reset_hidden()
     torch.cuda.synchronize()
     return res
@@ -179,62 +210,96 @@ def gemm_algorithmic_bytes(M, K, N, epi, nseg, residual):
     return b
 
 
-def prefill_mfma(torch, N, dev):
-    """MFMA-i8 utilisation of the prefill GEMM at the configured shapes."""
+PREFILL_SHAPES = [(512, 2560, 3840), (512, 2560, 6912), (512, 2560, 2560), (512, 6912, 2560),
+                  (2048, 2560, 3840), (2048, 2560, 6912), (2048, 2560, 2560), (2048, 6912, 2560)]
+PREFILL_SEED = 77
+
+
+def graph_time_us(torch, dev, launch, reps=20, warm=3):
+    """Average us per call of `reps` calls of launch(i) recorded into one
+    graph, bracketed by HIP events on the capture stream (eager warm-up calls
+    first, so workspaces exist before the capture)."""
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(warm):
+            launch(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(reps):
+            launch(i)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        g.replay()
+        e0.record(s)
+        g.replay()
+        e1.record(s)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    del g
+    torch.cuda.synchronize()
+    return us
+
+
+def prefill_mfma(torch, N, dev, shapes=PREFILL_SHAPES):
+    """MFMA-i8 utilisation of the prefill BitLinear at the configured shapes.
+
+    Inputs as the prefill configuration states them: x bf16 ~N(0, 1) with 1 %
+    of the channels x20, gain ~N(1, 0.1), weights absmean-quantised from
+    seeded N(0, 0.02) latents (4 copies with distinct latents, cycled).  Two
+    figures per shape: the GEMM alone (btl_gemm_i8t2 on the activation
+    kernel's int8 operand, scales and row sums) and the whole BitLinear
+    (btl_bitlinear_fused: RMSNorm + absmax activation kernel, then the GEMM)."""
+    from bitnet_tt.layers.bitlinear import pack_for_device
+    from bitnet_tt.ternary_matmul import ternary_matmul_into
+    from bitnet_tt.utils.quantization import weight_quant_ternary
+
     L = N.lib()
-    shapes = [(512, 2560, 3840), (512, 2560, 6912), (512, 2560, 2560), (512, 6912, 2560),
-              (2048, 2560, 3840), (2048, 2560, 6912), (2048, 2560, 2560), (2048, 6912, 2560)]
     out = []
     gen = torch.Generator(device=dev)
-    gen.manual_seed(77)
+    gen.manual_seed(PREFILL_SEED)
     for M, K, Nf in shapes:
-        KS = (K + 127) // 128
-        # activations as the layer makes them: absmax int8 operand, scales and
-        # row sums from the activation kernel
-        x = torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16)
+        x = torch.randn((M, K), generator=gen, device=dev)
+        cols = torch.randperm(K, generator=gen, device=dev)[: K // 100]
+        x[:, cols] *= 20.0
+        x = x.to(torch.bfloat16)
+        gamma = (1.0 + 0.1 * torch.randn((K,), generator=gen, device=dev)).to(torch.bfloat16)
         xa = torch.empty((int(L.btl_act_bytes(M, K)),), dtype=torch.int8, device=dev)
         a_dq = torch.empty((32 * ((M + 31) // 32),), dtype=torch.float32, device=dev)
         rowsum = torch.empty((32 * ((M + 31) // 32),), dtype=torch.int32, device=dev)
-        N.check(L.btl_quant_absmax(N.ptr(x), M, K, K, None, 0.0, N.ptr(xa), N.ptr(a_dq), N.ptr(rowsum), None, None,
-                                   None, N.stream_of(dev)), "prefill activations")
+        N.check(L.btl_quant_absmax(N.ptr(x), M, K, K, N.ptr(gamma), 1e-5, N.ptr(xa), N.ptr(a_dq), N.ptr(rowsum),
+                                   None, None, None, N.stream_of(dev)), "prefill activations")
         copies = 4
-        wd = [torch.randint(0, 1 << 30, (Nf // 32, KS, 256), generator=gen, device=dev, dtype=torch.int32) & 0x55555555
-              for _ in range(copies)]  # codes 0/1 only: valid ternary offsets
+        pws = []
+        for _ in range(copies):
+            lat = torch.randn((Nf, K), generator=gen, device=dev) * 0.02
+            q, sc_w = weight_quant_ternary(lat)
+            pws.append(pack_for_device(q, dev, (sc_w,), (Nf,)))
+            del lat, q
         o = torch.empty((M, Nf), dtype=torch.bfloat16, device=dev)
-        sc, en, nseg = N.segments_arrays([0.02], [Nf])
-        stream = N.stream_of(dev)
         # split-K partials and counters (zero-filled once; every call leaves them clean)
         ws = torch.zeros(max(int(L.btl_gemm_workspace_bytes(M, K, Nf, 0, 0)), 256), dtype=torch.uint8, device=dev)
 
-        def launch(i):
-            N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(a_dq), N.ptr(rowsum), M, K, Nf, N.ptr(wd[i % copies]), sc, en,
-                                    nseg, 0, None, N.ptr(o), None, N.ptr(ws), ws.numel(), 0, stream), "prefill gemm")
+        def gemm(i):
+            pw = pws[i % copies]
+            sc, en, nseg = N.segments_arrays(pw.segment_scales, pw.segment_ends)
+            N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(a_dq), N.ptr(rowsum), M, K, Nf, N.ptr(pw.data), sc, en,
+                                    nseg, 0, None, N.ptr(o), None, N.ptr(ws), ws.numel(), 0, N.stream_of(dev)),
+                    "prefill gemm")
 
-        reps = 20
-        s = torch.cuda.Stream(device=dev)
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            stream = N.stream_of(dev)
-            for i in range(3):
-                launch(i)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):
-            stream = N.stream_of(dev)
-            for i in range(reps):
-                launch(i)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(s):
-            g.replay()
-            e0.record(s)
-            g.replay()
-            e1.record(s)
-        e1.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / reps
-        del g
-        tops = 2.0 * M * K * Nf / (us * 1e-6) / 1e12
-        out.append({"M": M, "K": K, "N": Nf, "us": round(us, 2), "tops": round(tops, 1),
-                    "mfma_i8_util": round(tops / MFMA_I8_PEAK_TOPS, 4)})
+        def bitlinear(i):
+            ternary_matmul_into(x, pws[i % copies], o, norm_weight=gamma, norm_epsilon=1e-5)
+
+        us = graph_time_us(torch, dev, gemm)
+        us_bl = graph_time_us(torch, dev, bitlinear)
+        ops = 2.0 * M * K * Nf
+        tops = ops / (us * 1e-6) / 1e12
+        out.append({"M": M, "K": K, "N": Nf, "splitk": int(L.btl_choose_splitk(M, K, Nf, 0)),
+                    "us": round(us, 2), "tops": round(tops, 1), "mfma_i8_util": round(tops / MFMA_I8_PEAK_TOPS, 4),
+                    "us_bitlinear": round(us_bl, 2),
+                    "mfma_i8_util_bitlinear": round(ops / (us_bl * 1e-6) / 1e12 / MFMA_I8_PEAK_TOPS, 4)})
+        del pws
     return out
 
 
@@ -364,53 +429,124 @@ def lm_head_timing(torch, N, dev, reps=20):
 
 
 # ------------------------------------------------------------ CPU baseline ----
-def cpu_baseline(step, torch, seconds):
-    """Scalar C oracle (one thread) on a bounded sample of the same workload:
-    whole decode layers (4 BitLinears at M = 32), run until `seconds` pass."""
+def cpu_model_name() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: the process's CPU affinity, capped
+    by OMP_NUM_THREADS when the environment sets it (the GPU box gives one GPU
+    a share of its cores and says so there)."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(n, 1)
+
+
+def cpu_baseline(step, torch, gpu_hidden, reps=20, warmup=3):
+    """The reference's CPU path of the same 30-layer BitLinear step, timed on
+    the host: per BitLinear the RMSNorm in HF BitNetRMSNorm order (torch fp32),
+    numpy per-token absmax quantisation (activation_quant_absmax,
+    src/bitnet_tt/utils/quantization.py:60-91), a torch fp32 GEMM of the
+    int-valued operands (exact: |acc| < 2^24), and the scale to bf16; relu^2*up
+    and the residual adds in bf16 as the model does.  Same weights, gains and
+    inputs as the GPU step.  Median of `reps` full steps after `warmup`."""
     import numpy as np
 
+    from bitnet_tt.utils.quantization import activation_quant_absmax
     from oracle import oracle as orc
 
     orc.lib()
+    n_thr = cpu_threads()
+    torch.set_num_threads(n_thr)
     c = step.config
-
-    def wkn(pw):
-        return orc.devlayout_decode(pw.data.cpu().numpy().view(np.uint32), pw.in_features, pw.out_features)
-
-    def bits(t):
-        return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
-
     eps = step.eps
-    hidden = bits(step.hidden0)
-    attn = bits(step.attn_out)
-    per_layer = step.algorithmic_bytes()["layer"]
-    done, t_total = 0, 0.0
-    for i, w in enumerate(step.layers):
-        mats = (wkn(w.qkv), wkn(w.o_proj), wkn(w.gate_up), wkn(w.down))
-        g = [bits(t) for t in (w.input_layernorm, w.attn_sub_norm, w.post_attention_layernorm, w.ffn_sub_norm)]
+    bf = torch.bfloat16
+
+    def w_f32(pw):  # ternary (K, N) as float32, from the device weight
+        w = orc.devlayout_decode(pw.data.cpu().numpy().view(np.uint32), pw.in_features, pw.out_features)
+        return torch.from_numpy(w.astype(np.float32))
+
+    def seg_scale_row(pw):
+        v = torch.empty(pw.out_features, dtype=torch.float32)
+        lo = 0
+        for sc, end in zip(pw.segment_scales, pw.segment_ends):
+            v[lo:end] = float(sc)
+            lo = end
+        return v
+
+    layers = []
+    for w in step.layers:
+        layers.append({
+            "qkv": (w_f32(w.qkv), seg_scale_row(w.qkv)), "o": (w_f32(w.o_proj), seg_scale_row(w.o_proj)),
+            "gu": (w_f32(w.gate_up), seg_scale_row(w.gate_up)), "dn": (w_f32(w.down), seg_scale_row(w.down)),
+            "g_in": w.input_layernorm.cpu(), "g_sub": w.attn_sub_norm.cpu(),
+            "g_post": w.post_attention_layernorm.cpu(), "g_ffn": w.ffn_sub_norm.cpu(),
+        })
+    hidden0 = step.hidden0.cpu()
+    attn = step.attn_out.cpu()
+    F = c.intermediate_size
+
+    def rmsnorm(x, g):  # HF BitNetRMSNorm: fp32 statistic, bf16 normalised value times the bf16 gain
+        x32 = x.float()
+        var = x32.pow(2).mean(-1, keepdim=True)
+        return g * (x32 * torch.rsqrt(var + eps)).to(bf)
+
+    def bitlinear(x, g, wm):
+        w, srow = wm
+        y = rmsnorm(x, g).float().numpy()
+        q, scale = activation_quant_absmax(y)
+        acc = torch.from_numpy(q.astype(np.float32)) @ w
+        a_dq = torch.from_numpy((1.0 / scale).astype(np.float32))  # a/127 per token
+        return (acc * (srow * a_dq)).to(bf)
+
+    def run_step():
+        h = hidden0.clone()
+        qkv = None
+        for L_ in layers:
+            qkv = bitlinear(h, L_["g_in"], L_["qkv"])
+            h = (h.float() + bitlinear(attn, L_["g_sub"], L_["o"]).float()).to(bf)
+            gu = bitlinear(h, L_["g_post"], L_["gu"])
+            g_, u_ = gu[:, :F].float(), gu[:, F:].float()
+            r = (torch.relu(g_).pow(2).to(bf).float() * u_).to(bf)
+            h = (h.float() + bitlinear(r, L_["g_ffn"], L_["dn"]).float()).to(bf)
+        return h, qkv
+
+    for _ in range(warmup):
+        run_step()
+    times = []
+    for _ in range(reps):
         t0 = time.perf_counter()
-        orc.bitlinear(hidden, mats[0], list(w.qkv.segment_scales), list(w.qkv.segment_ends), gamma_bf16=g[0],
-                      norm_eps=eps)
-        hidden = orc.bitlinear(attn, mats[1], list(w.o_proj.segment_scales), gamma_bf16=g[1], norm_eps=eps,
-                               residual_bf16=hidden)["out"]
-        r = orc.gate_up_relu2(hidden, mats[2], w.gate_up.segment_scales[0], w.gate_up.segment_scales[1],
-                              gamma_bf16=g[2], norm_eps=eps)
-        hidden = orc.bitlinear(r["h"], mats[3], list(w.down.segment_scales), gamma_bf16=g[3], norm_eps=eps,
-                               residual_bf16=hidden)["out"]
-        t_total += time.perf_counter() - t0
-        done += 1
-        if t_total >= seconds:
-            break
-    gbs = per_layer * done / t_total / 1e9
-    ms_step = t_total / done * len(step.layers) * 1e3
+        h, _qkv = run_step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    nbytes = step.algorithmic_bytes()["step"]
+    equal = float((h.view(torch.int16) == gpu_hidden.view(torch.int16)).float().mean().item())
     return {
-        "value": round(gbs, 4),
+        "value": round(nbytes / med / 1e9, 3),
         "unit": "GB/s",
-        "cores": 1,
+        "cores": n_thr,
         "kind": "port",
-        "sample": f"{done} of {len(step.layers)} decode layers (4 BitLinears each, M=32) through the scalar C "
-                  f"oracle; {t_total:.1f} s; extrapolated {ms_step:.0f} ms per 30-layer step",
-        "ms_per_step_extrapolated": round(ms_step, 1),
+        "sample": f"the full {len(layers)}-layer BitLinear step (4 BitLinears per layer, M=32) on the host: numpy "
+                  f"absmax quantisation + torch fp32 GEMM on {n_thr} threads; median of {reps} steps after {warmup} "
+                  "warm-ups",
+        "ms_per_step": round(med * 1e3, 2),
+        "ms_per_step_min": round(times[0] * 1e3, 2),
+        "us_per_bitlinear": round(med * 1e6 / (4 * len(layers)), 1),
+        "cpu_model": cpu_model_name(),
+        "affinity_cpus": len(os.sched_getaffinity(0)),
+        "torch": torch.__version__,
+        "numpy": np.__version__,
+        "hidden_bits_equal_to_gpu": round(equal, 6),
     }
 
 
@@ -465,6 +601,7 @@ def main():
             graph.replay()
     torch.cuda.synchronize()
     t_el = time.perf_counter() - t_start
+    step.check()  # a bounded wait that ran out inside the timed replays raises here
     ms_per_step = t_el * 1e3 / args.steps
     nbytes = step.algorithmic_bytes()
     value = nbytes["step"] / (ms_per_step * 1e-3) / 1e9
@@ -488,6 +625,7 @@ def main():
             graph_l.replay()
     torch.cuda.synchronize()
     us_layers = (time.perf_counter() - t_l) * 1e6 / args.steps
+    step.check()
     del graph_l
     log(f"[bench] persistent per-layer launches: {us_layers:.1f} us per step")
 
@@ -544,9 +682,15 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        log("[bench] CPU baseline (oracle) ...")
-        cpu = cpu_baseline(step, torch, args.cpu_seconds)
-        log(f"[bench] CPU: {cpu['sample']}")
+        # the GPU's result of one step from the seeded input, for the CPU path's agreement figure
+        step.reset_hidden()
+        step.step()
+        step.check()
+        gpu_hidden = step.hidden.cpu()
+        log("[bench] CPU baseline (reference CPU path: numpy absmax + torch fp32 GEMM) ...")
+        cpu = cpu_baseline(step, torch, gpu_hidden, reps=args.cpu_reps)
+        log(f"[bench] CPU: {cpu['ms_per_step']} ms per step on {cpu['cores']} threads ({cpu['cpu_model']}); "
+            f"{cpu['value']} GB/s; hidden bits equal to the GPU's: {cpu['hidden_bits_equal_to_gpu']}")
 
     line = {
         "metric": "ternary GEMM HBM GB/s (% roofline) at M=32; BitLinear ms per batch-32 decode step",
@@ -560,7 +704,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8xternary->int32 (bf16 in/out)",
-        "data": "synthetic (seeded random-init ternary weights, N(0,1) activations)",
+        "data": "synthetic (seeded random-init ternary weights from N(0,0.02) latents, RMSNorm gains N(1,0.1), "
+                "activations N(0,1) with 1% outlier channels x20)",
         "config": {
             "workload": f"BitLinear portion of a batch-32 BitNet b1.58 2B decode step ({args.layers} layers x "
                         "4 fused BitLinear launches: RMSNorm->QKV 2560->3840, o_proj 2560->2560, "
@@ -572,6 +717,9 @@ def main():
             "us_per_step_layer_launches": round(us_layers, 1),
             "us_per_launch": kernel_us,
             "roofline_frac_per_launch": kernel_frac,
+            "per_kind_rotation_bytes": {k: v["distinct_weight_bytes"] for k, v in kt.items()},
+            "seeds": {"weights": args.seed, "activations": 1, "kv_cache": 3, "prefill": PREFILL_SEED,
+                      "lm_head": 31},
         },
         "roofline": roofline,
         "cpu_baseline": cpu,

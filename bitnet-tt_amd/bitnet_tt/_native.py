@@ -196,24 +196,81 @@ def has_workspace(device, nbytes: int, kind: str = "bitlinear") -> bool:
     """True when the current stream already owns a workspace of nbytes."""
     import torch
 
-    buf = _workspaces.get((kind, str(device), torch.cuda.current_stream(device).cuda_stream))
+    buf = _workspaces.get((kind, _device_key(device), torch.cuda.current_stream(device).cuda_stream))
     return buf is not None and buf.numel() >= nbytes
 
 
-def workspace(device, nbytes: int, kind: str = "bitlinear"):
+# Byte offsets of the sticky error words each workspace holds (a bounded wait
+# of a kernel that ran out sets one; see check_errors).
+_error_words: dict = {}
+
+
+def _device_key(device) -> str:
+    import torch
+
+    d = torch.device(device)
+    if d.index is None:
+        d = torch.device(d.type, torch.cuda.current_device())
+    return str(d)
+
+
+def workspace(device, nbytes: int, kind: str = "bitlinear", error_offset: int | None = None):
     """Zero-filled device workspace of at least nbytes for the current stream.
 
     kind separates workspaces whose layouts differ ("bitlinear" for
     btl_bitlinear_fused / btl_gemm_i8t2, "layer" for btl_decode_layer).  A
     workspace that grows is replaced by a fresh zero-filled one; the old one
-    is released in stream order, after the calls that used it."""
+    is released in stream order, after the calls that used it.
+    ``error_offset`` registers the byte offset of a sticky error word inside
+    the workspace, which :func:`check_errors` reads."""
     import torch
 
     stream = torch.cuda.current_stream(device)
-    key = (kind, str(device), stream.cuda_stream)
+    key = (kind, _device_key(device), stream.cuda_stream)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
         size = max(int(nbytes), 1 << 20)
         buf = torch.zeros(size, dtype=torch.uint8, device=device)
         _workspaces[key] = buf
+    if error_offset is not None:
+        _error_words.setdefault(key, set()).add(int(error_offset))
     return buf
+
+
+def check_errors(device=None) -> None:
+    """Raise RuntimeError if any kernel on ``device`` set its sticky error word.
+
+    The kernels that hand data between workgroups of one launch (the fused
+    decode BitLinear, the decode layer, decode attention) never hang: a wait
+    that exceeds its spin limit sets a sticky error word in the call's
+    workspace and the kernel finishes with invalid outputs.  This reads every
+    registered error word of the device's workspaces (all streams) after a
+    device synchronisation.  When one is set, the affected workspaces are
+    zero-filled in place (the start state of their launch counters, so later
+    calls and graphs captured on them work again) and RuntimeError names
+    them: the outputs of the calls since the last check are not valid."""
+    import torch
+
+    dev = _device_key(device if device is not None else "cuda")
+    keys = [k for k in _workspaces if k[1] == dev and _error_words.get(k)]
+    if not keys:
+        return
+    torch.cuda.synchronize(dev)
+    bad = []
+    for key in keys:
+        buf = _workspaces[key]
+        for off in sorted(_error_words[key]):
+            word = int(buf[off:off + 4].view(torch.int32).item())
+            if word:
+                bad.append((key, off, word))
+    if not bad:
+        return
+    for key in {b[0] for b in bad}:
+        _workspaces[key].zero_()
+    torch.cuda.synchronize(dev)
+    what = ", ".join(f"{k[0]} workspace (stream {k[2]:#x}) word at byte {off} = {w}" for k, off, w in bad)
+    raise RuntimeError(
+        f"a kernel on {dev} set its error word ({what}): a bounded wait ran out, or a decode-attention position "
+        "was out of range; the outputs of the calls since the last check are invalid, and the workspaces have "
+        "been reset"
+    )

@@ -232,9 +232,11 @@ class BitLinearDecodeStep:
         self._lw = None  # layer structs of the persistent launch are rebuilt
 
     # -- buffers -----------------------------------------------------------
-    def alloc_buffers(self, seed: int = 1):
+    def alloc_buffers(self, seed: int = 1, outliers: bool = True):
         """hidden [B, H], attention output stand-in [B, q_dim], qkv [B, qkv_dim],
-        FFN intermediate [B, F]; hidden and the attention buffer ~N(0, 1)."""
+        FFN intermediate [B, F]; hidden and the attention buffer ~N(0, 1), with
+        1 % of the channels (drawn from the seed) scaled by 20 for every token
+        when ``outliers``."""
         import torch
 
         c = self.config
@@ -242,9 +244,17 @@ class BitLinearDecodeStep:
         gen = torch.Generator(device=self.device)
         gen.manual_seed(seed)
         B = self.batch
-        self.hidden0 = torch.randn((B, c.hidden_size), generator=gen, device=self.device).to(torch.bfloat16)
+
+        def acts(k):
+            x = torch.randn((B, k), generator=gen, device=self.device)
+            if outliers:
+                cols = torch.randperm(k, generator=gen, device=self.device)[: max(1, k // 100)]
+                x[:, cols] *= 20.0
+            return x.to(torch.bfloat16)
+
+        self.hidden0 = acts(c.hidden_size)
         self.hidden = self.hidden0.clone()
-        self.attn_out = torch.randn((B, qd), generator=gen, device=self.device).to(torch.bfloat16)
+        self.attn_out = acts(qd)
         self.qkv_out = torch.empty((B, c.qkv_dim), dtype=torch.bfloat16, device=self.device)
         self.ffn_h = torch.empty((B, c.intermediate_size), dtype=torch.bfloat16, device=self.device)
         return self
@@ -346,7 +356,7 @@ class BitLinearDecodeStep:
             # a workspace made inside a capture would be re-zeroed by every
             # replay, resetting the launch counters the kernel's flags rely on
             raise RuntimeError("run one eager decode step on this stream before capturing it in a graph")
-        ws = N.workspace(hidden.device, nbytes, kind="layer")
+        ws = N.workspace(hidden.device, nbytes, kind="layer", error_offset=int(L.btl_decode_layer_error_offset()))
         N.check(
             L.btl_decode_layer(B, H, qd, F, c.qkv_dim, ctypes.byref(lw[i][0]), ctypes.byref(lw[i][1]),
                                ctypes.byref(lw[i][2]), ctypes.byref(nxt) if nxt is not None else None,
@@ -364,6 +374,12 @@ class BitLinearDecodeStep:
         ws = N.workspace(self.device, 0, kind="layer")
         off = int(L.btl_decode_layer_error_offset())
         return int(ws[off:off + 4].view(torch.int32).item())
+
+    def check(self) -> None:
+        """Raise RuntimeError if a bounded wait in any launch of this
+        device's steps (fused BitLinears, decode layers, decode attention)
+        ran out since the last check; synchronises the device."""
+        N.check_errors(self.device)
 
     def step_layers(self):
         w0 = self.layers[0]

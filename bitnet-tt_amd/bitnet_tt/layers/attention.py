@@ -161,7 +161,8 @@ class DecodeAttention:
         nbytes = int(L.btl_decode_attention_workspace_bytes(B, H, Hkv, S))
         if torch.cuda.is_current_stream_capturing() and not N.has_workspace(qkv.device, nbytes, "attention"):
             raise RuntimeError("run one eager attention call on this stream before capturing it in a graph")
-        ws = N.workspace(qkv.device, nbytes, kind="attention")
+        ws = N.workspace(qkv.device, nbytes, kind="attention",
+                         error_offset=int(L.btl_decode_attention_error_offset(B, Hkv)))
         N.check(
             L.btl_decode_attention(N.ptr(qkv), B, H, Hkv, D, S, N.ptr(pos), N.ptr(self.rope_cos), N.ptr(self.rope_sin),
                                    int(self.use_fused_rope), float(self.scale), N.ptr(kv_cache.key_cache),
@@ -170,6 +171,14 @@ class DecodeAttention:
             "btl_decode_attention",
         )
         return out
+
+    def check(self) -> None:
+        """Raise RuntimeError if a call since the last check met a position
+        outside [0, max_seq_len) (or any other launch on the device reported
+        a timed-out wait); synchronises the device."""
+        from .. import _native as N
+
+        N.check_errors(self.device)
 
     def error_word(self, device=None, B: int = 32) -> int:
         """Non-zero once a position outside [0, max_seq_len) reached a call on

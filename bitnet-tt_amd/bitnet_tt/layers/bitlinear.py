@@ -154,6 +154,14 @@ class Linear:
         return ternary_matmul_into(x, self.weight, out, norm_weight=norm_weight, norm_epsilon=norm_epsilon,
                                    epilogue=self.epilogue, residual=residual)
 
+    def check(self) -> None:
+        """Raise RuntimeError if a bounded wait of a launch on this layer's
+        device ran out since the last check (its outputs are then invalid);
+        synchronises the device."""
+        from ..ternary_matmul import check
+
+        check(_device(self.device))
+
 
 class RMSNorm:
     """RMSNorm ``y = bf16(gamma * bf16(x / sqrt(mean(x^2) + eps)))``

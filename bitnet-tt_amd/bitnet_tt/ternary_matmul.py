@@ -117,6 +117,15 @@ def ternary_matmul(
     return out
 
 
+def check(device=None) -> None:
+    """Raise RuntimeError if a bounded wait of a fused decode launch on
+    ``device`` ran out since the last check (the launch then returned invalid
+    bf16 values).  Synchronises the device; call it at synchronisation points.
+    The reference surfaces op failures as RuntimeError
+    (src/bitnet_tt/layers/bitlinear.py:329-330)."""
+    N.check_errors(device)
+
+
 def ternary_matmul_into(
     x,
     w: PackedTernaryWeight,
@@ -177,7 +186,7 @@ def ternary_matmul_into(
     L = N.lib()
     dev = x.device
     ws_bytes = int(L.btl_fused_workspace_bytes(M, K, Nf, epi, splitk))
-    ws = N.workspace(dev, ws_bytes)
+    ws = N.workspace(dev, ws_bytes, error_offset=int(L.btl_fused_error_offset()))
     N.check(
         L.btl_bitlinear_fused(
             N.ptr(x), M, K, K, N.ptr(gamma), eps, N.ptr(w.data), Nf, sc, en, nseg, epi, N.ptr(residual),

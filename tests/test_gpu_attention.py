@@ -109,6 +109,12 @@ def test_position_out_of_range_is_flagged(orc):
         out = att(qkv, cache, torch.tensor([3, S], dtype=torch.int32, device=H.dev()))
         torch.cuda.synchronize()
         assert att.error_word(B=B) != 0
+    # check() surfaces the sticky word as RuntimeError and resets the workspace
+    with pytest.raises(RuntimeError, match="error word"):
+        att.check()
+    with torch.cuda.stream(s):
+        assert att.error_word(B=B) == 0
+    att.check()
     assert torch.all(out[1] == 0) and torch.isfinite(out[0].float()).all()
     assert not cache.key_cache[1].any()  # nothing written for the bad row
 

@@ -214,19 +214,35 @@ def test_prefill_splitk_bit_exact(orc, m, k, n, epi):
         assert not ws[:256].cpu().numpy().any(), f"call {call}: arrival counters not back at zero"
 
 
-@pytest.mark.parametrize("m,k,n,epi,rowsum", [(512, 2560, 3840, 0, False), (512, 2560, 13824, 1, True),
-                                              (2048, 2560, 6912, 0, True), (2048, 6912, 2560, 0, False),
-                                              (2048, 6912, 2560, 0, True), (512, 2560, 2560, 0, True)])
+# Every prefill shape of the configured sweep (M in {512, 2048}; K = 2560 -> N in
+# {3840, 6912, 2560}; 6912 -> 2560), with and without the activation kernel's
+# row sums (split-K at M = 512 runs only with them), plus the gate||up pair.
+PREFILL_SHAPES = [
+    (512, 2560, 3840, 0, False), (512, 2560, 3840, 0, True),
+    (512, 2560, 6912, 0, False), (512, 2560, 6912, 0, True),
+    (512, 2560, 2560, 0, False), (512, 2560, 2560, 0, True),
+    (512, 6912, 2560, 0, False), (512, 6912, 2560, 0, True),
+    (2048, 2560, 3840, 0, False), (2048, 2560, 3840, 0, True),
+    (2048, 2560, 6912, 0, True), (2048, 2560, 2560, 0, False), (2048, 2560, 2560, 0, True),
+    (2048, 6912, 2560, 0, False), (2048, 6912, 2560, 0, True),
+    (512, 2560, 13824, 1, True),
+]
+
+
+@pytest.mark.parametrize("m,k,n,epi,rowsum", PREFILL_SHAPES)
 def test_prefill_full_size_properties(orc, m, k, n, epi, rowsum):
-    """Full prefill shapes: sampled rows exact, row/column checksums exact."""
-    print(f"prefill full m={m} k={k} n={n} epi={epi} rowsum={rowsum}", flush=True)
-    rng = np.random.default_rng(m + n)
+    """Full prefill shapes: 16 sampled rows exact (accumulators and bf16),
+    every row checksum and every column checksum exact."""
+    print(f"prefill full m={m} k={k} n={n} epi={epi} rowsum={rowsum} splitk={N.lib().btl_choose_splitk(m, k, n, epi)}",
+          flush=True)
+    rng = np.random.default_rng(m + n + k)
     q = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
     w = H.ternary(k, n, seed=k + n)
     scales = [0.02] if epi == 0 else [0.02, 0.03]
     ends = [n] if epi == 0 else [n // 2, n]
-    acc, out, a_dq, _ = run_gemm(orc, q, w, scales, ends, epi=epi, rowsum=rowsum)
-    rows = np.sort(rng.choice(m, 6, replace=False))
+    acc, out, a_dq, clean = run_gemm(orc, q, w, scales, ends, epi=epi, rowsum=rowsum)
+    assert clean, "split-K arrival counters not back at zero"
+    rows = np.sort(rng.choice(m, 16, replace=False))
     ref_rows = orc.gemm_i8t(np.ascontiguousarray(q[rows]), w)
     assert np.array_equal(acc[rows], ref_rows)
     q64, w64 = q.astype(np.int64), w.astype(np.int64)
@@ -234,6 +250,44 @@ def test_prefill_full_size_properties(orc, m, k, n, epi, rowsum):
     assert np.array_equal(acc.astype(np.int64).sum(0), q64.sum(0) @ w64)
     exp_rows = expected_out(orc, ref_rows, a_dq[rows], scales, ends, epi)
     assert np.array_equal(out[rows], exp_rows)
+
+
+@pytest.mark.parametrize("m", [512, 2048])
+def test_prefill_gate_up_relu2_through_ternary_matmul(orc, m):
+    """Prefill gate||up as the layer runs it: ternary_matmul (RMSNorm +
+    absmax activation kernel, then the prefill GEMM with its row sums) on
+    x ~ N(0, 1) with 1 % outlier channels and gate/up weights absmean-quantised
+    from seeded N(0, 0.02) latents.  The quantised activations are compared
+    with the oracle for every row, every row and column checksum of the
+    accumulators exactly, and 64 sampled rows of accumulators and relu^2*up
+    outputs bit for bit."""
+    from bitnet_tt.ternary_matmul import PackedTernaryWeight, ternary_matmul
+
+    k, f = 2560, 6912
+    print(f"prefill gate||up relu2 m={m} through ternary_matmul", flush=True)
+    xb = H.activations(orc, m, k, seed=m + 3)
+    gb = H.gamma(orc, k, seed=m + 4)
+    gq, gs = orc.weight_quant_ternary(H.latent(f, k, seed=m + 5))
+    uq, us = orc.weight_quant_ternary(H.latent(f, k, seed=m + 6))
+    w = np.ascontiguousarray(np.concatenate([gq, uq]).T)  # (K, 2F)
+    pw = PackedTernaryWeight(device_weight(orc, w), k, 2 * f, (float(gs), float(us)), (f, 2 * f))
+    acc = torch.empty((m, 2 * f), dtype=torch.int32, device=H.dev())
+    xq = torch.empty((m, k), dtype=torch.int8, device=H.dev())
+    out = ternary_matmul(H.to_dev_bf16(xb), pw, norm_weight=H.to_dev_bf16(gb), norm_epsilon=1e-5,
+                         epilogue="relu2_mul", acc_out=acc, xq_out=xq)
+    torch.cuda.synchronize()
+    y = orc.rmsnorm_bf16(xb, gb, 1e-5)
+    q_ref, _, _, _ = orc.act_quant_absmax(orc.bf16_to_f32(y))
+    q_got = xq.cpu().numpy()
+    assert np.array_equal(q_got, q_ref), "quantised activations differ"
+    a = acc.cpu().numpy().astype(np.int64)
+    q64, w64 = q_ref.astype(np.int64), w.astype(np.int64)
+    assert np.array_equal(a.sum(1), q64 @ w64.sum(1)), "row checksums"
+    assert np.array_equal(a.sum(0), q64.sum(0) @ w64), "column checksums"
+    rows = np.sort(np.random.default_rng(m).choice(m, 64, replace=False))
+    ref = orc.gate_up_relu2(np.ascontiguousarray(xb[rows]), w, float(gs), float(us), gamma_bf16=gb, norm_eps=1e-5)
+    assert np.array_equal(a[rows], ref["acc"]), "sampled accumulators"
+    assert np.array_equal(H.bits_of(out)[rows], ref["h"]), "sampled relu^2*up outputs"
 
 
 @pytest.mark.parametrize("m", [32, 100])
@@ -362,3 +416,28 @@ def test_fused_workspace_shared_across_shapes(orc):
     for key, ws in N._workspaces.items():
         if key[0] == "bitlinear":
             assert int(ws[:8192].view(torch.int32)[err // 4]) == 0, "a bounded wait ran out"
+
+
+def test_check_raises_on_sticky_error_word(orc):
+    """check() reads the fused workspace's sticky error word: set from the host
+    (as a timed-out wait would set it), it raises RuntimeError and leaves the
+    workspace zero-filled, so the next call computes correct results."""
+    from bitnet_tt.ternary_matmul import PackedTernaryWeight, check, ternary_matmul
+
+    m, k, n = 32, 512, 256
+    xb = H.activations(orc, m, k, seed=5)
+    w = H.ternary(k, n, seed=6)
+    pw = PackedTernaryWeight(device_weight(orc, w), k, n, (0.02,), (n,))
+    ref = orc.bitlinear(xb, w, [0.02])
+    out = ternary_matmul(H.to_dev_bf16(xb), pw)
+    check()  # clean
+    key = next(key for key in N._workspaces if key[0] == "bitlinear" and key[1] == str(H.dev()))
+    ws = N._workspaces[key]
+    off = int(N.lib().btl_fused_error_offset())
+    ws[off:off + 4].view(torch.int32).fill_(1)
+    with pytest.raises(RuntimeError, match="bounded wait ran out"):
+        check()
+    assert not ws.cpu().numpy().any(), "workspace not reset"
+    out = ternary_matmul(H.to_dev_bf16(xb), pw)
+    check()
+    assert np.array_equal(H.bits_of(out), ref["out"])
