@@ -95,6 +95,10 @@ EXPORTS = {
         [_P, _I64, _I64, _I64, _P, _F, _P, _I64, _P, _P, _I, _I, _P, _P, _P, _P, _P, _SZ, _I, _P],
         _I,
     ),
+    "btl_bitlinear_fused_noalloc": (
+        [_P, _I64, _I64, _I64, _P, _F, _P, _I64, _P, _P, _I, _I, _P, _P, _P, _P, _P, _I, _P],
+        _I,
+    ),
     "btl_decode_layer_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64], _I64),
     "btl_decode_layer_error_offset": ([], _I64),
     "btl_lm_head_weight_bytes": ([_I64, _I64], _I64),

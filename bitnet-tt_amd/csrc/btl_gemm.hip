@@ -33,6 +33,7 @@
 #include <stdlib.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "btl_act_row.h"
 #include "btl_mfma.h"
@@ -78,6 +79,7 @@ struct GemmArgs {
 // (zero-filled = no launch yet), whatever grid sizes share the workspace.
 struct FusedSync {
   uint32_t* words;  // handshake words
+  uint32_t* err;    // sticky error word (the workspace's own, or the caller's)
   int nact;         // activation workgroups (32)
   int ngemm;        // GEMM workgroups (at most kGemmSlots)
   unsigned spin_limit;
@@ -146,7 +148,7 @@ __device__ __forceinline__ void wait_rows_ready(const FusedSync& fs, int bid, in
                       (int32_t)(ld_coherent(ready_word(fs, lane)) - e) >= 0;
     if (__all(mine)) break;
     if (++n > fs.spin_limit) {
-      if (lane == 0) st_coherent(sync_word(fs, kErrorWord), 1u);
+      if (lane == 0) st_coherent(fs.err, 1u);
       break;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -1249,6 +1251,139 @@ static void launch_fused(int cpt, int epilogue, const GemmPlan& pl, int nsb, dim
     launch_fused_epi<NORM, 4>(epilogue, pl, nsb, grid, s, g, a, fs);
 }
 
+
+// Argument checks shared by both fused entry points.
+static int check_fused_args(const char* who, const uint16_t* x, int64_t M, int64_t K, int64_t ldx,
+                            const uint16_t* gamma, const uint32_t* wdev, int64_t N, const float* seg_scale,
+                            const int64_t* seg_end, int nseg, int epilogue, const uint16_t* residual,
+                            const uint16_t* out, const int32_t* acc_out, const int8_t* xq_debug, int splitk) {
+  int rc = check_act_args(who, x, M, K, ldx, gamma);
+  if (rc) return rc;
+  rc = check_gemm_args(who, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out);
+  if (rc) return rc;
+  if (splitk < 0) return set_error(BTL_ERR_ARG, "%s: splitk=%d", who, splitk);
+  if ((acc_out && !aligned(acc_out, 4)) || (xq_debug && !aligned(xq_debug, 8)))
+    return set_error(BTL_ERR_ALIGN, "%s: misaligned debug output", who);
+  return BTL_OK;
+}
+
+// ---- the static scratch of btl_bitlinear_fused_noalloc ---------------------
+// A workspace the library owns for callers that cannot allocate: one copy
+// per device (each GPU the library runs on holds it until the process ends),
+// zero at load and cleared once more by the first call on a device.  Calls
+// on one device share it and leave its launch counters consistent for the
+// next call; calls that overlap on one device race on it.
+constexpr int64_t kNoAllocScratchBytes = BTL_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+static_assert(kNoAllocScratchBytes % 256 == 0, "scratch size");
+
+__global__ __launch_bounds__(256) void k_zero_words(uint4* p, int64_t n16) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+constexpr int kMaxDevices = 64;
+static std::atomic<char*> g_scratch[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of this device's scratch (hipGetSymbolAddress once per
+// device, with that device current); the first call also clears it on the
+// caller's stream, ahead of the call's own kernels.
+static int noalloc_scratch(char** out, hipStream_t stream) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return set_error(BTL_ERR_LAUNCH, "btl_bitlinear_fused_noalloc: no current device (or device id >= %d)",
+                     kMaxDevices);
+  }
+  char* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p) {
+    *out = p;
+    return BTL_OK;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    void* addr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !addr) {
+      (void)hipGetLastError();
+      return set_error(BTL_ERR_LAUNCH, "btl_bitlinear_fused_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                       dev, hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(k_zero_words, dim3(256), dim3(256), 0, stream, reinterpret_cast<uint4*>(addr),
+                       (int64_t)(kNoAllocScratchBytes / 16));
+    const int rc = check_launch("btl_bitlinear_fused_noalloc: scratch clear");
+    if (rc) return rc;
+    p = static_cast<char*>(addr);
+    g_scratch[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return BTL_OK;
+}
+
+// Shared by btl_bitlinear_fused and btl_bitlinear_fused_noalloc: arguments
+// checked, workspace sized and aligned; err: the sticky error word the
+// fused kernel's bounded waits set (inside the workspace unless the caller
+// gives one).
+static int bitlinear_fused_impl(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint16_t* gamma,
+                                float norm_eps, const uint32_t* wdev, int64_t N, const float* seg_scale,
+                                const int64_t* seg_end, int nseg, int epilogue, const uint16_t* residual,
+                                uint16_t* out, int32_t* acc_out, int8_t* xq_debug, char* ws, const FusedLayout& L,
+                                uint32_t* err, int splitk, btl_stream_t stream) {
+  hipStream_t s = (hipStream_t)stream;
+  int8_t* xa = (int8_t*)(ws + L.xa);
+  float* a_dq = (float*)(ws + L.a_dq);
+
+  const GemmPlan pf = plan_fused(M, K, N, epilogue, splitk);
+  if (pf.fused) {
+    ActArgs a = {};
+    a.x = x;
+    a.ldx = ldx;
+    a.M = (int)M;
+    a.K = (int)K;
+    a.KS = (int)ksb(K);
+    a.gamma = gamma;
+    a.norm_eps = norm_eps;
+    a.act_eps = 1e-5f;
+    a.xa = xa;
+    a.a_dq = a_dq;
+    a.rowsum = nullptr;
+    a.xq_rm = xq_debug;
+    // Row 0 also clears the split-K counters, so a workspace left dirty by an
+    // interrupted call is repaired by the next one.
+    a.zero_words = pf.splitk > 1 ? (uint32_t*)(ws + L.gemm_ws) : nullptr;
+    a.n_zero_words = pf.splitk > 1 ? pf.ngroups : 0;
+    const GemmArgs g = gemm_args(xa, a_dq, nullptr, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out,
+                                 acc_out, ws + L.gemm_ws, pf);
+    FusedSync fs;
+    fs.words = (uint32_t*)ws;
+    fs.err = err ? err : fs.words + kErrorWord * kSyncStride;
+    fs.nact = kFusedActBlocks;
+    fs.ngemm = pf.ngroups * pf.splitk * g.mh;
+    fs.spin_limit = 1u << 20;
+    const int nsb = decode_nsb(pf, ksb(K), epilogue);
+    const dim3 grid((unsigned)(kFusedActBlocks + fs.ngemm));
+    const int cpt = act_cpt(K);
+    if (gamma)
+      launch_fused<true>(cpt, epilogue, pf, nsb, grid, s, g, a, fs);
+    else
+      launch_fused<false>(cpt, epilogue, pf, nsb, grid, s, g, a, fs);
+    return check_launch("fused decode BitLinear");
+  }
+
+  const GemmPlan pl = plan_gemm(M, K, N, epilogue, splitk);
+  // The prefill GEMM takes the row sums from the activation kernel, which
+  // has them in registers anyway; the decode GEMM sums its own operand.
+  int32_t* rowsum = pl.prefill ? (int32_t*)(ws + L.rowsum) : nullptr;
+  const int rc = launch_act(x, M, K, ldx, gamma, norm_eps, xa, a_dq, rowsum, nullptr, xq_debug, nullptr,
+                  pl.splitk > 1 ? (uint32_t*)(ws + L.gemm_ws) : nullptr, pl.splitk > 1 ? pl.ngroups : 0, s);
+  if (rc) return rc;
+  const GemmArgs g = gemm_args(xa, a_dq, rowsum, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out,
+                               acc_out, ws + L.gemm_ws, pl);
+  return launch_gemm(g, epilogue, pl, s);
+}
+
 }  // namespace btl
 
 using namespace btl;
@@ -1301,70 +1436,41 @@ int btl_bitlinear_fused(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, co
                         int epilogue, const uint16_t* residual, uint16_t* out, int32_t* acc_out, int8_t* xq_debug,
                         void* workspace, size_t workspace_bytes, int splitk, btl_stream_t stream) {
   clear_error();
-  int rc = check_act_args("btl_bitlinear_fused", x, M, K, ldx, gamma);
-  if (rc) return rc;
-  rc = check_gemm_args("btl_bitlinear_fused", M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out);
+  int rc = check_fused_args("btl_bitlinear_fused", x, M, K, ldx, gamma, wdev, N, seg_scale, seg_end, nseg, epilogue,
+                            residual, out, acc_out, xq_debug, splitk);
   if (rc) return rc;
   if (!workspace) return set_error(BTL_ERR_NULL, "btl_bitlinear_fused: workspace is NULL");
   if (!aligned(workspace, 256)) return set_error(BTL_ERR_ALIGN, "btl_bitlinear_fused: workspace must be 256-byte aligned");
-  if (splitk < 0) return set_error(BTL_ERR_ARG, "btl_bitlinear_fused: splitk=%d", splitk);
-  if ((acc_out && !aligned(acc_out, 4)) || (xq_debug && !aligned(xq_debug, 8)))
-    return set_error(BTL_ERR_ALIGN, "btl_bitlinear_fused: misaligned debug output");
   const FusedLayout L = fused_layout(M, K, N, epilogue, splitk);
   if ((int64_t)workspace_bytes < L.total)
     return set_error(BTL_ERR_WORKSPACE, "btl_bitlinear_fused: workspace %zu < %lld bytes", workspace_bytes,
                      (long long)L.total);
-  char* ws = (char*)workspace;
-  hipStream_t s = (hipStream_t)stream;
-  int8_t* xa = (int8_t*)(ws + L.xa);
-  float* a_dq = (float*)(ws + L.a_dq);
+  return bitlinear_fused_impl(x, M, K, ldx, gamma, norm_eps, wdev, N, seg_scale, seg_end, nseg, epilogue, residual,
+                              out, acc_out, xq_debug, (char*)workspace, L, nullptr, splitk, stream);
+}
 
-  const GemmPlan pf = plan_fused(M, K, N, epilogue, splitk);
-  if (pf.fused) {
-    ActArgs a = {};
-    a.x = x;
-    a.ldx = ldx;
-    a.M = (int)M;
-    a.K = (int)K;
-    a.KS = (int)ksb(K);
-    a.gamma = gamma;
-    a.norm_eps = norm_eps;
-    a.act_eps = 1e-5f;
-    a.xa = xa;
-    a.a_dq = a_dq;
-    a.rowsum = nullptr;
-    a.xq_rm = xq_debug;
-    // Row 0 also clears the split-K counters, so a workspace left dirty by an
-    // interrupted call is repaired by the next one.
-    a.zero_words = pf.splitk > 1 ? (uint32_t*)(ws + L.gemm_ws) : nullptr;
-    a.n_zero_words = pf.splitk > 1 ? pf.ngroups : 0;
-    const GemmArgs g = gemm_args(xa, a_dq, nullptr, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out,
-                                 acc_out, ws + L.gemm_ws, pf);
-    FusedSync fs;
-    fs.words = (uint32_t*)ws;
-    fs.nact = kFusedActBlocks;
-    fs.ngemm = pf.ngroups * pf.splitk * g.mh;
-    fs.spin_limit = 1u << 20;
-    const int nsb = decode_nsb(pf, ksb(K), epilogue);
-    const dim3 grid((unsigned)(kFusedActBlocks + fs.ngemm));
-    const int cpt = act_cpt(K);
-    if (gamma)
-      launch_fused<true>(cpt, epilogue, pf, nsb, grid, s, g, a, fs);
-    else
-      launch_fused<false>(cpt, epilogue, pf, nsb, grid, s, g, a, fs);
-    return check_launch("fused decode BitLinear");
-  }
-
-  const GemmPlan pl = plan_gemm(M, K, N, epilogue, splitk);
-  // The prefill GEMM takes the row sums from the activation kernel, which
-  // has them in registers anyway; the decode GEMM sums its own operand.
-  int32_t* rowsum = pl.prefill ? (int32_t*)(ws + L.rowsum) : nullptr;
-  rc = launch_act(x, M, K, ldx, gamma, norm_eps, xa, a_dq, rowsum, nullptr, xq_debug, nullptr,
-                  pl.splitk > 1 ? (uint32_t*)(ws + L.gemm_ws) : nullptr, pl.splitk > 1 ? pl.ngroups : 0, s);
+int btl_bitlinear_fused_noalloc(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint16_t* gamma,
+                                float norm_eps, const uint32_t* wdev, int64_t N, const float* seg_scale,
+                                const int64_t* seg_end, int nseg, int epilogue, const uint16_t* residual,
+                                uint16_t* out, int32_t* acc_out, int8_t* xq_debug, uint32_t* error_word, int splitk,
+                                btl_stream_t stream) {
+  clear_error();
+  int rc = check_fused_args("btl_bitlinear_fused_noalloc", x, M, K, ldx, gamma, wdev, N, seg_scale, seg_end, nseg,
+                            epilogue, residual, out, acc_out, xq_debug, splitk);
   if (rc) return rc;
-  const GemmArgs g = gemm_args(xa, a_dq, rowsum, M, K, N, wdev, seg_scale, seg_end, nseg, epilogue, residual, out,
-                               acc_out, ws + L.gemm_ws, pl);
-  return launch_gemm(g, epilogue, pl, s);
+  if (error_word && !aligned(error_word, 4))
+    return set_error(BTL_ERR_ALIGN, "btl_bitlinear_fused_noalloc: error_word must be 4-byte aligned");
+  const FusedLayout L = fused_layout(M, K, N, epilogue, splitk);
+  if (L.total > kNoAllocScratchBytes)
+    return set_error(BTL_ERR_WORKSPACE,
+                     "btl_bitlinear_fused_noalloc: M=%lld K=%lld N=%lld needs %lld bytes of scratch, more than the "
+                     "library's static %lld (use btl_bitlinear_fused with a workspace)",
+                     (long long)M, (long long)K, (long long)N, (long long)L.total, (long long)kNoAllocScratchBytes);
+  char* ws = nullptr;
+  rc = noalloc_scratch(&ws, (hipStream_t)stream);
+  if (rc) return rc;
+  return bitlinear_fused_impl(x, M, K, ldx, gamma, norm_eps, wdev, N, seg_scale, seg_end, nseg, epilogue, residual,
+                              out, acc_out, xq_debug, ws, L, error_word, splitk, stream);
 }
 
 }  // extern "C"

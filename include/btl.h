@@ -176,6 +176,29 @@ int btl_bitlinear_fused(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, co
                         int32_t* acc_out, int8_t* xq_debug, void* workspace, size_t workspace_bytes, int splitk,
                         btl_stream_t stream);
 
+/* Same as btl_bitlinear_fused, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference: it exists for those
+ * callers only.  Instead of a caller workspace it uses a scratch array the
+ * library holds in static device memory, BTL_NOALLOC_SCRATCH_BYTES per device
+ * (each GPU the library runs on keeps its copy until the process ends); it
+ * calls no allocating routine.  Shapes whose workspace
+ * (btl_fused_workspace_bytes) exceeds that size are rejected with
+ * BTL_ERR_WORKSPACE; every decode shape (M <= 32, K <= 16384) without a
+ * split-K request fits.  error_word: optional device uint32 the caller owns;
+ * a bounded wait that runs out stores a non-zero value there (the call's
+ * outputs are then invalid; the library never clears it).  Every call on a
+ * device shares that device's scratch and leaves it ready for the next call;
+ * calls that overlap on one device (concurrent streams or threads) race on
+ * it and must be serialised by the caller.  The first call on a device
+ * clears the scratch with a kernel on `stream`. */
+#define BTL_NOALLOC_SCRATCH_BYTES (2 << 20)
+int btl_bitlinear_fused_noalloc(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint16_t* gamma,
+                                float norm_eps, const uint32_t* wdev, int64_t N, const float* seg_scale,
+                                const int64_t* seg_end, int nseg, int epilogue, const uint16_t* residual,
+                                uint16_t* out, int32_t* acc_out, int8_t* xq_debug, uint32_t* error_word, int splitk,
+                                btl_stream_t stream);
+
 /* ---- persistent decode layer ------------------------------------------ */
 
 /* One BitLinear weight of a decode layer: device layout (btl_repack), its
