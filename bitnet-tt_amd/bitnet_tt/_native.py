@@ -99,6 +99,10 @@ EXPORTS = {
         [_P, _I64, _I64, _I64, _P, _F, _P, _I64, _P, _P, _I, _I, _P, _P, _P, _P, _P, _I, _P],
         _I,
     ),
+    "btl_decode_step_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64], _I64),
+    "btl_decode_step_error_offset": ([], _I64),
+    "btl_decode_step_prepare": ([_I64, _I64, _I64, _I64, _I64, _LWP, _P, _SZ], _I),
+    "btl_decode_step": ([_I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P, _P, _SZ, _P], _I),
     "btl_decode_layer_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64], _I64),
     "btl_decode_layer_error_offset": ([], _I64),
     "btl_lm_head_weight_bytes": ([_I64, _I64], _I64),
@@ -207,6 +211,17 @@ def has_workspace(device, nbytes: int, kind: str = "bitlinear") -> bool:
 # Byte offsets of the sticky error words each workspace holds (a bounded wait
 # of a kernel that ran out sets one; see check_errors).
 _error_words: dict = {}
+# What a workspace was prepared for (data_ptr -> owner object), for launches
+# whose workspace holds host-prepared state (the decode step's weight table).
+_prepared_for: dict = {}
+
+
+def workspace_prepared_for(buf):
+    return _prepared_for.get(buf.data_ptr())
+
+
+def set_workspace_prepared_for(buf, owner) -> None:
+    _prepared_for[buf.data_ptr()] = owner
 
 
 def _device_key(device) -> str:
@@ -233,8 +248,11 @@ def workspace(device, nbytes: int, kind: str = "bitlinear", error_offset: int | 
     key = (kind, _device_key(device), stream.cuda_stream)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
+        if buf is not None:
+            _prepared_for.pop(buf.data_ptr(), None)
         size = max(int(nbytes), 1 << 20)
         buf = torch.zeros(size, dtype=torch.uint8, device=device)
+        _prepared_for.pop(buf.data_ptr(), None)
         _workspaces[key] = buf
     if error_offset is not None:
         _error_words.setdefault(key, set()).add(int(error_offset))
@@ -271,6 +289,7 @@ def check_errors(device=None) -> None:
         return
     for key in {b[0] for b in bad}:
         _workspaces[key].zero_()
+        _prepared_for.pop(_workspaces[key].data_ptr(), None)
     torch.cuda.synchronize(dev)
     what = ", ".join(f"{k[0]} workspace (stream {k[2]:#x}) word at byte {off} = {w}" for k, off, w in bad)
     raise RuntimeError(

@@ -229,7 +229,8 @@ class BitLinearDecodeStep:
         while len(self.layers) <= layer_idx:
             self.layers.append(None)
         self.layers[layer_idx] = lw
-        self._lw = None  # layer structs of the persistent launch are rebuilt
+        self._lw = None  # layer structs of the persistent launches are rebuilt
+        self._st = None
 
     # -- buffers -----------------------------------------------------------
     def alloc_buffers(self, seed: int = 1, outliers: bool = True):
@@ -386,6 +387,60 @@ class BitLinearDecodeStep:
         ternary_matmul_into(self.hidden, w0.qkv, self.qkv_out, norm_weight=w0.input_layernorm, norm_epsilon=self.eps)
         for i in range(len(self.layers)):
             self.decode_layer(i, self.hidden, self.attn_out, self.qkv_out, self.ffn_h)
+        return self.hidden
+
+    # -- one launch for the whole step ----------------------------------------
+    def _step_table(self):
+        """btl_layer_weight_t[L][4] (qkv, o_proj, gate_up, down with the gain of
+        the RMSNorm in front of each), kept alive with the step."""
+        if getattr(self, "_st", None) is None:
+            n = len(self.layers)
+            arr = (N.LayerWeight * (4 * n))()
+            for i, w in enumerate(self.layers):
+                arr[4 * i + 0] = N.layer_weight(w.qkv, w.input_layernorm)
+                arr[4 * i + 1] = N.layer_weight(w.o_proj, w.attn_sub_norm)
+                arr[4 * i + 2] = N.layer_weight(w.gate_up, w.post_attention_layernorm)
+                arr[4 * i + 3] = N.layer_weight(w.down, w.ffn_sub_norm)
+            self._st = arr
+        return self._st
+
+    def step_persistent(self):
+        """The whole step's BitLinears as one btl_decode_step launch (every
+        layer's QKV, o_proj, gate||up and down; o_proj reads the attention
+        output buffer).  Bit-identical to step_per_call.  The first call on a
+        stream prepares that stream's workspace (a synchronous copy of the
+        weight table), so it must happen before a graph capture."""
+        import torch
+
+        c = self.config
+        B = self.batch
+        H, F, qd = c.hidden_size, c.intermediate_size, c.num_attention_heads * c.head_dim
+        if qd != H:
+            raise ValueError(f"btl_decode_step needs the attention width ({qd}) equal to hidden ({H})")
+        nl = len(self.layers)
+        for t, name in ((self.hidden, "hidden"), (self.attn_out, "attn_out"), (self.qkv_out, "qkv_out"),
+                        (self.ffn_h, "ffn_h")):
+            N.require_cuda(t, name)
+        L = N.lib()
+        table = self._step_table()
+        dev = self.hidden.device
+        nbytes = int(L.btl_decode_step_workspace_bytes(B, H, F, c.qkv_dim, nl))
+        capturing = torch.cuda.is_current_stream_capturing()
+        if capturing and not N.has_workspace(dev, nbytes, "step"):
+            raise RuntimeError("run one eager decode step on this stream before capturing it in a graph")
+        ws = N.workspace(dev, nbytes, kind="step", error_offset=int(L.btl_decode_step_error_offset()))
+        if N.workspace_prepared_for(ws) is not table:
+            if capturing:
+                raise RuntimeError("run one eager decode step on this stream before capturing it in a graph")
+            torch.cuda.current_stream(dev).synchronize()  # earlier launches on this workspace are done
+            N.check(L.btl_decode_step_prepare(B, H, F, c.qkv_dim, nl, table, N.ptr(ws), ws.numel()),
+                    "btl_decode_step_prepare")
+            N.set_workspace_prepared_for(ws, table)
+        N.check(
+            L.btl_decode_step(B, H, F, c.qkv_dim, nl, float(self.eps), N.ptr(self.attn_out), N.ptr(self.hidden),
+                              N.ptr(self.qkv_out), N.ptr(self.ffn_h), N.ptr(ws), ws.numel(), N.stream_of(dev)),
+            "btl_decode_step",
+        )
         return self.hidden
 
     def step(self):

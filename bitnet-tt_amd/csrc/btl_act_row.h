@@ -100,6 +100,19 @@ __device__ __forceinline__ void wait_memory() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// Workgroup barrier after this wave's LDS accesses have completed
+// (lgkmcnt(0)), without the memory fence of __syncthreads, whose release part
+// would also wait for every global load in flight (weights prefetched for a
+// later phase, LDS-direct loads).  The compiler fences keep LDS instructions
+// on their side of it; the explicit wait covers their results, which the
+// compiler would otherwise be free to collect after the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 __device__ __forceinline__ int64_t xa_offset(int m, int k0, int KS) {
   const int mb = m >> 5, mr = m & 31;
   const int ks = k0 >> 7, qs = (k0 >> 5) & 3, h = (k0 >> 4) & 1, p0 = k0 & 15;

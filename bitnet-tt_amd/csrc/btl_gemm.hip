@@ -557,19 +557,6 @@ __device__ __forceinline__ void pf_wait(int later) {
   }
 }
 
-// Workgroup barrier after this wave's LDS accesses have completed
-// (lgkmcnt(0)), without the memory fence of __syncthreads, whose release part
-// would also wait for every global load in flight, the LDS-direct ones
-// included.  The compiler fences keep LDS instructions on their side of it;
-// the explicit wait covers their results, which the compiler would otherwise
-// be free to collect after the barrier.
-__device__ __forceinline__ void lds_barrier() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt unconstrained
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 template <int RB, int WR>
 struct PfShape {
   static_assert(RB == 2 || RB == 4, "64- or 128-row tiles");

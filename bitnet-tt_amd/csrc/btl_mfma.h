@@ -30,6 +30,14 @@ __device__ __forceinline__ v4i unpack_b(uint32_t d) {
 
 __device__ __forceinline__ v4i ld128(const void* p) { return *reinterpret_cast<const v4i*>(p); }
 
+// 16-byte load through a pointer known to address global memory.  A pointer
+// read from memory (a table of weight addresses) is generic to the compiler,
+// which then emits a flat load; flat loads count in the LDS/scalar counter as
+// well, so every later LDS wait would also wait for them.
+__device__ __forceinline__ v4i ldg128(const void* p) {
+  return *(const __attribute__((address_space(1))) v4i*)p;
+}
+
 // Row of element r (0..15) of a lane's 32x32 MFMA accumulator (its column is
 // lane & 31).
 __device__ __forceinline__ int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }

@@ -1,0 +1,885 @@
+// The BitLinear portion of a whole batch-32 decode step of a BitNet b1.58
+// model as one persistent launch on gfx950 (every layer's QKV, o_proj,
+// gate||up and down; src/bitnet_tt/inference/generator_batch32.py:713-761).
+//
+// Roles.  One workgroup per CU, 512 threads.
+//   Row workgroups 0..31: one token row each.  A row workgroup keeps its row
+//     of the residual stream (hidden) in registers for the whole step and runs
+//     every elementwise stage of that row: residual adds, RMSNorm, per-token
+//     absmax int8 quantisation into the GEMM's operand tile, publication.
+//   GEMM workgroups 32..: one unit (column tiles x row half) of each
+//     BitLinear.  The weights of a unit are loaded into registers one
+//     BitLinear ahead (while the GEMMs of the current one wait for their
+//     operand tile), so no weight load is on the hand-off chain.
+//
+// Per layer (BitLinear j = QKV, O, GU, DN):
+//   row:  y = RMSNorm(h; input_layernorm) -> int8 tile[QKV]                 publish
+//   GEMM: qkv = bf16(acc * s_seg * a)                       -> tagged words, qkv_out
+//   row:  wait for row m of qkv (the attention of that user needs exactly it;
+//         the BitLinear portion reads its output from the attention stand-in
+//         buffer), y = RMSNorm(attn; attn_sub_norm) -> tile[O]               publish
+//   GEMM: o = bf16(acc * s * a)                                -> tagged words
+//   row:  h = bf16(h + o); y = RMSNorm(h; post_attention_layernorm) -> tile[GU]
+//   GEMM: relu(g)^2 * u (gate tile and up tile in one unit)    -> tagged words, ffn_h
+//   row:  y = RMSNorm(r; ffn_sub_norm) -> tile[DN]
+//   GEMM: d = bf16(acc * s * a)                                -> tagged words
+//   row:  h = bf16(h + d), next layer.
+// The arithmetic is that of btl_bitlinear_fused (same row code, same epilogue
+// expressions), so the step is bit-identical to the 120 single-BitLinear
+// launches.
+//
+// Hand-offs (every one crosses XCDs; a coherent hop costs ~0.45 us each way):
+//   row -> GEMM: the row's int8 operand bytes and a/127 with device-coherent
+//     stores, a wait for their acknowledgement, then the row's flag; a GEMM
+//     unit polls the flags of its 16 (or 32) rows and reads the tile with
+//     plain loads (each tile is written once per launch, before its flags).
+//   GEMM -> row: 8-byte words holding two bf16 outputs and a 32-bit tag, each
+//     one device-coherent store; the row workgroup polls the words it needs
+//     (the data is its own flag: no acknowledgement wait, no flag hop).
+// Tags and flags carry (launch epoch << 8 | layer*4 + BitLinear), the epoch
+// being a per-workgroup launch counter kept in the workspace, so nothing is
+// ever cleared.  Every wait is bounded: a wait that runs out sets the error
+// word, and a workgroup that has seen an error stops waiting, so the launch
+// always ends (with invalid outputs).
+#include <string.h>
+
+#include <algorithm>
+
+#include "btl_act_row.h"
+#include "btl_mfma.h"
+#include "btl_trace.h"
+
+namespace btl {
+
+constexpr int kStepRows = 32;       // row workgroups (token rows)
+constexpr int kStepWaves = 8;
+constexpr int kStepPollWave = 7;    // the GEMM workgroup's wave that polls the row flags (then computes)
+constexpr int kStepMaxGrid = 1024;
+constexpr int kStepWSlots = 8;      // weight registers (16 B each) per wave and buffer
+enum { S_QKV = 0, S_O = 1, S_GU = 2, S_DN = 3, kStepOps = 4 };
+
+// Workspace: header, op table, then one region per layer.
+constexpr int64_t kStEpoch = 0;          // [kStepMaxGrid] u32
+constexpr int64_t kStError = 4096;       // u32
+constexpr int64_t kStTable = 8192;       // StepOp[L][4]
+constexpr int kStepMaxLayers = 64;
+
+struct StepOp {
+  const uint32_t* wdev;
+  const uint16_t* gamma;
+  float seg_scale[BTL_MAX_SEGMENTS];
+  int seg_end[BTL_MAX_SEGMENTS];
+  int nseg;
+  int pad[3];
+};
+static_assert(sizeof(StepOp) == 64, "op table entry");
+constexpr int64_t kStHeader = kStTable + (int64_t)kStepMaxLayers * kStepOps * sizeof(StepOp);
+
+struct StepArgs {
+  const StepOp* ops;  // [L][4] (in the workspace)
+  int L, M, H, F, NQKV;
+  int KSH, KSF;       // superblocks of K = H and K = F
+  float eps;
+  const uint16_t* attn;  // [M][H] o_proj input (attention output stand-in)
+  uint16_t* hidden;      // [M][H] in/out
+  uint16_t* qkv_out;     // [M][NQKV]
+  uint16_t* ffn_h;       // [M][F]
+  uint32_t* epoch;
+  uint32_t* error;
+  char* layers;          // first layer region
+  int64_t layer_bytes;
+  int64_t off_xa[kStepOps], off_adq, off_flag, off_out[kStepOps];
+  unsigned spin_limit;
+};
+
+__device__ __forceinline__ uint32_t step_tag(uint32_t E, int l, int j) { return (E << 8) | (uint32_t)(l * 4 + j); }
+
+// Measurement builds (-DBTL_TRACE) time-stamp the phases of one layer.
+#ifndef BTL_STEP_TRACE_LAYER
+#define BTL_STEP_TRACE_LAYER 10
+#endif
+#define STEP_TRACE(l, ev)                         \
+  do {                                            \
+    if ((l) == BTL_STEP_TRACE_LAYER) BTL_TRACE_AT(ev); \
+  } while (0)
+__device__ __forceinline__ char* layer_base(const StepArgs& p, int l) { return p.layers + (int64_t)l * p.layer_bytes; }
+__device__ __forceinline__ int8_t* tile_of(const StepArgs& p, int l, int j) {
+  return reinterpret_cast<int8_t*>(layer_base(p, l) + p.off_xa[j]);
+}
+__device__ __forceinline__ float* adq_of(const StepArgs& p, int l, int j) {
+  return reinterpret_cast<float*>(layer_base(p, l) + p.off_adq) + j * 32;
+}
+__device__ __forceinline__ uint32_t* flag_of(const StepArgs& p, int l, int j, int m) {
+  return reinterpret_cast<uint32_t*>(layer_base(p, l) + p.off_flag) + (j * 32 + m) * 32;  // own 128-byte line
+}
+// tagged output words of BitLinear j, row m (N_j / 2 words per row)
+__device__ __forceinline__ uint64_t* out_of(const StepArgs& p, int l, int j) {
+  return reinterpret_cast<uint64_t*>(layer_base(p, l) + p.off_out[j]);
+}
+
+__device__ __forceinline__ float op_seg_scale(const StepOp& op, int n) {
+  float s = op.seg_scale[0];
+#pragma unroll
+  for (int i = 0; i + 1 < BTL_MAX_SEGMENTS; ++i)
+    if (i + 1 < op.nseg && n >= op.seg_end[i]) s = op.seg_scale[i + 1];
+  return s;
+}
+
+// Bounded wait state of a workgroup: once any wait anywhere ran out, the
+// error word is set and waits end early.
+struct WaitState {
+  bool dead;
+};
+__device__ __forceinline__ bool should_stop(const StepArgs& p, unsigned n, WaitState& ws) {
+  if (n > p.spin_limit) {
+    st_coherent(p.error, 1u);
+    ws.dead = true;
+    return true;
+  }
+  if ((n & 255u) == 255u && ld_coherent(p.error) != 0u) {
+    ws.dead = true;
+    return true;
+  }
+  return false;
+}
+
+// ------------------------------------------------------------------ rows ----
+// Chunk c = tid + 512 i of a row holds its elements 8c .. 8c + 7.
+
+// Waits for the tagged words of row m of an output with `ncols` columns and
+// returns this thread's chunks as bf16 pairs (pr[i][0..3]).  Each thread polls
+// its own words and re-reads only the ones whose tag is not there yet.
+template <int C>
+__device__ void wait_row_words(const StepArgs& p, const uint64_t* row, int ncols, uint32_t want, uint32_t (&pr)[C][4],
+                               WaitState& ws) {
+  const int tid = threadIdx.x;
+  const int nch = ncols >> 3;
+  unsigned pending = 0u;  // bit 4i + k: word k of chunk i still to read
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) pr[i][k] = 0u;
+    if (tid + kActThreads * i < nch) pending |= 0xFu << (4 * i);
+  }
+  unsigned n = 0;
+  while (pending && !ws.dead) {
+#pragma unroll
+    for (int i = 0; i < C; ++i)
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (pending & (1u << (4 * i + k))) {
+          const uint64_t d = ld_coherent(row + 4 * (tid + kActThreads * i) + k);
+          if ((uint32_t)(d >> 32) == want) {
+            pr[i][k] = (uint32_t)d;
+            pending &= ~(1u << (4 * i + k));
+          }
+        }
+    if (!pending) break;
+    if (should_stop(p, ++n, ws)) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+template <int C>
+__device__ __forceinline__ void load_gain(const uint16_t* gamma, int nch, uint4 (&g)[C]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    const int c = tid + kActThreads * i;
+    g[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (c < nch) {
+      const v4i t = ldg128(gamma + 8 * c);
+      g[i] = make_uint4((uint32_t)t.x, (uint32_t)t.y, (uint32_t)t.z, (uint32_t)t.w);
+    }
+  }
+}
+
+template <int C>
+__device__ __forceinline__ void pairs_to_floats(const uint32_t (&pr)[C][4], float (&v)[C][8]) {
+#pragma unroll
+  for (int i = 0; i < C; ++i)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[i][2 * k] = bf2f((uint16_t)(pr[i][k] & 0xffffu));
+      v[i][2 * k + 1] = bf2f((uint16_t)(pr[i][k] >> 16));
+    }
+}
+
+// RMSNorm with gain g, absmax int8 quantisation into the tile of (l, j), a/127,
+// then the row's flag (after the stores are acknowledged).  Rows m >= M
+// publish zeros.  The same row code as btl_bitlinear_fused.
+template <int C>
+__device__ void publish_row(const StepArgs& p, int l, int j, int m, int K, int KS, float (&v)[C][8],
+                            const uint4 (&g)[C], uint32_t want, float* s_sum, float* s_max) {
+  const int tid = threadIdx.x;
+  const int nch = K >> 3, nchp = KS * 16;
+  int8_t* xa = tile_of(p, l, j);
+  float* adq = adq_of(p, l, j);
+  if (m < p.M) {
+    const float r = row_rms_inv<C>(v, nch, K, p.eps, tid, s_sum);
+    row_apply_norm<C>(v, g, true, r, nch, tid);
+    const float a = row_absmax<C>(v, nch, 1e-5f, tid, s_max);
+    const float scale = 127.0f / a;
+    if (tid == 0) st_coherent(adq + m, a / 127.0f);
+    int rs = 0;
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+      const int c = tid + kActThreads * i;
+      if (c < nch) {
+        uint32_t lo, hi;
+        quant8(v[i], scale, lo, hi, rs);
+        store_chunk<true>(xa, m, c, KS, lo, hi);
+      }
+    }
+    for (int c = nch + tid; c < nchp; c += kActThreads) store8<true>(xa + xa_offset(m, 8 * c, KS), 0u, 0u);
+  } else {
+    for (int c = tid; c < nchp; c += kActThreads) store8<true>(xa + xa_offset(m, 8 * c, KS), 0u, 0u);
+    if (tid == 0) st_coherent(adq + m, 0.0f);
+  }
+  wait_memory();
+  __syncthreads();
+  if (tid == 0) st_coherent(flag_of(p, l, j, m), want);
+}
+
+// CH: chunks per thread of a row of H (and of the QKV output, NQKV <= 4096);
+// CF: of a row of F.
+template <int CH, int CF>
+__device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t E, float* s_sum, float* s_max) {
+  const int tid = threadIdx.x;
+  const bool live = m < p.M;
+  const int nh = p.H >> 3, nf = p.F >> 3;
+  WaitState ws{false};
+  uint32_t hid[CH][4];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int c = tid + kActThreads * i;
+    uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+    if (live && c < nh) raw = *reinterpret_cast<const uint4*>(p.hidden + (int64_t)m * p.H + 8 * c);
+    hid[i][0] = raw.x;
+    hid[i][1] = raw.y;
+    hid[i][2] = raw.z;
+    hid[i][3] = raw.w;
+  }
+  for (int l = 0; l < p.L; ++l) {
+    const StepOp* ops = sops + l * kStepOps;
+    // ---- QKV: RMSNorm(h; input_layernorm)
+    {
+      float v[CH][8];
+      uint4 g[CH];
+      load_gain<CH>(ops[S_QKV].gamma, nh, g);
+      pairs_to_floats<CH>(hid, v);
+      STEP_TRACE(l, 0);
+      publish_row<CH>(p, l, S_QKV, m, p.H, p.KSH, v, g, step_tag(E, l, S_QKV), s_sum, s_max);
+      STEP_TRACE(l, 1);
+    }
+    // ---- O: the user's QKV row, then RMSNorm(attn; attn_sub_norm)
+    {
+      uint4 g[CH];
+      load_gain<CH>(ops[S_O].gamma, nh, g);
+      uint32_t pr[CH][4];
+      if (live) wait_row_words<CH>(p, out_of(p, l, S_QKV) + (int64_t)m * (p.NQKV >> 1), p.NQKV, step_tag(E, l, S_QKV),
+                                   pr, ws);
+      STEP_TRACE(l, 2);
+      float v[CH][8];
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int c = tid + kActThreads * i;
+        uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+        if (live && c < nh) raw = *reinterpret_cast<const uint4*>(p.attn + (int64_t)m * p.H + 8 * c);
+        pr[i][0] = raw.x;
+        pr[i][1] = raw.y;
+        pr[i][2] = raw.z;
+        pr[i][3] = raw.w;
+      }
+      pairs_to_floats<CH>(pr, v);
+      publish_row<CH>(p, l, S_O, m, p.H, p.KSH, v, g, step_tag(E, l, S_O), s_sum, s_max);
+      STEP_TRACE(l, 3);
+    }
+    // ---- GU: h = bf16(h + o); RMSNorm(h; post_attention_layernorm)
+    {
+      uint4 g[CH];
+      load_gain<CH>(ops[S_GU].gamma, nh, g);
+      uint32_t pr[CH][4];
+      if (live) wait_row_words<CH>(p, out_of(p, l, S_O) + (int64_t)m * (p.H >> 1), p.H, step_tag(E, l, S_O), pr, ws);
+      STEP_TRACE(l, 4);
+#pragma unroll
+      for (int i = 0; i < CH; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t lo = f2bf(bf2f((uint16_t)(hid[i][k] & 0xffffu)) + bf2f((uint16_t)(pr[i][k] & 0xffffu)));
+          const uint32_t hi = f2bf(bf2f((uint16_t)(hid[i][k] >> 16)) + bf2f((uint16_t)(pr[i][k] >> 16)));
+          hid[i][k] = live ? (lo | (hi << 16)) : 0u;
+        }
+      float v[CH][8];
+      pairs_to_floats<CH>(hid, v);
+      publish_row<CH>(p, l, S_GU, m, p.H, p.KSH, v, g, step_tag(E, l, S_GU), s_sum, s_max);
+      STEP_TRACE(l, 5);
+    }
+    // ---- DN: RMSNorm(relu(g)^2 * u; ffn_sub_norm)
+    {
+      uint4 g[CF];
+      load_gain<CF>(ops[S_DN].gamma, nf, g);
+      uint32_t pr[CF][4];
+      if (live) {
+        wait_row_words<CF>(p, out_of(p, l, S_GU) + (int64_t)m * (p.F >> 1), p.F, step_tag(E, l, S_GU), pr, ws);
+        STEP_TRACE(l, 6);
+      } else {
+#pragma unroll
+        for (int i = 0; i < CF; ++i)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) pr[i][k] = 0u;
+      }
+      float v[CF][8];
+      pairs_to_floats<CF>(pr, v);
+      publish_row<CF>(p, l, S_DN, m, p.F, p.KSF, v, g, step_tag(E, l, S_DN), s_sum, s_max);
+      STEP_TRACE(l, 7);
+    }
+    // ---- h = bf16(h + d)
+    {
+      uint32_t pr[CH][4];
+      if (live) wait_row_words<CH>(p, out_of(p, l, S_DN) + (int64_t)m * (p.H >> 1), p.H, step_tag(E, l, S_DN), pr, ws);
+#pragma unroll
+      for (int i = 0; i < CH; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t lo = f2bf(bf2f((uint16_t)(hid[i][k] & 0xffffu)) + bf2f((uint16_t)(pr[i][k] & 0xffffu)));
+          const uint32_t hi = f2bf(bf2f((uint16_t)(hid[i][k] >> 16)) + bf2f((uint16_t)(pr[i][k] >> 16)));
+          hid[i][k] = live ? (lo | (hi << 16)) : 0u;
+        }
+    }
+  }
+  if (live) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + kActThreads * i;
+      if (c < nh)
+        *reinterpret_cast<uint4*>(p.hidden + (int64_t)m * p.H + 8 * c) =
+            make_uint4(hid[i][0], hid[i][1], hid[i][2], hid[i][3]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ GEMM ----
+// Units.  QKV: 2 column tiles x one 16-row half; O, DN: 1 tile x half; GU: a
+// gate tile and its up tile x all 32 rows.  Unit u runs on GEMM workgroup u;
+// the two halves of a column group are 8 workgroups apart, so round-robin
+// dispatch puts them on one XCD and its L2 fetches their weights once.
+struct HalfUnit {
+  int g, h;
+};
+__device__ __forceinline__ HalfUnit half_unit(int u, int ngroups) {
+  const int g8 = ngroups & ~7;
+  HalfUnit r;
+  if (u < 2 * g8) {
+    r.g = ((u >> 4) << 3) | (u & 7);
+    r.h = (u >> 3) & 1;
+  } else {
+    const int i = u - 2 * g8, rem = ngroups - g8;
+    r.g = g8 + i % rem;
+    r.h = i / rem;
+  }
+  return r;
+}
+
+template <int J>
+struct OpShape;  // TPW: weight tiles per unit; HALF: 16-row unit
+template <>
+struct OpShape<S_QKV> {
+  static constexpr int TPW = 2, HALF = 1;
+};
+template <>
+struct OpShape<S_O> {
+  static constexpr int TPW = 1, HALF = 1;
+};
+template <>
+struct OpShape<S_GU> {
+  static constexpr int TPW = 2, HALF = 0;
+};
+template <>
+struct OpShape<S_DN> {
+  static constexpr int TPW = 1, HALF = 1;
+};
+
+__device__ __forceinline__ int op_n(const StepArgs& p, int j) {  // output columns of the GEMM
+  return j == S_QKV ? p.NQKV : j == S_GU ? 2 * p.F : p.H;
+}
+__device__ __forceinline__ int op_ks(const StepArgs& p, int j) { return j == S_DN ? p.KSF : p.KSH; }
+__device__ __forceinline__ int op_units(const StepArgs& p, int j) {
+  const int NT = op_n(p, j) / 32;
+  return j == S_GU ? NT / 2 : j == S_QKV ? NT : 2 * NT;  // QKV: NT/2 groups x 2 halves
+}
+
+// Tile t of unit u of BitLinear J (and the unit's half).
+template <int J>
+__device__ __forceinline__ int unit_tile(const StepArgs& p, int u, int t, int& h) {
+  const int NT = op_n(p, J) / 32;
+  if (J == S_GU) {
+    h = 0;
+    return t == 0 ? u : u + NT / 2;
+  }
+  const HalfUnit hu = half_unit(u, NT / OpShape<J>::TPW);
+  h = hu.h;
+  return hu.g * OpShape<J>::TPW + t;
+}
+
+// This wave's superblock range of K: waves w and w + 4 share a SIMD, so the
+// first KS % 8 waves take one superblock more (0-3 before 4-7) and every
+// SIMD gets the same share.
+__device__ __forceinline__ void wave_ks(int KS, int wv, int& wb, int& we) {
+  const int base = KS / kStepWaves, rem = KS % kStepWaves;
+  wb = wv * base + (wv < rem ? wv : rem);
+  we = wb + base + (wv < rem ? 1 : 0);
+}
+
+// Weights of this wave's superblocks of unit u of BitLinear J into w
+// (slot t * NSW + i); slots past the wave's range re-read its last superblock.
+template <int J, int NSW>
+__device__ __forceinline__ void load_unit_weights(const StepArgs& p, const StepOp* sops, int l, int u,
+                                                  v4i (&w)[kStepWSlots]) {
+  static_assert(OpShape<J>::TPW * NSW <= kStepWSlots, "weight slots");
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (u >= op_units(p, J)) return;
+  const int KS = op_ks(p, J);
+  int wb, we;
+  wave_ks(KS, wv, wb, we);
+  if (wb >= we) return;
+  const uint32_t* wdev = sops[l * kStepOps + J].wdev;
+#pragma unroll
+  for (int t = 0; t < OpShape<J>::TPW; ++t) {
+    int h;
+    const int tile = unit_tile<J>(p, u, t, h);
+#pragma unroll
+    for (int i = 0; i < NSW; ++i) {
+      const int sb = wb + i < we ? wb + i : we - 1;
+      w[t * NSW + i] = ldg128(wdev + (((int64_t)tile * KS + sb) * 64 + lane) * 4);
+    }
+  }
+}
+
+// Poll wave: wait for the flags of rows [r0, r0 + n) of (l, j).
+__device__ void wait_flags(const StepArgs& p, int l, int j, int r0, int n, uint32_t want, WaitState& ws) {
+  const int lane = threadIdx.x & 63;
+  unsigned k = 0;
+  while (!ws.dead) {
+    const bool ok = lane >= n || ld_coherent(flag_of(p, l, j, r0 + lane)) == want;
+    if (__all(ok)) break;
+    if (should_stop(p, ++k, ws)) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// One BitLinear J of layer l on GEMM workgroup gi: wait for the operand
+// tile's rows, MFMA against the weights held in w, prefetch the next
+// BitLinear's weights into wn, reduce the waves in LDS, epilogue.
+template <int J, int NSW, int NJ, int NNSW>
+__device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int gi, uint32_t E,
+                             const v4i (&w)[kStepWSlots], v4i (&wn)[kStepWSlots], int nl, int32_t* lds,
+                             WaitState& ws) {
+  constexpr int TPW = OpShape<J>::TPW;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int units = op_units(p, J);
+  if (gi >= units) {
+    if (nl < p.L) load_unit_weights<NJ, NNSW>(p, sops, nl, gi, wn);
+    return;
+  }
+  const int KS = op_ks(p, J);
+  const StepOp& op = sops[l * kStepOps + J];
+  int tile[TPW];
+  int h = 0;
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) tile[t] = unit_tile<J>(p, gi, t, h);
+  const uint32_t want = step_tag(E, l, J);
+  if (wv == kStepPollWave) {
+    if (OpShape<J>::HALF)
+      wait_flags(p, l, J, 16 * h, 16, want, ws);
+    else
+      wait_flags(p, l, J, 0, 32, want, ws);
+  }
+  lds_barrier();  // the operand rows are out (no wait for loads in flight)
+  STEP_TRACE(l, 8 + 2 * J);
+  const int8_t* xa = tile_of(p, l, J);
+  const float* adq = adq_of(p, l, J);
+  int wb, we;
+  wave_ks(KS, wv, wb, we);
+  const int cnt = we - wb;
+
+  if constexpr (OpShape<J>::HALF) {
+    // ---- 16-row half on v_mfma_i32_16x16x64_i8 (see gemm_decode_half) ----
+    const int er = tid >> 5, ec = tid & 31;
+    const int row = 16 * h + er;
+    const float ad = ld_coherent(adq + row);
+    const int a_lane = 16 * h + (lane & 15) + 32 * ((lane >> 4) & 1);
+    const int a_step = lane >> 5;
+    v4i a[NSW][2];
+#pragma unroll
+    for (int i = 0; i < NSW; ++i) {
+      if (i < cnt)
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) a[i][pp] = ld128(xa + (((wb + i) * 4 + 2 * pp + a_step) * 64 + a_lane) * 16);
+    }
+    v4i acc[TPW][2];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) acc[t][0] = acc[t][1] = (v4i){0, 0, 0, 0};
+    int32_t rs_lane = 0;  // sum of this lane's operand bytes: row 16h + (lane & 15), k-group lane >> 4
+#pragma unroll
+    for (int i = 0; i < NSW; ++i) {
+      if (i < cnt) {
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+#pragma unroll
+          for (int t = 0; t < TPW; ++t) {
+            const auto s32 = __builtin_amdgcn_permlane32_swap((uint32_t)w[t * NSW + i][2 * pp],
+                                                              (uint32_t)w[t * NSW + i][2 * pp + 1], false, false);
+            const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
+            acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[0]), acc[t][0], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[1]), acc[t][1], 0, 0, 0);
+          }
+          rs_lane = bytes_sum(a[i][pp], rs_lane);
+        }
+      }
+    }
+    // LDS: red[8][TPW][8][64], red_rs[8][16]
+    int32_t* red = lds;
+    int32_t* red_rs = lds + kStepWaves * TPW * 8 * 64;
+    rs_lane += (int32_t)xor_partner_u<16>((uint32_t)rs_lane);  // the four k-groups of a row
+    rs_lane += (int32_t)xor_partner_u<32>((uint32_t)rs_lane);
+    if (lane < 16) red_rs[wv * 16 + lane] = rs_lane;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        red[((wv * TPW + t) * 8 + q) * 64 + lane] = acc[t][0][q];
+        red[((wv * TPW + t) * 8 + 4 + q) * 64 + lane] = acc[t][1][q];
+      }
+    lds_barrier();
+    const int reg = 4 * (ec >> 4) + (er & 3), src = 16 * (er >> 2) + (ec & 15);
+    int32_t rs = 0;
+#pragma unroll
+    for (int v2 = 0; v2 < kStepWaves; ++v2) rs += red_rs[v2 * 16 + er];
+    int32_t vsum[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      int32_t sum = -rs;
+#pragma unroll
+      for (int v2 = 0; v2 < kStepWaves; ++v2) sum += red[((v2 * TPW + t) * 8 + reg) * 64 + src];
+      vsum[t] = sum;
+    }
+    lds_barrier();  // LDS free for the next BitLinear
+    uint64_t* outw = out_of(p, l, J);
+    const int n_row = op_n(p, J);
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int n = tile[t] * 32 + ec;
+      const uint32_t o = f2bf((float)vsum[t] * (op_seg_scale(op, n) * ad));
+      const uint32_t pair = o | ((uint32_t)__shfl_down((int)o, 1, 64) << 16);  // lanes ec, ec+1 share the row
+      if (row < p.M) {
+        if ((ec & 1) == 0) st_coherent(outw + (int64_t)row * (n_row >> 1) + (n >> 1), ((uint64_t)want << 32) | pair);
+        if (J == S_QKV) p.qkv_out[(int64_t)row * p.NQKV + n] = (uint16_t)o;
+      }
+    }
+    STEP_TRACE(l, 9 + 2 * J);
+    // The next BitLinear's weights, issued after this one's last wait: its
+    // hand-off takes longer than the loads, and no wait here covers them.
+    if (nl < p.L) load_unit_weights<NJ, NNSW>(p, sops, nl, gi, wn);
+  } else {
+    // ---- gate tile and up tile, all 32 rows, v_mfma_i32_32x32x32_i8 ----
+    float ad_r[2];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) ad_r[rr] = ld_coherent(adq + acc_row(wv + kStepWaves * rr, lane));
+    v4i a[NSW][4];
+#pragma unroll
+    for (int i = 0; i < NSW; ++i) {
+      if (i < cnt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[i][q] = ld128(xa + (((wb + i) * 4 + q) * 64 + lane) * 16);
+    }
+    v16i acc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[t] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    int32_t rs_lane = 0;
+#pragma unroll
+    for (int i = 0; i < NSW; ++i) {
+      if (i < cnt) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+            acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][q], unpack_b((uint32_t)w[t * NSW + i][q]), acc[t], 0,
+                                                           0, 0);
+          rs_lane = bytes_sum(a[i][q], rs_lane);
+        }
+      }
+    }
+    // LDS: red[8][2][16][64], red_rs[8][32]
+    int32_t* red = lds;
+    int32_t* red_rs = lds + kStepWaves * 2 * 16 * 64;
+    {
+      const int32_t rs_row = rs_lane + (int32_t)xor_partner_u<32>((uint32_t)rs_lane);
+      if (lane < 32) red_rs[wv * 32 + lane] = rs_row;
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[((wv * 2 + t) * 16 + r) * 64 + lane] = acc[t][r];
+    lds_barrier();
+    const int jc = lane & 31;
+    int32_t vg[2], vu[2];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int r = wv + kStepWaves * rr;
+      const int i = acc_row(r, lane);
+      int32_t rs = 0;
+#pragma unroll
+      for (int v2 = 0; v2 < kStepWaves; ++v2) rs += red_rs[v2 * 32 + i];
+      int32_t sg = -rs, su = -rs;
+#pragma unroll
+      for (int v2 = 0; v2 < kStepWaves; ++v2) {
+        sg += red[((v2 * 2 + 0) * 16 + r) * 64 + lane];
+        su += red[((v2 * 2 + 1) * 16 + r) * 64 + lane];
+      }
+      vg[rr] = sg;
+      vu[rr] = su;
+    }
+    lds_barrier();
+    uint64_t* outw = out_of(p, l, J);
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int i = acc_row(wv + kStepWaves * rr, lane);
+      const int ng = tile[0] * 32 + jc, nu = tile[1] * 32 + jc;
+      const float gg = bf2f(f2bf((float)vg[rr] * (op_seg_scale(op, ng) * ad_r[rr])));
+      const float uu = bf2f(f2bf((float)vu[rr] * (op_seg_scale(op, nu) * ad_r[rr])));
+      const float gr = gg > 0.0f ? gg : 0.0f;
+      const float sq = bf2f(f2bf(gr * gr));
+      const uint32_t hv = f2bf(sq * uu);
+      const uint32_t pair = hv | ((uint32_t)__shfl_down((int)hv, 1, 64) << 16);
+      if (i < p.M) {
+        if ((jc & 1) == 0) st_coherent(outw + (int64_t)i * (p.F >> 1) + (ng >> 1), ((uint64_t)want << 32) | pair);
+        p.ffn_h[(int64_t)i * p.F + ng] = (uint16_t)hv;
+      }
+    }
+    STEP_TRACE(l, 9 + 2 * J);
+    if (nl < p.L) load_unit_weights<NJ, NNSW>(p, sops, nl, gi, wn);
+  }
+}
+
+template <int NSWH, int NSWF>
+__device__ void step_gemm(const StepArgs& p, const StepOp* sops, int gi, uint32_t E, int32_t* lds) {
+  WaitState ws{false};
+  v4i wa[kStepWSlots], wb[kStepWSlots];
+  load_unit_weights<S_QKV, NSWH>(p, sops, 0, gi, wa);
+  for (int l = 0; l < p.L; ++l) {
+    step_gemm_op<S_QKV, NSWH, S_O, NSWH>(p, sops, l, gi, E, wa, wb, l, lds, ws);
+    step_gemm_op<S_O, NSWH, S_GU, NSWH>(p, sops, l, gi, E, wb, wa, l, lds, ws);
+    step_gemm_op<S_GU, NSWH, S_DN, NSWF>(p, sops, l, gi, E, wa, wb, l, lds, ws);
+    step_gemm_op<S_DN, NSWF, S_QKV, NSWH>(p, sops, l, gi, E, wb, wa, l + 1, lds, ws);
+  }
+}
+
+template <int CH, int CF, int NSWH, int NSWF>
+__global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
+  // GEMM reductions need max(8*2*8*64 + 8*16, 8*2*16*64 + 8*32) int32 (64.5 KiB); rows use the first 64
+  // bytes.  96 KiB: more than half of a CU's LDS, so no CU ever holds two workgroups of the launch.
+  // The op table (up to 16 KiB) is copied into LDS above the reduction area, so reading a weight
+  // address or a scale is an LDS read, never a vector memory load waited for with the weight stream.
+  __shared__ __attribute__((aligned(16))) int32_t lds[24576];
+  constexpr int kTableInts = kStepMaxLayers * kStepOps * (int)sizeof(StepOp) / 4;
+  static_assert(kStepWaves * 2 * 16 * 64 + kStepWaves * 32 + kTableInts <= 24576, "LDS layout");
+  StepOp* sops = reinterpret_cast<StepOp*>(lds + (24576 - kTableInts));
+  {
+    const uint4* src = reinterpret_cast<const uint4*>(p.ops);
+    uint4* dst = reinterpret_cast<uint4*>(sops);
+    const int n16 = p.L * kStepOps * (int)sizeof(StepOp) / 16;
+    for (int i = threadIdx.x; i < n16; i += blockDim.x) dst[i] = src[i];
+  }
+  __syncthreads();
+  const int b = blockIdx.x;
+  const uint32_t E = p.epoch[b] + 1u;  // this launch (written by the previous launch of the step)
+  if (b < kStepRows) {
+    step_row<CH, CF>(p, sops, b, E, reinterpret_cast<float*>(lds), reinterpret_cast<float*>(lds) + kActWaves);
+  } else {
+    step_gemm<NSWH, NSWF>(p, sops, b - kStepRows, E, lds);
+  }
+  if (threadIdx.x == 0) p.epoch[b] = E;
+}
+
+// ---------------------------------------------------------------- host ----
+struct StepSizes {
+  int64_t off_xa[kStepOps], off_adq, off_flag, off_out[kStepOps], layer_bytes, total;
+};
+
+static StepSizes step_sizes(int64_t H, int64_t F, int64_t NQKV, int64_t L) {
+  StepSizes z;
+  const int64_t Ks[kStepOps] = {H, H, H, F};
+  const int64_t Nout[kStepOps] = {NQKV, H, F, H};  // bf16 columns a row workgroup reads back
+  int64_t off = 0;
+  for (int j = 0; j < kStepOps; ++j) {
+    z.off_xa[j] = off;
+    off += round_up(32 * ksb(Ks[j]) * 128, 4096);
+  }
+  z.off_adq = off;
+  off += 4096;
+  z.off_flag = off;
+  off += kStepOps * 32 * 128;
+  for (int j = 0; j < kStepOps; ++j) {
+    z.off_out[j] = off;
+    off += round_up(32 * (Nout[j] / 2) * 8, 4096);
+  }
+  z.layer_bytes = round_up(off, 65536);
+  z.total = kStHeader + z.layer_bytes * L;
+  return z;
+}
+
+static int step_grid() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return cus;
+}
+
+static int step_check_shape(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L) {
+  if (M <= 0 || M > 32) return set_error(BTL_ERR_SHAPE, "btl_decode_step: M=%lld (1..32 decode rows)", (long long)M);
+  if (L <= 0 || L > kStepMaxLayers)
+    return set_error(BTL_ERR_SHAPE, "btl_decode_step: L=%lld layers (1..%d)", (long long)L, kStepMaxLayers);
+  if (H % 128 || F % 128 || NQKV % 64 || H <= 0 || F <= 0 || NQKV <= 0)
+    return set_error(BTL_ERR_SHAPE, "btl_decode_step: H=%lld and F=%lld must be multiples of 128, NQKV=%lld of 64",
+                     (long long)H, (long long)F, (long long)NQKV);
+  if (H > 4096 || NQKV > 4096 || F > 8192)
+    return set_error(BTL_ERR_SHAPE, "btl_decode_step: H=%lld NQKV=%lld (<= 4096), F=%lld (<= 8192) exceed the kernel's "
+                     "row registers", (long long)H, (long long)NQKV, (long long)F);
+  // weights per wave: ceil(KS/8) superblocks per tile within the register slots
+  const int64_t nswh = (ksb(H) + kStepWaves - 1) / kStepWaves, nswf = (ksb(F) + kStepWaves - 1) / kStepWaves;
+  if (nswh > 3 || nswf > 7)
+    return set_error(BTL_ERR_SHAPE, "btl_decode_step: H=%lld or F=%lld too large for the weight registers",
+                     (long long)H, (long long)F);
+  const int grid = step_grid();
+  const int64_t units = std::max({NQKV / 32, 2 * (H / 32), F / 32});
+  if (grid <= kStepRows || grid > kStepMaxGrid || units > grid - kStepRows)
+    return set_error(BTL_ERR_SHAPE, "btl_decode_step: %lld GEMM units do not fit %d workgroups", (long long)units,
+                     grid - kStepRows);
+  return BTL_OK;
+}
+
+}  // namespace btl
+
+using namespace btl;
+
+extern "C" {
+
+int64_t btl_decode_step_workspace_bytes(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L) {
+  if (M <= 0 || M > 32 || H <= 0 || F <= 0 || NQKV <= 0 || L <= 0 || L > kStepMaxLayers) return 0;
+  return step_sizes(H, F, NQKV, L).total;
+}
+
+int64_t btl_decode_step_error_offset(void) { return kStError; }
+
+int btl_decode_step_prepare(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L,
+                            const btl_layer_weight_t* weights, void* workspace, size_t workspace_bytes) {
+  clear_error();
+  int rc = step_check_shape(M, H, F, NQKV, L);
+  if (rc) return rc;
+  if (!weights || !workspace) return set_error(BTL_ERR_NULL, "btl_decode_step_prepare: null pointer");
+  if (!aligned(workspace, 256)) return set_error(BTL_ERR_ALIGN, "btl_decode_step_prepare: workspace must be 256-byte aligned");
+  const StepSizes z = step_sizes(H, F, NQKV, L);
+  if ((int64_t)workspace_bytes < z.total)
+    return set_error(BTL_ERR_WORKSPACE, "btl_decode_step_prepare: workspace %zu < %lld bytes", workspace_bytes,
+                     (long long)z.total);
+  static const char* names[kStepOps] = {"qkv", "o_proj", "gate_up", "down"};
+  const int64_t Ns[kStepOps] = {NQKV, H, 2 * F, H};
+  StepOp table[kStepMaxLayers * kStepOps];
+  memset(table, 0, sizeof(table));
+  for (int64_t l = 0; l < L; ++l)
+    for (int j = 0; j < kStepOps; ++j) {
+      const btl_layer_weight_t& w = weights[l * kStepOps + j];
+      if (!w.wdev || !w.gamma)
+        return set_error(BTL_ERR_NULL, "btl_decode_step_prepare: layer %lld %s weight or gain is NULL", (long long)l,
+                         names[j]);
+      if (!aligned(w.wdev, 16) || !aligned(w.gamma, 16))
+        return set_error(BTL_ERR_ALIGN, "btl_decode_step_prepare: layer %lld %s weight / gain must be 16-byte aligned",
+                         (long long)l, names[j]);
+      if (w.nseg < 1 || w.nseg > BTL_MAX_SEGMENTS)
+        return set_error(BTL_ERR_ARG, "btl_decode_step_prepare: layer %lld %s has %d segments", (long long)l, names[j],
+                         w.nseg);
+      int64_t prev = 0;
+      for (int i = 0; i < w.nseg; ++i) {
+        if (w.seg_end[i] <= prev || w.seg_end[i] % 32)
+          return set_error(BTL_ERR_ARG, "btl_decode_step_prepare: layer %lld %s segment ends must increase in "
+                           "multiples of 32", (long long)l, names[j]);
+        prev = w.seg_end[i];
+      }
+      if (prev != Ns[j])
+        return set_error(BTL_ERR_ARG, "btl_decode_step_prepare: layer %lld %s last segment end %lld != N=%lld",
+                         (long long)l, names[j], (long long)prev, (long long)Ns[j]);
+      if (j == S_GU && (w.nseg != 2 || w.seg_end[0] != F))
+        return set_error(BTL_ERR_ARG, "btl_decode_step_prepare: layer %lld gate_up needs two segments split at F",
+                         (long long)l);
+      StepOp& op = table[l * kStepOps + j];
+      op.wdev = w.wdev;
+      op.gamma = w.gamma;
+      op.nseg = w.nseg;
+      for (int i = 0; i < BTL_MAX_SEGMENTS; ++i) {
+        op.seg_scale[i] = i < w.nseg ? w.seg_scale[i] : 0.0f;
+        op.seg_end[i] = i < w.nseg ? (int)w.seg_end[i] : (int)Ns[j];
+      }
+    }
+  if (hipMemcpy((char*)workspace + kStTable, table, sizeof(StepOp) * L * kStepOps, hipMemcpyHostToDevice) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(BTL_ERR_LAUNCH, "btl_decode_step_prepare: copying the op table failed");
+  }
+  return BTL_OK;
+}
+
+int btl_decode_step(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, float eps, const uint16_t* attn,
+                    uint16_t* hidden, uint16_t* qkv_out, uint16_t* ffn_h, void* workspace, size_t workspace_bytes,
+                    btl_stream_t stream) {
+  clear_error();
+  int rc = step_check_shape(M, H, F, NQKV, L);
+  if (rc) return rc;
+  if (!attn || !hidden || !qkv_out || !ffn_h || !workspace) return set_error(BTL_ERR_NULL, "btl_decode_step: null pointer");
+  if (!aligned(attn, 16) || !aligned(hidden, 16) || !aligned(workspace, 256) || !aligned(qkv_out, 2) ||
+      !aligned(ffn_h, 2))
+    return set_error(BTL_ERR_ALIGN, "btl_decode_step: attn/hidden must be 16-byte aligned, workspace 256");
+  const StepSizes z = step_sizes(H, F, NQKV, L);
+  if ((int64_t)workspace_bytes < z.total)
+    return set_error(BTL_ERR_WORKSPACE, "btl_decode_step: workspace %zu < %lld bytes", workspace_bytes,
+                     (long long)z.total);
+  char* ws = (char*)workspace;
+  StepArgs a = {};
+  a.ops = reinterpret_cast<const StepOp*>(ws + kStTable);
+  a.L = (int)L;
+  a.M = (int)M;
+  a.H = (int)H;
+  a.F = (int)F;
+  a.NQKV = (int)NQKV;
+  a.KSH = (int)ksb(H);
+  a.KSF = (int)ksb(F);
+  a.eps = eps;
+  a.attn = attn;
+  a.hidden = hidden;
+  a.qkv_out = qkv_out;
+  a.ffn_h = ffn_h;
+  a.epoch = reinterpret_cast<uint32_t*>(ws + kStEpoch);
+  a.error = reinterpret_cast<uint32_t*>(ws + kStError);
+  a.layers = ws + kStHeader;
+  a.layer_bytes = z.layer_bytes;
+  for (int j = 0; j < kStepOps; ++j) {
+    a.off_xa[j] = z.off_xa[j];
+    a.off_out[j] = z.off_out[j];
+  }
+  a.off_adq = z.off_adq;
+  a.off_flag = z.off_flag;
+  a.spin_limit = 1u << 18;
+  const int grid = step_grid();
+  const int ch = act_cpt(H), cf = act_cpt(F);
+  hipStream_t s = (hipStream_t)stream;
+  if (ch == 1 && cf == 1)
+    hipLaunchKernelGGL((k_decode_step<1, 1, 3, 7>), dim3(grid), dim3(512), 0, s, a);
+  else if (ch == 1 && cf == 2)
+    hipLaunchKernelGGL((k_decode_step<1, 2, 3, 7>), dim3(grid), dim3(512), 0, s, a);
+  else
+    return set_error(BTL_ERR_SHAPE, "btl_decode_step: no kernel instance for H=%lld F=%lld", (long long)H, (long long)F);
+  return check_launch("decode step");
+}
+
+}  // extern "C"
+
+BTL_TRACE_READ_FN(btl_trace_read_step)

@@ -241,6 +241,40 @@ int btl_decode_layer(int64_t M, int64_t H, int64_t Q, int64_t F, int64_t NQKV, c
                      uint16_t* ffn_h, uint16_t* qkv_out, void* workspace, size_t workspace_bytes,
                      btl_stream_t stream);
 
+/* ---- persistent decode step ------------------------------------------- */
+
+/* The BitLinear portion of a whole decode step as one launch: for every
+ * layer l, QKV (RMSNorm(hidden; input_layernorm), output to qkv_out), o_proj
+ * (RMSNorm(attn; attn_sub_norm), residual into hidden), gate||up (RMSNorm;
+ * relu(g)^2*u into ffn_h), down (RMSNorm(ffn_h; ffn_sub_norm), residual into
+ * hidden) -- src/bitnet_tt/inference/generator_batch32.py:713-761, with the
+ * attention between QKV and o_proj replaced by the `attn` input (the same
+ * buffer for every layer).  o_proj's row stage starts only after that row's
+ * QKV output exists, as attention would.  Each BitLinear is the arithmetic of
+ * btl_bitlinear_fused (bit-identical results).
+ *
+ * weights: [L][4] = qkv, o_proj, gate_up, down of each layer, with the gain
+ * of the RMSNorm in front of each (qkv: three segments ending at Q, Q+KV,
+ * NQKV; gate_up: two segments split at F).  Shapes: M <= 32 rows, H = the
+ * attention width (o_proj is H -> H), H and F multiples of 128, H <= 3072,
+ * F <= 7168, NQKV <= 4096.  attn [M,H], hidden [M,H] (in/out), qkv_out
+ * [M,NQKV] and ffn_h [M,F] bf16 (the last layer's values).
+ *
+ * Workspace (256-byte aligned): btl_decode_step_workspace_bytes(...) bytes,
+ * zero-filled once, then prepared with btl_decode_step_prepare (which copies
+ * the weight table into it, synchronously: not under graph capture) and used
+ * only by btl_decode_step calls on one device and one stream.  One workgroup
+ * per CU waits on the others: nothing else may hold the GPU's CUs during the
+ * launch (a wait that runs out sets the word at btl_decode_step_error_offset
+ * and the outputs are invalid). */
+int64_t btl_decode_step_workspace_bytes(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L);
+int64_t btl_decode_step_error_offset(void);
+int btl_decode_step_prepare(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L,
+                            const btl_layer_weight_t* weights, void* workspace, size_t workspace_bytes);
+int btl_decode_step(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, float eps, const uint16_t* attn,
+                    uint16_t* hidden, uint16_t* qkv_out, uint16_t* ffn_h, void* workspace, size_t workspace_bytes,
+                    btl_stream_t stream);
+
 /* ---- LM head (final norm is btl_rmsnorm) ------------------------------
  * Replaces the head matmul of src/bitnet_tt/inference/generator_batch32.py:
  * 768-811 (ttnn.matmul of the normed hidden state with the head weight that

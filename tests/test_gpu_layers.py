@@ -268,3 +268,69 @@ def test_c4_full_model_layer_launches_exact(orc, c4_model):
         bad = int((got != hiddens[-1]).sum())
         assert bad == 0, f"run {rep}: {bad} of {got.size} hidden values differ after 30 layers"
         assert np.array_equal(H.bits_of(step.qkv_out), ref_qkv), f"run {rep}: last QKV output"
+
+
+@pytest.mark.parametrize("batch,layers", [(32, 2), (5, 3), (17, 1)])
+def test_persistent_step_mini_matches_per_call(orc, batch, layers):
+    """btl_decode_step (every BitLinear of the step in one launch) against the
+    120-launch chain and the oracle: hidden, the last QKV output and the last
+    FFN intermediate bit for bit, over three launches in a row (the launch
+    epochs advance; nothing is cleared between launches)."""
+    cfg = BitNetMiniConfig(num_layers=layers)
+    step = BitLinearDecodeStep.random_init(cfg, H.dev(), seed=31 + batch, batch=batch).alloc_buffers(seed=32)
+    hid, attn = H.bits_of(step.hidden0), H.bits_of(step.attn_out)
+    for i in range(layers):
+        hid, qkv = oracle_layer(orc, step, i, hid, attn)
+    step.step_per_call()
+    step.check()
+    ref_ffn = H.bits_of(step.ffn_h)
+    assert np.array_equal(H.bits_of(step.hidden), hid)
+    for rep in range(3):
+        print(f"persistent step batch={batch} layers={layers} launch {rep}", flush=True)
+        step.reset_hidden()
+        step.qkv_out.zero_()
+        step.ffn_h.zero_()
+        step.step_persistent()
+        step.check()
+        assert np.array_equal(H.bits_of(step.hidden), hid), f"launch {rep}: hidden"
+        assert np.array_equal(H.bits_of(step.qkv_out), qkv), f"launch {rep}: qkv_out"
+        assert np.array_equal(H.bits_of(step.ffn_h), ref_ffn), f"launch {rep}: ffn_h"
+
+
+def test_persistent_step_graph_replay(orc):
+    """The one-launch step captured in a HIP graph: every replay, with eager
+    work between replays, equals the eager launch."""
+    cfg = BitNetMiniConfig(num_layers=3)
+    step = BitLinearDecodeStep.random_init(cfg, H.dev(), seed=41).alloc_buffers(seed=42)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step.reset_hidden()
+        step.step_persistent()  # prepares this stream's workspace
+    torch.cuda.synchronize()
+    eager = H.bits_of(step.hidden)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step.step_persistent()
+    for rep in range(4):
+        step.reset_hidden()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(H.bits_of(step.hidden), eager), f"replay {rep} differs"
+        _ = torch.ones(1024, device=H.dev()).sum().item()
+    step.check()
+
+
+def test_c4_full_model_persistent_step_exact(orc, c4_model):
+    """The 2B 30-layer step as one btl_decode_step launch against the oracle
+    chain, twice in a row."""
+    step, hiddens, ref_qkv = c4_model
+    for rep in range(2):
+        step.reset_hidden()
+        step.step_persistent()
+        step.check()
+        got = H.bits_of(step.hidden)
+        bad = int((got != hiddens[-1]).sum())
+        assert bad == 0, f"run {rep}: {bad} of {got.size} hidden values differ after 30 layers"
+        assert np.array_equal(H.bits_of(step.qkv_out), ref_qkv), f"run {rep}: last QKV output"
