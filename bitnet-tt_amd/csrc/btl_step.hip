@@ -41,6 +41,7 @@
 // ever cleared.  Every wait is bounded: a wait that runs out sets the error
 // word, and a workgroup that has seen an error stops waiting, so the launch
 // always ends (with invalid outputs).
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -55,7 +56,7 @@ constexpr int kStepRows = 32;       // row workgroups (token rows)
 constexpr int kStepWaves = 8;
 constexpr int kStepPollWave = 7;    // the GEMM workgroup's wave that polls the row flags (then computes)
 constexpr int kStepMaxGrid = 1024;
-constexpr int kStepWSlots = 8;      // weight registers (16 B each) per wave and buffer
+constexpr int kStepWSlots = 7;      // weight registers (16 B each) per wave and buffer
 enum { S_QKV = 0, S_O = 1, S_GU = 2, S_DN = 3, kStepOps = 4 };
 
 // Workspace: header, op table, then one region per layer.
@@ -75,6 +76,31 @@ struct StepOp {
 static_assert(sizeof(StepOp) == 64, "op table entry");
 constexpr int64_t kStHeader = kStTable + (int64_t)kStepMaxLayers * kStepOps * sizeof(StepOp);
 
+// GEMM unit shapes.  QKV, o_proj and gate||up units cover all 32 rows
+// (v_mfma_i32_32x32x32_i8: each unpacked weight dword feeds one MFMA); down,
+// whose operand tile is 221 KB at K = 6912, runs 16-row halves
+// (v_mfma_i32_16x16x64_i8), so that a unit reads half of it.  Every unit
+// covers all of K and writes bf16 outputs (two per tagged word).
+enum { MODE_SCALE = 0, MODE_RELU2 = 1 };
+template <int J>
+struct OpShape;
+template <>
+struct OpShape<S_QKV> {
+  static constexpr int TPW = 1, HALF = 0, MODE = MODE_SCALE;
+};
+template <>
+struct OpShape<S_O> {
+  static constexpr int TPW = 1, HALF = 0, MODE = MODE_SCALE;
+};
+template <>
+struct OpShape<S_GU> {
+  static constexpr int TPW = 2, HALF = 0, MODE = MODE_RELU2;
+};
+template <>
+struct OpShape<S_DN> {
+  static constexpr int TPW = 1, HALF = 1, MODE = MODE_SCALE;
+};
+
 struct StepArgs {
   const StepOp* ops;  // [L][4] (in the workspace)
   int L, M, H, F, NQKV;
@@ -87,7 +113,7 @@ struct StepArgs {
   uint32_t* epoch;
   uint32_t* error;
   char* layers;          // first layer region
-  int64_t layer_bytes;
+  int64_t layer_stride;  // bytes between layers' hand-off regions (0: one region for all layers)
   int64_t off_xa[kStepOps], off_adq, off_flag, off_out[kStepOps];
   unsigned spin_limit;
 };
@@ -98,21 +124,24 @@ __device__ __forceinline__ uint32_t step_tag(uint32_t E, int l, int j) { return 
 #ifndef BTL_STEP_TRACE_LAYER
 #define BTL_STEP_TRACE_LAYER 10
 #endif
-#define STEP_TRACE(l, ev)                         \
-  do {                                            \
+#define STEP_TRACE(l, ev)                              \
+  do {                                                 \
     if ((l) == BTL_STEP_TRACE_LAYER) BTL_TRACE_AT(ev); \
   } while (0)
-__device__ __forceinline__ char* layer_base(const StepArgs& p, int l) { return p.layers + (int64_t)l * p.layer_bytes; }
+
+__device__ __forceinline__ char* layer_base(const StepArgs& p, int l) { return p.layers + (int64_t)l * p.layer_stride; }
 __device__ __forceinline__ int8_t* tile_of(const StepArgs& p, int l, int j) {
   return reinterpret_cast<int8_t*>(layer_base(p, l) + p.off_xa[j]);
 }
 __device__ __forceinline__ float* adq_of(const StepArgs& p, int l, int j) {
   return reinterpret_cast<float*>(layer_base(p, l) + p.off_adq) + j * 32;
 }
-__device__ __forceinline__ uint32_t* flag_of(const StepArgs& p, int l, int j, int m) {
-  return reinterpret_cast<uint32_t*>(layer_base(p, l) + p.off_flag) + (j * 32 + m) * 32;  // own 128-byte line
+// Row m's flag of (l, j), on its own 128-byte line: tag << 32 | the row's
+// sum of its quantised values.
+__device__ __forceinline__ uint64_t* flag_of(const StepArgs& p, int l, int j, int m) {
+  return reinterpret_cast<uint64_t*>(layer_base(p, l) + p.off_flag) + (j * 32 + m) * 16;
 }
-// tagged output words of BitLinear j, row m (N_j / 2 words per row)
+// Tagged output words of BitLinear j: bf16 pairs [32][N_out / 2].
 __device__ __forceinline__ uint64_t* out_of(const StepArgs& p, int l, int j) {
   return reinterpret_cast<uint64_t*>(layer_base(p, l) + p.off_out[j]);
 }
@@ -146,9 +175,22 @@ __device__ __forceinline__ bool should_stop(const StepArgs& p, unsigned n, WaitS
 // ------------------------------------------------------------------ rows ----
 // Chunk c = tid + 512 i of a row holds its elements 8c .. 8c + 7.
 
-// Waits for the tagged words of row m of an output with `ncols` columns and
-// returns this thread's chunks as bf16 pairs (pr[i][0..3]).  Each thread polls
-// its own words and re-reads only the ones whose tag is not there yet.
+// Waits for the tagged bf16-pair words of row m of an output with `ncols`
+// columns and returns this thread's chunks as bf16 pairs (pr[i][0..3]).  Each
+// thread polls its own words and re-reads only the ones whose tag is not
+// there yet.
+// Sleep between two polls of a bounded wait (s_sleep units of 64 clocks).
+#ifndef BTL_STEP_POLL_SLEEP
+#define BTL_STEP_POLL_SLEEP 1
+#endif
+
+// Waits for the tagged bf16-pair words of row m of an output with `ncols`
+// columns and returns this thread's chunks as bf16 pairs (pr[i][0..3]).  Each
+// thread polls its own words and re-reads only the ones whose tag is not
+// there yet.  Every load of a round is issued before the first tag is
+// checked (a check between two loads would make each wait for the one
+// before); one round is in flight at a time (more polling traffic slows the
+// stores being waited for more than it speeds up their detection).
 template <int C>
 __device__ void wait_row_words(const StepArgs& p, const uint64_t* row, int ncols, uint32_t want, uint32_t (&pr)[C][4],
                                WaitState& ws) {
@@ -163,20 +205,24 @@ __device__ void wait_row_words(const StepArgs& p, const uint64_t* row, int ncols
   }
   unsigned n = 0;
   while (pending && !ws.dead) {
+    uint64_t d[C][4];
+    const unsigned pend = pending;
 #pragma unroll
     for (int i = 0; i < C; ++i)
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        if (pending & (1u << (4 * i + k))) {
-          const uint64_t d = ld_coherent(row + 4 * (tid + kActThreads * i) + k);
-          if ((uint32_t)(d >> 32) == want) {
-            pr[i][k] = (uint32_t)d;
-            pending &= ~(1u << (4 * i + k));
-          }
+        d[i][k] = (pend & (1u << (4 * i + k))) ? ld_coherent(row + 4 * (tid + kActThreads * i) + k) : 0;
+#pragma unroll
+    for (int i = 0; i < C; ++i)
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if ((pend & (1u << (4 * i + k))) && (uint32_t)(d[i][k] >> 32) == want) {
+          pr[i][k] = (uint32_t)d[i][k];
+          pending &= ~(1u << (4 * i + k));
         }
     if (!pending) break;
     if (should_stop(p, ++n, ws)) break;
-    __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_s_sleep(BTL_STEP_POLL_SLEEP);
   }
 }
 
@@ -205,23 +251,30 @@ __device__ __forceinline__ void pairs_to_floats(const uint32_t (&pr)[C][4], floa
     }
 }
 
+struct RowStats {
+  float adq;   // a/127
+  int32_t rs;  // sum of the row's quantised values
+};
+
 // RMSNorm with gain g, absmax int8 quantisation into the tile of (l, j), a/127,
-// then the row's flag (after the stores are acknowledged).  Rows m >= M
-// publish zeros.  The same row code as btl_bitlinear_fused.
+// then the row's flag (after the stores are acknowledged) carrying the row
+// sum.  Rows m >= M publish zeros.  The same row code as btl_bitlinear_fused.
 template <int C>
-__device__ void publish_row(const StepArgs& p, int l, int j, int m, int K, int KS, float (&v)[C][8],
-                            const uint4 (&g)[C], uint32_t want, float* s_sum, float* s_max) {
-  const int tid = threadIdx.x;
+__device__ RowStats publish_row(const StepArgs& p, int l, int j, int m, int K, int KS, float (&v)[C][8],
+                                const uint4 (&g)[C], uint32_t want, float* s_sum, float* s_max, int* s_rs) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nch = K >> 3, nchp = KS * 16;
   int8_t* xa = tile_of(p, l, j);
   float* adq = adq_of(p, l, j);
+  RowStats st{0.0f, 0};
+  int rs = 0;
   if (m < p.M) {
     const float r = row_rms_inv<C>(v, nch, K, p.eps, tid, s_sum);
     row_apply_norm<C>(v, g, true, r, nch, tid);
     const float a = row_absmax<C>(v, nch, 1e-5f, tid, s_max);
     const float scale = 127.0f / a;
-    if (tid == 0) st_coherent(adq + m, a / 127.0f);
-    int rs = 0;
+    st.adq = a / 127.0f;
+    if (tid == 0) st_coherent(adq + m, st.adq);
 #pragma unroll
     for (int i = 0; i < C; ++i) {
       const int c = tid + kActThreads * i;
@@ -236,63 +289,85 @@ __device__ void publish_row(const StepArgs& p, int l, int j, int m, int K, int K
     for (int c = tid; c < nchp; c += kActThreads) store8<true>(xa + xa_offset(m, 8 * c, KS), 0u, 0u);
     if (tid == 0) st_coherent(adq + m, 0.0f);
   }
+  rs += (int)xor_partner_u<32>((uint32_t)rs);
+  rs += (int)xor_partner_u<16>((uint32_t)rs);
+  rs += (int)xor_partner_u<8>((uint32_t)rs);
+  rs += (int)xor_partner_u<4>((uint32_t)rs);
+  rs += (int)xor_partner_u<2>((uint32_t)rs);
+  rs += (int)xor_partner_u<1>((uint32_t)rs);
+  if (lane == 0) s_rs[wv] = rs;
   wait_memory();
   __syncthreads();
-  if (tid == 0) st_coherent(flag_of(p, l, j, m), want);
+#pragma unroll
+  for (int w = 0; w < kActWaves; ++w) st.rs += s_rs[w];
+  if (tid == 0) st_coherent(flag_of(p, l, j, m), ((uint64_t)want << 32) | (uint32_t)st.rs);
+  return st;
 }
 
-// CH: chunks per thread of a row of H (and of the QKV output, NQKV <= 4096);
-// CF: of a row of F.
-template <int CH, int CF>
-__device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t E, float* s_sum, float* s_max) {
+// h = bf16(h + o) for this thread's chunk (one chunk per thread), o the
+// BitLinear's bf16 outputs as pairs: the residual epilogue of
+// btl_bitlinear_fused.
+__device__ __forceinline__ void residual_add(uint32_t (&hid)[4], const uint32_t (&o)[4], bool live) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t lo = f2bf(bf2f((uint16_t)(hid[k] & 0xffffu)) + bf2f((uint16_t)(o[k] & 0xffffu)));
+    const uint32_t hi = f2bf(bf2f((uint16_t)(hid[k] >> 16)) + bf2f((uint16_t)(o[k] >> 16)));
+    hid[k] = live ? (lo | (hi << 16)) : 0u;
+  }
+}
+
+// CF: chunks per thread of a row of F (a row of H, and of the QKV output,
+// is one chunk per thread: H, NQKV <= 4096).
+template <int CF>
+__device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t E, float* s_sum, float* s_max,
+                         int* s_rs) {
+  constexpr int CH = 1;
   const int tid = threadIdx.x;
   const bool live = m < p.M;
   const int nh = p.H >> 3, nf = p.F >> 3;
   WaitState ws{false};
   uint32_t hid[CH][4];
-#pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    const int c = tid + kActThreads * i;
+  {
     uint4 raw = make_uint4(0u, 0u, 0u, 0u);
-    if (live && c < nh) raw = *reinterpret_cast<const uint4*>(p.hidden + (int64_t)m * p.H + 8 * c);
-    hid[i][0] = raw.x;
-    hid[i][1] = raw.y;
-    hid[i][2] = raw.z;
-    hid[i][3] = raw.w;
+    if (live && tid < nh) raw = *reinterpret_cast<const uint4*>(p.hidden + (int64_t)m * p.H + 8 * tid);
+    hid[0][0] = raw.x;
+    hid[0][1] = raw.y;
+    hid[0][2] = raw.z;
+    hid[0][3] = raw.w;
   }
+  // gains of the next QKV stage: loaded ahead, during the wait before it
+  uint4 g_qkv[CH];
+  load_gain<CH>(sops[S_QKV].gamma, nh, g_qkv);
   for (int l = 0; l < p.L; ++l) {
     const StepOp* ops = sops + l * kStepOps;
     // ---- QKV: RMSNorm(h; input_layernorm)
     {
       float v[CH][8];
       uint4 g[CH];
-      load_gain<CH>(ops[S_QKV].gamma, nh, g);
+#pragma unroll
+      for (int i = 0; i < CH; ++i) g[i] = g_qkv[i];
       pairs_to_floats<CH>(hid, v);
       STEP_TRACE(l, 0);
-      publish_row<CH>(p, l, S_QKV, m, p.H, p.KSH, v, g, step_tag(E, l, S_QKV), s_sum, s_max);
+      publish_row<CH>(p, l, S_QKV, m, p.H, p.KSH, v, g, step_tag(E, l, S_QKV), s_sum, s_max, s_rs);
       STEP_TRACE(l, 1);
     }
     // ---- O: the user's QKV row, then RMSNorm(attn; attn_sub_norm)
     {
       uint4 g[CH];
       load_gain<CH>(ops[S_O].gamma, nh, g);
+      // the attention output row: an input of the step, loaded before the wait
+      uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+      if (live && tid < nh) raw = *reinterpret_cast<const uint4*>(p.attn + (int64_t)m * p.H + 8 * tid);
       uint32_t pr[CH][4];
-      if (live) wait_row_words<CH>(p, out_of(p, l, S_QKV) + (int64_t)m * (p.NQKV >> 1), p.NQKV, step_tag(E, l, S_QKV),
-                                   pr, ws);
+      wait_row_words<CH>(p, out_of(p, l, S_QKV) + (int64_t)m * (p.NQKV >> 1), p.NQKV, step_tag(E, l, S_QKV), pr, ws);
       STEP_TRACE(l, 2);
+      pr[0][0] = raw.x;
+      pr[0][1] = raw.y;
+      pr[0][2] = raw.z;
+      pr[0][3] = raw.w;
       float v[CH][8];
-#pragma unroll
-      for (int i = 0; i < CH; ++i) {
-        const int c = tid + kActThreads * i;
-        uint4 raw = make_uint4(0u, 0u, 0u, 0u);
-        if (live && c < nh) raw = *reinterpret_cast<const uint4*>(p.attn + (int64_t)m * p.H + 8 * c);
-        pr[i][0] = raw.x;
-        pr[i][1] = raw.y;
-        pr[i][2] = raw.z;
-        pr[i][3] = raw.w;
-      }
       pairs_to_floats<CH>(pr, v);
-      publish_row<CH>(p, l, S_O, m, p.H, p.KSH, v, g, step_tag(E, l, S_O), s_sum, s_max);
+      publish_row<CH>(p, l, S_O, m, p.H, p.KSH, v, g, step_tag(E, l, S_O), s_sum, s_max, s_rs);
       STEP_TRACE(l, 3);
     }
     // ---- GU: h = bf16(h + o); RMSNorm(h; post_attention_layernorm)
@@ -300,19 +375,12 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       uint4 g[CH];
       load_gain<CH>(ops[S_GU].gamma, nh, g);
       uint32_t pr[CH][4];
-      if (live) wait_row_words<CH>(p, out_of(p, l, S_O) + (int64_t)m * (p.H >> 1), p.H, step_tag(E, l, S_O), pr, ws);
+      wait_row_words<CH>(p, out_of(p, l, S_O) + (int64_t)m * (p.H >> 1), p.H, step_tag(E, l, S_O), pr, ws);
       STEP_TRACE(l, 4);
-#pragma unroll
-      for (int i = 0; i < CH; ++i)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint32_t lo = f2bf(bf2f((uint16_t)(hid[i][k] & 0xffffu)) + bf2f((uint16_t)(pr[i][k] & 0xffffu)));
-          const uint32_t hi = f2bf(bf2f((uint16_t)(hid[i][k] >> 16)) + bf2f((uint16_t)(pr[i][k] >> 16)));
-          hid[i][k] = live ? (lo | (hi << 16)) : 0u;
-        }
+      residual_add(hid[0], pr[0], live);
       float v[CH][8];
       pairs_to_floats<CH>(hid, v);
-      publish_row<CH>(p, l, S_GU, m, p.H, p.KSH, v, g, step_tag(E, l, S_GU), s_sum, s_max);
+      publish_row<CH>(p, l, S_GU, m, p.H, p.KSH, v, g, step_tag(E, l, S_GU), s_sum, s_max, s_rs);
       STEP_TRACE(l, 5);
     }
     // ---- DN: RMSNorm(relu(g)^2 * u; ffn_sub_norm)
@@ -320,114 +388,70 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       uint4 g[CF];
       load_gain<CF>(ops[S_DN].gamma, nf, g);
       uint32_t pr[CF][4];
-      if (live) {
-        wait_row_words<CF>(p, out_of(p, l, S_GU) + (int64_t)m * (p.F >> 1), p.F, step_tag(E, l, S_GU), pr, ws);
-        STEP_TRACE(l, 6);
-      } else {
-#pragma unroll
-        for (int i = 0; i < CF; ++i)
-#pragma unroll
-          for (int k = 0; k < 4; ++k) pr[i][k] = 0u;
-      }
+      wait_row_words<CF>(p, out_of(p, l, S_GU) + (int64_t)m * (p.F >> 1), p.F, step_tag(E, l, S_GU), pr, ws);
+      STEP_TRACE(l, 6);
       float v[CF][8];
       pairs_to_floats<CF>(pr, v);
-      publish_row<CF>(p, l, S_DN, m, p.F, p.KSF, v, g, step_tag(E, l, S_DN), s_sum, s_max);
+      publish_row<CF>(p, l, S_DN, m, p.F, p.KSF, v, g, step_tag(E, l, S_DN), s_sum, s_max, s_rs);
       STEP_TRACE(l, 7);
     }
     // ---- h = bf16(h + d)
     {
+      if (l + 1 < p.L) load_gain<CH>(sops[(l + 1) * kStepOps + S_QKV].gamma, nh, g_qkv);
       uint32_t pr[CH][4];
-      if (live) wait_row_words<CH>(p, out_of(p, l, S_DN) + (int64_t)m * (p.H >> 1), p.H, step_tag(E, l, S_DN), pr, ws);
-#pragma unroll
-      for (int i = 0; i < CH; ++i)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint32_t lo = f2bf(bf2f((uint16_t)(hid[i][k] & 0xffffu)) + bf2f((uint16_t)(pr[i][k] & 0xffffu)));
-          const uint32_t hi = f2bf(bf2f((uint16_t)(hid[i][k] >> 16)) + bf2f((uint16_t)(pr[i][k] >> 16)));
-          hid[i][k] = live ? (lo | (hi << 16)) : 0u;
-        }
+      wait_row_words<CH>(p, out_of(p, l, S_DN) + (int64_t)m * (p.H >> 1), p.H, step_tag(E, l, S_DN), pr, ws);
+      residual_add(hid[0], pr[0], live);
     }
   }
-  if (live) {
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int c = tid + kActThreads * i;
-      if (c < nh)
-        *reinterpret_cast<uint4*>(p.hidden + (int64_t)m * p.H + 8 * c) =
-            make_uint4(hid[i][0], hid[i][1], hid[i][2], hid[i][3]);
-    }
-  }
+  if (live && tid < nh)
+    *reinterpret_cast<uint4*>(p.hidden + (int64_t)m * p.H + 8 * tid) =
+        make_uint4(hid[0][0], hid[0][1], hid[0][2], hid[0][3]);
 }
 
 // ------------------------------------------------------------------ GEMM ----
-// Units.  QKV: 2 column tiles x one 16-row half; O, DN: 1 tile x half; GU: a
-// gate tile and its up tile x all 32 rows.  Unit u runs on GEMM workgroup u;
-// the two halves of a column group are 8 workgroups apart, so round-robin
-// dispatch puts them on one XCD and its L2 fetches their weights once.
-struct HalfUnit {
-  int g, h;
-};
-__device__ __forceinline__ HalfUnit half_unit(int u, int ngroups) {
-  const int g8 = ngroups & ~7;
-  HalfUnit r;
-  if (u < 2 * g8) {
-    r.g = ((u >> 4) << 3) | (u & 7);
-    r.h = (u >> 3) & 1;
-  } else {
-    const int i = u - 2 * g8, rem = ngroups - g8;
-    r.g = g8 + i % rem;
-    r.h = i / rem;
-  }
-  return r;
-}
-
-template <int J>
-struct OpShape;  // TPW: weight tiles per unit; HALF: 16-row unit
-template <>
-struct OpShape<S_QKV> {
-  static constexpr int TPW = 2, HALF = 1;
-};
-template <>
-struct OpShape<S_O> {
-  static constexpr int TPW = 1, HALF = 1;
-};
-template <>
-struct OpShape<S_GU> {
-  static constexpr int TPW = 2, HALF = 0;
-};
-template <>
-struct OpShape<S_DN> {
-  static constexpr int TPW = 1, HALF = 1;
-};
-
 __device__ __forceinline__ int op_n(const StepArgs& p, int j) {  // output columns of the GEMM
   return j == S_QKV ? p.NQKV : j == S_GU ? 2 * p.F : p.H;
 }
 __device__ __forceinline__ int op_ks(const StepArgs& p, int j) { return j == S_DN ? p.KSF : p.KSH; }
-__device__ __forceinline__ int op_units(const StepArgs& p, int j) {
-  const int NT = op_n(p, j) / 32;
-  return j == S_GU ? NT / 2 : j == S_QKV ? NT : 2 * NT;  // QKV: NT/2 groups x 2 halves
-}
-
-// Tile t of unit u of BitLinear J (and the unit's half).
 template <int J>
-__device__ __forceinline__ int unit_tile(const StepArgs& p, int u, int t, int& h) {
+__device__ __forceinline__ int op_units(const StepArgs& p) {
   const int NT = op_n(p, J) / 32;
-  if (J == S_GU) {
-    h = 0;
-    return t == 0 ? u : u + NT / 2;
-  }
-  const HalfUnit hu = half_unit(u, NT / OpShape<J>::TPW);
-  h = hu.h;
-  return hu.g * OpShape<J>::TPW + t;
+  return J == S_GU ? NT / 2 : OpShape<J>::HALF ? 2 * NT : NT;
 }
 
-// This wave's superblock range of K: waves w and w + 4 share a SIMD, so the
-// first KS % 8 waves take one superblock more (0-3 before 4-7) and every
-// SIMD gets the same share.
-__device__ __forceinline__ void wave_ks(int KS, int wv, int& wb, int& we) {
-  const int base = KS / kStepWaves, rem = KS % kStepWaves;
-  wb = wv * base + (wv < rem ? wv : rem);
+// Unit u of BitLinear J: its first tile (GU: the gate tile; the up tile is
+// F/32 further) and, for 16-row units, its row half h.  The two halves of a
+// tile are 8 workgroups apart, so round-robin dispatch puts them on one XCD
+// and its L2 fetches their weights once.
+template <int J>
+__device__ __forceinline__ void unit_of(const StepArgs& p, int u, int& tile0, int& h) {
+  const int NT = op_n(p, J) / 32;
+  h = 0;
+  if (!OpShape<J>::HALF) {
+    tile0 = u;
+    return;
+  }
+  const int g8 = NT & ~7;
+  if (u < 2 * g8) {
+    tile0 = ((u >> 4) << 3) | (u & 7);
+    h = (u >> 3) & 1;
+  } else {
+    const int i = u - 2 * g8, rem = NT - g8;
+    tile0 = g8 + i % rem;
+    h = i / rem;
+  }
+}
+template <int J>
+__device__ __forceinline__ int unit_tile(const StepArgs& p, int tile0, int t) {
+  return t == 0 ? tile0 : tile0 + op_n(p, J) / 64;  // GU: up tile F/32 after the gate tile
+}
+
+// This wave's superblocks of [sb0, sb1): waves w and w + 4 share a SIMD, so
+// the first (n % 8) waves take one more (0-3 before 4-7) and every SIMD gets
+// the same share.
+__device__ __forceinline__ void wave_ks(int sb0, int sb1, int wv, int& wb, int& we) {
+  const int n = sb1 - sb0, base = n / kStepWaves, rem = n % kStepWaves;
+  wb = sb0 + wv * base + (wv < rem ? wv : rem);
   we = wb + base + (wv < rem ? 1 : 0);
 }
 
@@ -438,16 +462,16 @@ __device__ __forceinline__ void load_unit_weights(const StepArgs& p, const StepO
                                                   v4i (&w)[kStepWSlots]) {
   static_assert(OpShape<J>::TPW * NSW <= kStepWSlots, "weight slots");
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (u >= op_units(p, J)) return;
+  if (u >= op_units<J>(p)) return;
   const int KS = op_ks(p, J);
-  int wb, we;
-  wave_ks(KS, wv, wb, we);
+  int tile0, h, wb, we;
+  unit_of<J>(p, u, tile0, h);
+  wave_ks(0, KS, wv, wb, we);
   if (wb >= we) return;
   const uint32_t* wdev = sops[l * kStepOps + J].wdev;
 #pragma unroll
   for (int t = 0; t < OpShape<J>::TPW; ++t) {
-    int h;
-    const int tile = unit_tile<J>(p, u, t, h);
+    const int tile = unit_tile<J>(p, tile0, t);
 #pragma unroll
     for (int i = 0; i < NSW; ++i) {
       const int sb = wb + i < we ? wb + i : we - 1;
@@ -456,55 +480,59 @@ __device__ __forceinline__ void load_unit_weights(const StepArgs& p, const StepO
   }
 }
 
-// Poll wave: wait for the flags of rows [r0, r0 + n) of (l, j).
-__device__ void wait_flags(const StepArgs& p, int l, int j, int r0, int n, uint32_t want, WaitState& ws) {
+// Poll wave: wait for the flags of rows [r0, r0 + n) of (l, j); the row sums
+// they carry go to s_rsum[0 .. n).
+__device__ void wait_flags(const StepArgs& p, int l, int j, int r0, int n, uint32_t want, int* s_rsum, WaitState& ws) {
   const int lane = threadIdx.x & 63;
   unsigned k = 0;
+  uint64_t f = 0;
   while (!ws.dead) {
-    const bool ok = lane >= n || ld_coherent(flag_of(p, l, j, r0 + lane)) == want;
+    if (lane < n) f = ld_coherent(flag_of(p, l, j, r0 + lane));
+    const bool ok = lane >= n || (uint32_t)(f >> 32) == want;
     if (__all(ok)) break;
     if (should_stop(p, ++k, ws)) break;
-    __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_s_sleep(BTL_STEP_POLL_SLEEP);
   }
+  if (lane < n) s_rsum[lane] = (int32_t)(uint32_t)f;
 }
 
 // One BitLinear J of layer l on GEMM workgroup gi: wait for the operand
-// tile's rows, MFMA against the weights held in w, prefetch the next
-// BitLinear's weights into wn, reduce the waves in LDS, epilogue.
+// tile's rows, MFMA against the weights held in w, reduce the waves in LDS,
+// epilogue (tagged bf16 pairs), then issue the next BitLinear's weights into wn.
 template <int J, int NSW, int NJ, int NNSW>
 __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int gi, uint32_t E,
                              const v4i (&w)[kStepWSlots], v4i (&wn)[kStepWSlots], int nl, int32_t* lds,
                              WaitState& ws) {
-  constexpr int TPW = OpShape<J>::TPW;
+  constexpr int TPW = OpShape<J>::TPW, MODE = OpShape<J>::MODE;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int units = op_units(p, J);
-  if (gi >= units) {
+  if (gi >= op_units<J>(p)) {
     if (nl < p.L) load_unit_weights<NJ, NNSW>(p, sops, nl, gi, wn);
     return;
   }
-  const int KS = op_ks(p, J);
   const StepOp& op = sops[l * kStepOps + J];
-  int tile[TPW];
-  int h = 0;
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) tile[t] = unit_tile<J>(p, gi, t, h);
+  int tile0, h, wb, we;
+  unit_of<J>(p, gi, tile0, h);
+  wave_ks(0, op_ks(p, J), wv, wb, we);
+  const int cnt = we - wb;
   const uint32_t want = step_tag(E, l, J);
-  if (wv == kStepPollWave) {
-    if (OpShape<J>::HALF)
-      wait_flags(p, l, J, 16 * h, 16, want, ws);
-    else
-      wait_flags(p, l, J, 0, 32, want, ws);
-  }
+  int32_t* red = lds;                                // reductions
+  int32_t* s_rsum = lds + kStepWaves * 2 * 16 * 64;  // [32] row sums from the flags
+  constexpr int NR = OpShape<J>::HALF ? 16 : 32;     // rows of the unit
+  if (wv == kStepPollWave) wait_flags(p, l, J, 16 * h, NR, want, s_rsum, ws);
   lds_barrier();  // the operand rows are out (no wait for loads in flight)
   STEP_TRACE(l, 8 + 2 * J);
   const int8_t* xa = tile_of(p, l, J);
   const float* adq = adq_of(p, l, J);
-  int wb, we;
-  wave_ks(KS, wv, wb, we);
-  const int cnt = we - wb;
+  uint64_t* outw = out_of(p, l, J);
+  const int n_out = J == S_QKV ? p.NQKV : J == S_GU ? p.F : p.H;
 
   if constexpr (OpShape<J>::HALF) {
-    // ---- 16-row half on v_mfma_i32_16x16x64_i8 (see gemm_decode_half) ----
+    // ---- rows 16h .. 16h + 15 on v_mfma_i32_16x16x64_i8, two MFMAs (columns
+    // 0-15, 16-31) per 64 k.  A: lane l takes row 16h + (l & 15), k-group l >> 4
+    // of the 64-k step straight from the tile (32-k step 2p + (G >> 1), half
+    // G & 1).  B: a 32-lane and then a 16-lane swap of the packed words of
+    // steps 2p and 2p + 1 give lane l column (l & 15) (+16) with its k-group.
+    // C: lane l, element j is row 4 (l >> 4) + j, column l & 15.
     const int er = tid >> 5, ec = tid & 31;
     const int row = 16 * h + er;
     const float ad = ld_coherent(adq + row);
@@ -512,178 +540,136 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     const int a_step = lane >> 5;
     v4i a[NSW][2];
 #pragma unroll
-    for (int i = 0; i < NSW; ++i) {
+    for (int i = 0; i < NSW; ++i)
       if (i < cnt)
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) a[i][pp] = ld128(xa + (((wb + i) * 4 + 2 * pp + a_step) * 64 + a_lane) * 16);
-    }
-    v4i acc[TPW][2];
+    v4i acc[2] = {(v4i){0, 0, 0, 0}, (v4i){0, 0, 0, 0}};
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) acc[t][0] = acc[t][1] = (v4i){0, 0, 0, 0};
-    int32_t rs_lane = 0;  // sum of this lane's operand bytes: row 16h + (lane & 15), k-group lane >> 4
-#pragma unroll
-    for (int i = 0; i < NSW; ++i) {
-      if (i < cnt) {
-#pragma unroll
-        for (int pp = 0; pp < 2; ++pp) {
-#pragma unroll
-          for (int t = 0; t < TPW; ++t) {
-            const auto s32 = __builtin_amdgcn_permlane32_swap((uint32_t)w[t * NSW + i][2 * pp],
-                                                              (uint32_t)w[t * NSW + i][2 * pp + 1], false, false);
-            const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
-            acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[0]), acc[t][0], 0, 0, 0);
-            acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[1]), acc[t][1], 0, 0, 0);
-          }
-          rs_lane = bytes_sum(a[i][pp], rs_lane);
-        }
-      }
-    }
-    // LDS: red[8][TPW][8][64], red_rs[8][16]
-    int32_t* red = lds;
-    int32_t* red_rs = lds + kStepWaves * TPW * 8 * 64;
-    rs_lane += (int32_t)xor_partner_u<16>((uint32_t)rs_lane);  // the four k-groups of a row
-    rs_lane += (int32_t)xor_partner_u<32>((uint32_t)rs_lane);
-    if (lane < 16) red_rs[wv * 16 + lane] = rs_lane;
-#pragma unroll
-    for (int t = 0; t < TPW; ++t)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        red[((wv * TPW + t) * 8 + q) * 64 + lane] = acc[t][0][q];
-        red[((wv * TPW + t) * 8 + 4 + q) * 64 + lane] = acc[t][1][q];
-      }
-    lds_barrier();
-    const int reg = 4 * (ec >> 4) + (er & 3), src = 16 * (er >> 2) + (ec & 15);
-    int32_t rs = 0;
-#pragma unroll
-    for (int v2 = 0; v2 < kStepWaves; ++v2) rs += red_rs[v2 * 16 + er];
-    int32_t vsum[TPW];
-#pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-      int32_t sum = -rs;
-#pragma unroll
-      for (int v2 = 0; v2 < kStepWaves; ++v2) sum += red[((v2 * TPW + t) * 8 + reg) * 64 + src];
-      vsum[t] = sum;
-    }
-    lds_barrier();  // LDS free for the next BitLinear
-    uint64_t* outw = out_of(p, l, J);
-    const int n_row = op_n(p, J);
-#pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-      const int n = tile[t] * 32 + ec;
-      const uint32_t o = f2bf((float)vsum[t] * (op_seg_scale(op, n) * ad));
-      const uint32_t pair = o | ((uint32_t)__shfl_down((int)o, 1, 64) << 16);  // lanes ec, ec+1 share the row
-      if (row < p.M) {
-        if ((ec & 1) == 0) st_coherent(outw + (int64_t)row * (n_row >> 1) + (n >> 1), ((uint64_t)want << 32) | pair);
-        if (J == S_QKV) p.qkv_out[(int64_t)row * p.NQKV + n] = (uint16_t)o;
-      }
-    }
-    STEP_TRACE(l, 9 + 2 * J);
-    // The next BitLinear's weights, issued after this one's last wait: its
-    // hand-off takes longer than the loads, and no wait here covers them.
-    if (nl < p.L) load_unit_weights<NJ, NNSW>(p, sops, nl, gi, wn);
-  } else {
-    // ---- gate tile and up tile, all 32 rows, v_mfma_i32_32x32x32_i8 ----
-    float ad_r[2];
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr) ad_r[rr] = ld_coherent(adq + acc_row(wv + kStepWaves * rr, lane));
-    v4i a[NSW][4];
-#pragma unroll
-    for (int i = 0; i < NSW; ++i) {
+    for (int i = 0; i < NSW; ++i)
       if (i < cnt)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) a[i][q] = ld128(xa + (((wb + i) * 4 + q) * 64 + lane) * 16);
-    }
-    v16i acc[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) acc[t] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    int32_t rs_lane = 0;
-#pragma unroll
-    for (int i = 0; i < NSW; ++i) {
-      if (i < cnt) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-            acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][q], unpack_b((uint32_t)w[t * NSW + i][q]), acc[t], 0,
-                                                           0, 0);
-          rs_lane = bytes_sum(a[i][q], rs_lane);
+        for (int pp = 0; pp < 2; ++pp) {
+          const auto s32 = __builtin_amdgcn_permlane32_swap((uint32_t)w[i][2 * pp], (uint32_t)w[i][2 * pp + 1],
+                                                            false, false);
+          const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
+          acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[0]), acc[0], 0, 0, 0);
+          acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[1]), acc[1], 0, 0, 0);
         }
-      }
-    }
-    // LDS: red[8][2][16][64], red_rs[8][32]
-    int32_t* red = lds;
-    int32_t* red_rs = lds + kStepWaves * 2 * 16 * 64;
-    {
-      const int32_t rs_row = rs_lane + (int32_t)xor_partner_u<32>((uint32_t)rs_lane);
-      if (lane < 32) red_rs[wv * 32 + lane] = rs_row;
-    }
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) red[((wv * 2 + t) * 16 + r) * 64 + lane] = acc[t][r];
-    lds_barrier();
-    const int jc = lane & 31;
-    int32_t vg[2], vu[2];
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      const int r = wv + kStepWaves * rr;
-      const int i = acc_row(r, lane);
-      int32_t rs = 0;
-#pragma unroll
-      for (int v2 = 0; v2 < kStepWaves; ++v2) rs += red_rs[v2 * 32 + i];
-      int32_t sg = -rs, su = -rs;
-#pragma unroll
-      for (int v2 = 0; v2 < kStepWaves; ++v2) {
-        sg += red[((v2 * 2 + 0) * 16 + r) * 64 + lane];
-        su += red[((v2 * 2 + 1) * 16 + r) * 64 + lane];
-      }
-      vg[rr] = sg;
-      vu[rr] = su;
+    for (int q = 0; q < 4; ++q) {
+      red[(wv * 8 + q) * 64 + lane] = acc[0][q];
+      red[(wv * 8 + 4 + q) * 64 + lane] = acc[1][q];
     }
     lds_barrier();
-    uint64_t* outw = out_of(p, l, J);
+    const int reg = 4 * (ec >> 4) + (er & 3), src = 16 * (er >> 2) + (ec & 15);
+    int32_t sum = -s_rsum[er];
+#pragma unroll
+    for (int v2 = 0; v2 < kStepWaves; ++v2) sum += red[(v2 * 8 + reg) * 64 + src];
+    lds_barrier();  // LDS free for the next BitLinear
+    const int n = tile0 * 32 + ec;
+    const uint32_t o = f2bf((float)sum * (op_seg_scale(op, n) * ad));
+    const uint32_t pair = o | ((uint32_t)__shfl_down((int)o, 1, 64) << 16);  // lanes ec, ec+1 share the row
+    if ((ec & 1) == 0) st_coherent(outw + (int64_t)row * (n_out >> 1) + (n >> 1), ((uint64_t)want << 32) | pair);
+  } else {
+    // ---- all 32 rows on v_mfma_i32_32x32x32_i8 ----
+    float ad_r[2];
+    int32_t rs_r[2];
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
       const int i = acc_row(wv + kStepWaves * rr, lane);
-      const int ng = tile[0] * 32 + jc, nu = tile[1] * 32 + jc;
-      const float gg = bf2f(f2bf((float)vg[rr] * (op_seg_scale(op, ng) * ad_r[rr])));
-      const float uu = bf2f(f2bf((float)vu[rr] * (op_seg_scale(op, nu) * ad_r[rr])));
-      const float gr = gg > 0.0f ? gg : 0.0f;
-      const float sq = bf2f(f2bf(gr * gr));
-      const uint32_t hv = f2bf(sq * uu);
-      const uint32_t pair = hv | ((uint32_t)__shfl_down((int)hv, 1, 64) << 16);
-      if (i < p.M) {
-        if ((jc & 1) == 0) st_coherent(outw + (int64_t)i * (p.F >> 1) + (ng >> 1), ((uint64_t)want << 32) | pair);
-        p.ffn_h[(int64_t)i * p.F + ng] = (uint16_t)hv;
+      ad_r[rr] = ld_coherent(adq + i);
+      rs_r[rr] = s_rsum[i];
+    }
+    v4i a[NSW][4];
+#pragma unroll
+    for (int i = 0; i < NSW; ++i)
+      if (i < cnt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[i][q] = ld128(xa + (((wb + i) * 4 + q) * 64 + lane) * 16);
+    v16i acc[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) acc[t] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < NSW; ++i)
+      if (i < cnt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int t = 0; t < TPW; ++t)
+            acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][q], unpack_b((uint32_t)w[t * NSW + i][q]), acc[t], 0,
+                                                           0, 0);
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[((wv * TPW + t) * 16 + r) * 64 + lane] = acc[t][r];
+    lds_barrier();
+    // thread (wv, lane) finishes rows acc_row(wv + 8 rr, lane), column lane & 31, of every tile
+    int32_t v[TPW][2];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int r = wv + kStepWaves * rr;
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        int32_t sum = -rs_r[rr];
+#pragma unroll
+        for (int v2 = 0; v2 < kStepWaves; ++v2) sum += red[((v2 * TPW + t) * 16 + r) * 64 + lane];
+        v[t][rr] = sum;
       }
     }
-    STEP_TRACE(l, 9 + 2 * J);
-    if (nl < p.L) load_unit_weights<NJ, NNSW>(p, sops, nl, gi, wn);
+    lds_barrier();  // LDS free for the next BitLinear
+    const int jc = lane & 31;
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int i = acc_row(wv + kStepWaves * rr, lane);
+      const int n = tile0 * 32 + jc;
+      uint32_t o;
+      if (MODE == MODE_SCALE) {
+        o = f2bf((float)v[0][rr] * (op_seg_scale(op, n) * ad_r[rr]));
+      } else {
+        const int nu = unit_tile<J>(p, tile0, 1) * 32 + jc;
+        const float gg = bf2f(f2bf((float)v[0][rr] * (op_seg_scale(op, n) * ad_r[rr])));
+        const float uu = bf2f(f2bf((float)v[TPW - 1][rr] * (op_seg_scale(op, nu) * ad_r[rr])));
+        const float gr = gg > 0.0f ? gg : 0.0f;
+        const float sq = bf2f(f2bf(gr * gr));
+        o = f2bf(sq * uu);
+      }
+      const uint32_t pair = o | ((uint32_t)__shfl_down((int)o, 1, 64) << 16);  // lanes jc, jc+1 share the row
+      if ((jc & 1) == 0) st_coherent(outw + (int64_t)i * (n_out >> 1) + (n >> 1), ((uint64_t)want << 32) | pair);
+      if (J == S_QKV && i < p.M) p.qkv_out[(int64_t)i * p.NQKV + n] = (uint16_t)o;
+      if (J == S_GU && i < p.M) p.ffn_h[(int64_t)i * p.F + n] = (uint16_t)o;
+    }
   }
+  STEP_TRACE(l, 9 + 2 * J);
+  // The next BitLinear's weights, issued after this one's last wait: its
+  // hand-off takes longer than the loads, and no wait here covers them.
+  if (nl < p.L) load_unit_weights<NJ, NNSW>(p, sops, nl, gi, wn);
 }
 
-template <int NSWH, int NSWF>
+// NQ: superblocks per wave of a unit of QKV, O and GU (K = H); NDN: of DN (K = F).
+template <int NQ, int NDN>
 __device__ void step_gemm(const StepArgs& p, const StepOp* sops, int gi, uint32_t E, int32_t* lds) {
   WaitState ws{false};
   v4i wa[kStepWSlots], wb[kStepWSlots];
-  load_unit_weights<S_QKV, NSWH>(p, sops, 0, gi, wa);
+  load_unit_weights<S_QKV, NQ>(p, sops, 0, gi, wa);
   for (int l = 0; l < p.L; ++l) {
-    step_gemm_op<S_QKV, NSWH, S_O, NSWH>(p, sops, l, gi, E, wa, wb, l, lds, ws);
-    step_gemm_op<S_O, NSWH, S_GU, NSWH>(p, sops, l, gi, E, wb, wa, l, lds, ws);
-    step_gemm_op<S_GU, NSWH, S_DN, NSWF>(p, sops, l, gi, E, wa, wb, l, lds, ws);
-    step_gemm_op<S_DN, NSWF, S_QKV, NSWH>(p, sops, l, gi, E, wb, wa, l + 1, lds, ws);
+    step_gemm_op<S_QKV, NQ, S_O, NQ>(p, sops, l, gi, E, wa, wb, l, lds, ws);
+    step_gemm_op<S_O, NQ, S_GU, NQ>(p, sops, l, gi, E, wb, wa, l, lds, ws);
+    step_gemm_op<S_GU, NQ, S_DN, NDN>(p, sops, l, gi, E, wa, wb, l, lds, ws);
+    step_gemm_op<S_DN, NDN, S_QKV, NQ>(p, sops, l, gi, E, wb, wa, l + 1, lds, ws);
   }
 }
 
-template <int CH, int CF, int NSWH, int NSWF>
+template <int CF, int NQ, int NDN>
 __global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
-  // GEMM reductions need max(8*2*8*64 + 8*16, 8*2*16*64 + 8*32) int32 (64.5 KiB); rows use the first 64
-  // bytes.  96 KiB: more than half of a CU's LDS, so no CU ever holds two workgroups of the launch.
-  // The op table (up to 16 KiB) is copied into LDS above the reduction area, so reading a weight
-  // address or a scale is an LDS read, never a vector memory load waited for with the weight stream.
+  // GEMM: reductions [8][2][16][64] int32 + 32 row sums; rows: 24 words.  The op table
+  // (up to 16 KiB) is copied into LDS above them, so reading a weight address or a
+  // scale is an LDS read, never a vector memory load waited for with the weight
+  // stream.  96 KiB in all: more than half of a CU's LDS, so no CU ever holds two
+  // workgroups of the launch.
   __shared__ __attribute__((aligned(16))) int32_t lds[24576];
   constexpr int kTableInts = kStepMaxLayers * kStepOps * (int)sizeof(StepOp) / 4;
-  static_assert(kStepWaves * 2 * 16 * 64 + kStepWaves * 32 + kTableInts <= 24576, "LDS layout");
+  static_assert(kStepWaves * 2 * 16 * 64 + 32 + kTableInts <= 24576, "LDS layout");
   StepOp* sops = reinterpret_cast<StepOp*>(lds + (24576 - kTableInts));
   {
     const uint4* src = reinterpret_cast<const uint4*>(p.ops);
@@ -695,9 +681,10 @@ __global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
   const int b = blockIdx.x;
   const uint32_t E = p.epoch[b] + 1u;  // this launch (written by the previous launch of the step)
   if (b < kStepRows) {
-    step_row<CH, CF>(p, sops, b, E, reinterpret_cast<float*>(lds), reinterpret_cast<float*>(lds) + kActWaves);
+    float* f = reinterpret_cast<float*>(lds);
+    step_row<CF>(p, sops, b, E, f, f + kActWaves, reinterpret_cast<int*>(lds) + 2 * kActWaves);
   } else {
-    step_gemm<NSWH, NSWF>(p, sops, b - kStepRows, E, lds);
+    step_gemm<NQ, NDN>(p, sops, b - kStepRows, E, lds);
   }
   if (threadIdx.x == 0) p.epoch[b] = E;
 }
@@ -710,7 +697,8 @@ struct StepSizes {
 static StepSizes step_sizes(int64_t H, int64_t F, int64_t NQKV, int64_t L) {
   StepSizes z;
   const int64_t Ks[kStepOps] = {H, H, H, F};
-  const int64_t Nout[kStepOps] = {NQKV, H, F, H};  // bf16 columns a row workgroup reads back
+  // tagged words (bf16 pairs) a row workgroup reads back
+  const int64_t words[kStepOps] = {NQKV / 2, H / 2, F / 2, H / 2};
   int64_t off = 0;
   for (int j = 0; j < kStepOps; ++j) {
     z.off_xa[j] = off;
@@ -722,7 +710,7 @@ static StepSizes step_sizes(int64_t H, int64_t F, int64_t NQKV, int64_t L) {
   off += kStepOps * 32 * 128;
   for (int j = 0; j < kStepOps; ++j) {
     z.off_out[j] = off;
-    off += round_up(32 * (Nout[j] / 2) * 8, 4096);
+    off += round_up(32 * words[j] * 8, 4096);
   }
   z.layer_bytes = round_up(off, 65536);
   z.total = kStHeader + z.layer_bytes * L;
@@ -746,13 +734,13 @@ static int step_check_shape(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64
   if (H > 4096 || NQKV > 4096 || F > 8192)
     return set_error(BTL_ERR_SHAPE, "btl_decode_step: H=%lld NQKV=%lld (<= 4096), F=%lld (<= 8192) exceed the kernel's "
                      "row registers", (long long)H, (long long)NQKV, (long long)F);
-  // weights per wave: ceil(KS/8) superblocks per tile within the register slots
-  const int64_t nswh = (ksb(H) + kStepWaves - 1) / kStepWaves, nswf = (ksb(F) + kStepWaves - 1) / kStepWaves;
-  if (nswh > 3 || nswf > 7)
+  // weights per wave within the register slots: ceil(KS / 8) superblocks per tile, <= 3 for K = H
+  // (two tiles for gate||up), <= 7 for K = F
+  if ((ksb(H) + 7) / 8 > 3 || (ksb(F) + 7) / 8 > 7)
     return set_error(BTL_ERR_SHAPE, "btl_decode_step: H=%lld or F=%lld too large for the weight registers",
                      (long long)H, (long long)F);
   const int grid = step_grid();
-  const int64_t units = std::max({NQKV / 32, 2 * (H / 32), F / 32});
+  const int64_t units = std::max({NQKV / 32, 2 * (H / 32), F / 32});  // QKV and O, DN (two row halves), GU
   if (grid <= kStepRows || grid > kStepMaxGrid || units > grid - kStepRows)
     return set_error(BTL_ERR_SHAPE, "btl_decode_step: %lld GEMM units do not fit %d workgroups", (long long)units,
                      grid - kStepRows);
@@ -860,7 +848,7 @@ int btl_decode_step(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, fl
   a.epoch = reinterpret_cast<uint32_t*>(ws + kStEpoch);
   a.error = reinterpret_cast<uint32_t*>(ws + kStError);
   a.layers = ws + kStHeader;
-  a.layer_bytes = z.layer_bytes;
+  a.layer_stride = getenv("BTL_STEP_LAYER_REGIONS") ? z.layer_bytes : 0;
   for (int j = 0; j < kStepOps; ++j) {
     a.off_xa[j] = z.off_xa[j];
     a.off_out[j] = z.off_out[j];
@@ -869,12 +857,12 @@ int btl_decode_step(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, fl
   a.off_flag = z.off_flag;
   a.spin_limit = 1u << 18;
   const int grid = step_grid();
-  const int ch = act_cpt(H), cf = act_cpt(F);
+  const int cf = act_cpt(F);
   hipStream_t s = (hipStream_t)stream;
-  if (ch == 1 && cf == 1)
-    hipLaunchKernelGGL((k_decode_step<1, 1, 3, 7>), dim3(grid), dim3(512), 0, s, a);
-  else if (ch == 1 && cf == 2)
-    hipLaunchKernelGGL((k_decode_step<1, 2, 3, 7>), dim3(grid), dim3(512), 0, s, a);
+  if (cf == 1)
+    hipLaunchKernelGGL((k_decode_step<1, 3, 7>), dim3(grid), dim3(512), 0, s, a);
+  else if (cf == 2)
+    hipLaunchKernelGGL((k_decode_step<2, 3, 7>), dim3(grid), dim3(512), 0, s, a);
   else
     return set_error(BTL_ERR_SHAPE, "btl_decode_step: no kernel instance for H=%lld F=%lld", (long long)H, (long long)F);
   return check_launch("decode step");
