@@ -4,16 +4,19 @@ A step is the 30-layer chain of the model's BitLinear launches at M = 32
 tokens: per layer the fused RMSNorm->QKV (2560->3840), o_proj (2560->2560,
 attn_sub_norm prologue, residual epilogue), gate||up (2560->2x6912,
 post-attention RMSNorm prologue, relu^2*up epilogue) and down (6912->2560,
-ffn_sub_norm prologue, residual epilogue).  Weights are random-init ternary
+ffn_sub_norm prologue, residual epilogue), all 120 of them in one persistent
+kernel launch (btl_decode_step).  Weights are random-init ternary
 (latents ~N(0, 0.02), absmean-quantised on the device), RMSNorm gains ~N(1,
 0.1), activations ~N(0, 1): synthetic, seeded.  The attention core between
 QKV and o_proj is not part of the BitLinear path; o_proj reads a seeded
-stand-in buffer.  The step is captured once in a HIP graph and replayed.
+stand-in buffer.  The step is captured once in a HIP graph and replayed.  The
+same step as 120 per-BitLinear launches and as 31 per-layer launches is timed
+beside it, and the three structures are checked to give the same bits.
 
 Printed JSON (one line): value = algorithmic HBM bytes of a step / step time
 (GB/s), ms_per_step = BitLinear ms per decode step, plus the roofline of the
-dominant kernel (the BitLinear kind with the longest launch) measured with HIP
-events on the launch stream, the prefill MFMA-i8 utilisation, and the CPU
+step kernel measured with HIP events on the launch stream, each BitLinear
+kind's single-launch kernel time, the prefill MFMA-i8 utilisation, and the CPU
 reference CPU path (numpy absmax quantisation + torch fp32 GEMM of the same
 step) timed on the host as a reported baseline.  ``--pmc-pass`` runs only
 the workload of the rocprofv3 --pmc traffic measurement.
@@ -167,7 +170,8 @@ def kernel_event_timing(step, torch, reps):
 def pmc_pass(step, torch):
     """Workload for the rocprofv3 --pmc traffic runs: a plain 256 MiB device
     copy (the counter calibration: it reads and writes exactly 256 MiB), then
-    two eager passes of each BitLinear kind over all layers."""
+    two eager passes of each BitLinear kind over all layers, then three
+    persistent steps (one k_decode_step launch each)."""
     dev = step.device
     a = torch.empty(128 << 20, dtype=torch.int16, device=dev).fill_(1)
     b = torch.empty_like(a)
@@ -183,22 +187,30 @@ def pmc_pass(step, torch):
                 launch(i)
         torch.cuda.synchronize()
         log(f"[bench] pmc pass: {kind} done")
+    for _ in range(3):
+        step.reset_hidden()
+        step.step_persistent()
+    step.check()
+    log("[bench] pmc pass: persistent step done")
 
 
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "bitlinear_decode_b32_traffic.md")
+TRAFFIC_FILES = [os.path.join(REPO, "profiles", f) for f in
+                 ("decode_step_b32_traffic.md", "bitlinear_decode_b32_traffic.md")]
 
 
 def committed_traffic(kind):
-    """HBM bytes per launch of a kind from the committed rocprofv3 --pmc
-    summary (lines 'traffic_bytes_per_launch <kind> <bytes>'), or None."""
-    try:
-        with open(TRAFFIC_FILE) as f:
-            for line in f:
-                parts = line.strip().strip("`").split()
-                if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kind:
-                    return int(parts[2])
-    except OSError:
-        return None
+    """HBM bytes per launch of a kind ("step" for the persistent step kernel)
+    from the committed rocprofv3 --pmc summaries (lines
+    'traffic_bytes_per_launch <kind> <bytes>'), or None."""
+    for path in TRAFFIC_FILES:
+        try:
+            with open(path) as f:
+                for line in f:
+                    parts = line.strip().strip("`").split()
+                    if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kind:
+                        return int(parts[2])
+        except OSError:
+            continue
     return None
 
 
@@ -577,57 +589,77 @@ def main():
         pmc_pass(step, torch)
         return
 
-    # warm-up (eager), then capture the step on a side stream
     s = torch.cuda.Stream(device=dev)
     s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        for _ in range(max(args.warmup, 1)):
-            step.reset_hidden()
-            step.step()
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=s):
-        step.step()
-    with torch.cuda.stream(s):
-        for _ in range(args.warmup):
-            graph.replay()
-    torch.cuda.synchronize()
-    log("[bench] graph captured; timing")
 
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    with torch.cuda.stream(s):
-        for _ in range(args.steps):
-            graph.replay()
-    torch.cuda.synchronize()
-    t_el = time.perf_counter() - t_start
+    def capture(fn):
+        """Eager warm-up calls of fn on stream s (workspaces are prepared
+        outside the capture), then fn captured into a graph on s."""
+        with torch.cuda.stream(s):
+            for _ in range(max(args.warmup, 1)):
+                step.reset_hidden()
+                fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            fn()
+        with torch.cuda.stream(s):
+            for _ in range(args.warmup):
+                g.replay()
+        torch.cuda.synchronize()
+        return g
+
+    def timed(g, n):
+        """Wall-clock us per replay of n replays, and the same span from two
+        HIP events recorded on the launch stream around them."""
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        with torch.cuda.stream(s):
+            e0.record(s)
+            for _ in range(n):
+                g.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t) * 1e6 / n
+        return wall, e0.elapsed_time(e1) * 1e3 / n
+
+    # the headline step: the whole step's BitLinears as one persistent launch
+    graph = capture(step.step_persistent)
+    log("[bench] persistent step captured; timing")
+    us_wall, us_event = timed(graph, args.steps)
     step.check()  # a bounded wait that ran out inside the timed replays raises here
-    ms_per_step = t_el * 1e3 / args.steps
+    ms_per_step = us_wall * 1e-3
     nbytes = step.algorithmic_bytes()
     value = nbytes["step"] / (ms_per_step * 1e-3) / 1e9
-    log(f"[bench] {ms_per_step * 1e3:.1f} us per step, {value:.0f} GB/s")
+    log(f"[bench] {us_wall:.1f} us per step ({us_event:.1f} us between events on the launch stream), "
+        f"{value:.0f} GB/s")
+    del graph
 
-    # the same step as persistent per-layer launches (btl_decode_layer)
-    with torch.cuda.stream(s):
-        step.reset_hidden()
-        step.step_layers()
-    torch.cuda.synchronize()
-    graph_l = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph_l, stream=s):
-        step.step_layers()
-    with torch.cuda.stream(s):
-        for _ in range(args.warmup):
-            graph_l.replay()
-    torch.cuda.synchronize()
-    t_l = time.perf_counter()
-    with torch.cuda.stream(s):
-        for _ in range(args.steps):
-            graph_l.replay()
-    torch.cuda.synchronize()
-    us_layers = (time.perf_counter() - t_l) * 1e6 / args.steps
+    # the same step as 120 per-BitLinear launches and as 31 per-layer launches
+    graph_c = capture(step.step_per_call)
+    us_per_call, _ = timed(graph_c, args.steps)
+    step.check()
+    del graph_c
+    graph_l = capture(step.step_layers)
+    us_layers, _ = timed(graph_l, args.steps)
     step.check()
     del graph_l
-    log(f"[bench] persistent per-layer launches: {us_layers:.1f} us per step")
+    log(f"[bench] per-BitLinear launches: {us_per_call:.1f} us per step; per-layer launches: "
+        f"{us_layers:.1f} us per step")
+
+    # the three launch structures compute the same bits from the same input
+    outs = {}
+    for name, fn in (("persistent", step.step_persistent), ("per_call", step.step_per_call),
+                     ("layers", step.step_layers)):
+        step.reset_hidden()
+        fn()
+        step.check()
+        outs[name] = step.hidden.clone()
+    same_bits = all(torch.equal(outs["persistent"].view(torch.int16), o.view(torch.int16)) for o in outs.values())
+    log(f"[bench] persistent / per-call / per-layer hidden bits equal: {same_bits}")
+    if not same_bits:
+        raise SystemExit("launch structures disagree")
 
     # the whole step: decode attention (context 512, every user at the last
     # position) between each layer's QKV and o_proj
@@ -641,25 +673,18 @@ def main():
     kt = kernel_event_timing(step, torch, args.kernel_reps)
     for name, r in kt.items():
         log(f"[bench] {name}: {r['us_per_launch_median']:.2f} us per launch (median of {args.kernel_reps})")
-    # dominant kernel: the kind with the largest share of the step
-    dom = max(KINDS, key=lambda k: kt[k]["us_per_launch_median"])
-    dom_bytes = nbytes[dom]
-    dom_us = kt[dom]["us_per_launch_median"]
-    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
-    traffic = committed_traffic(dom)
+    # dominant kernel: the persistent step kernel, the only launch of a step
+    achieved = nbytes["step"] / (us_event * 1e-6) / 1e9
     roofline = {
         "bound": "hbm",
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": traffic,
-        "kernel": f"k_bitlinear_decode ({dom}: " + {
-            "qkv": "RMSNorm->QKV 2560->3840", "o_proj": "attn_sub_norm->o_proj 2560->2560 +residual",
-            "gate_up": "RMSNorm->gate||up 2560->2x6912, relu2*up", "down": "ffn_sub_norm->down 6912->2560 +residual",
-        }[dom] + ", M=32)",
-        "bytes_per_launch": dom_bytes,
-        "us_per_launch": round(dom_us, 3),
+        "traffic": committed_traffic("step"),
+        "kernel": f"k_decode_step (all {args.layers} layers' QKV, o_proj, gate||up, down at M=32 in one launch)",
+        "bytes_per_launch": nbytes["step"],
+        "us_per_launch": round(us_event, 3),
     }
     kernel_us = {k: round(v["us_per_launch_median"], 3) for k, v in kt.items()}
     kernel_frac = {k: round(nbytes[k] / (kt[k]["us_per_launch_median"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
@@ -683,8 +708,9 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         # the GPU's result of one step from the seeded input, for the CPU path's agreement figure
+        # (the attention timing above rewrote attn_out, so the GPU step runs again here)
         step.reset_hidden()
-        step.step()
+        step.step_persistent()
         step.check()
         gpu_hidden = step.hidden.cpu()
         log("[bench] CPU baseline (reference CPU path: numpy absmax + torch fp32 GEMM) ...")
@@ -708,14 +734,17 @@ def main():
                 "activations N(0,1) with 1% outlier channels x20)",
         "config": {
             "workload": f"BitLinear portion of a batch-32 BitNet b1.58 2B decode step ({args.layers} layers x "
-                        "4 fused BitLinear launches: RMSNorm->QKV 2560->3840, o_proj 2560->2560, "
-                        "gate||up 2560->2x6912 relu2, down 6912->2560), HIP-graph replay",
+                        "4 fused BitLinears: RMSNorm->QKV 2560->3840, o_proj 2560->2560, "
+                        "gate||up 2560->2x6912 relu2, down 6912->2560) as one persistent launch, HIP-graph replay",
             "batch": 32,
             "layers": args.layers,
             "bytes_per_step": nbytes["step"],
             "step_roofline_frac": round(value / HBM_PEAK_GBS, 4),
+            "us_per_step_event": round(us_event, 1),
+            "us_per_step_per_bitlinear_launches": round(us_per_call, 1),
             "us_per_step_layer_launches": round(us_layers, 1),
-            "us_per_launch": kernel_us,
+            "launch_structures_bits_equal": same_bits,
+            "us_per_bitlinear_launch": kernel_us,
             "roofline_frac_per_launch": kernel_frac,
             "per_kind_rotation_bytes": {k: v["distinct_weight_bytes"] for k, v in kt.items()},
             "seeds": {"weights": args.seed, "activations": 1, "kv_cache": 3, "prefill": PREFILL_SEED,

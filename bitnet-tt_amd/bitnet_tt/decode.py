@@ -11,16 +11,21 @@ generator_batch32.py:713-761) issues four ternary-matmul launches:
 Here the remaining norms and residual adds ride along with the BitLinears:
 attn_sub_norm and post_attention_layernorm become RMSNorm prologues, relu^2*up
 the gate||up epilogue, ffn_sub_norm the down prologue, and both residual adds
-epilogues.  Two launch structures compute the same bits:
+epilogues.  Three launch structures compute the same bits:
 
-* ``step_per_call`` (the default ``step``): one ``btl_bitlinear_fused``
-  launch per BitLinear (120 per 30-layer step);
+* ``step_persistent``: the whole step's BitLinears as one ``btl_decode_step``
+  launch (one workgroup per CU; 32 row workgroups run the elementwise stages
+  of the token rows, the others one GEMM unit of each BitLinear, with weights
+  loaded one BitLinear ahead).  The fastest on MI355X (0.81 ms for the 2B
+  model's 30 layers); it needs the attention width equal to hidden and the
+  shape limits of include/btl.h.
+* ``step_per_call`` (the default ``step``, which takes any shape the fused
+  op takes): one ``btl_bitlinear_fused`` launch per BitLinear (120 per
+  30-layer step, 1.0 ms);
 * ``step_layers``: layer 0's QKV as one such launch, then one
   ``btl_decode_layer`` launch per layer covering o_proj, gate||up, down and
   the next layer's QKV -- the BitLinear work between two attentions (31
-  launches per step).  On MI355X it measures within a few percent of the
-  per-call chain: the in-kernel hand-offs cost about what kernel boundaries
-  cost, so the default stays with the per-call launches.
+  launches per step, 1.26 ms).
 
 ``step`` takes the attention output as an input buffer (the BitLinear
 portion alone).  After ``alloc_attention`` the step can also run whole:

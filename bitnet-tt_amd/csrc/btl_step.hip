@@ -59,7 +59,14 @@ constexpr int kStepMaxGrid = 1024;
 constexpr int kStepWSlots = 7;      // weight registers (16 B each) per wave and buffer
 enum { S_QKV = 0, S_O = 1, S_GU = 2, S_DN = 3, kStepOps = 4 };
 
-// Workspace: header, op table, then one region per layer.
+// Workspace: header, op table, then one hand-off region (operand tiles, a/127,
+// row flags, tagged output words) that every layer reuses.  Reuse is safe by
+// the dependency chain: row m overwrites its slice of (layer l+1, BitLinear j)
+// only after it has received all of its outputs of (l, j) -- and every unit
+// that reads row m's slice of tile (l, j) or polls its flag writes row m's
+// outputs of (l, j) only after those reads -- and a GEMM unit overwrites the
+// tagged words of (l+1, j) only after every row it covers has published
+// (l+1, j), which each row does after reading its words of (l, j).
 constexpr int64_t kStEpoch = 0;          // [kStepMaxGrid] u32
 constexpr int64_t kStError = 4096;       // u32
 constexpr int64_t kStTable = 8192;       // StepOp[L][4]
@@ -112,8 +119,7 @@ struct StepArgs {
   uint16_t* ffn_h;       // [M][F]
   uint32_t* epoch;
   uint32_t* error;
-  char* layers;          // first layer region
-  int64_t layer_stride;  // bytes between layers' hand-off regions (0: one region for all layers)
+  char* layers;          // the hand-off region
   int64_t off_xa[kStepOps], off_adq, off_flag, off_out[kStepOps];
   unsigned spin_limit;
 };
@@ -129,7 +135,7 @@ __device__ __forceinline__ uint32_t step_tag(uint32_t E, int l, int j) { return 
     if ((l) == BTL_STEP_TRACE_LAYER) BTL_TRACE_AT(ev); \
   } while (0)
 
-__device__ __forceinline__ char* layer_base(const StepArgs& p, int l) { return p.layers + (int64_t)l * p.layer_stride; }
+__device__ __forceinline__ char* layer_base(const StepArgs& p, int) { return p.layers; }
 __device__ __forceinline__ int8_t* tile_of(const StepArgs& p, int l, int j) {
   return reinterpret_cast<int8_t*>(layer_base(p, l) + p.off_xa[j]);
 }
@@ -694,7 +700,7 @@ struct StepSizes {
   int64_t off_xa[kStepOps], off_adq, off_flag, off_out[kStepOps], layer_bytes, total;
 };
 
-static StepSizes step_sizes(int64_t H, int64_t F, int64_t NQKV, int64_t L) {
+static StepSizes step_sizes(int64_t H, int64_t F, int64_t NQKV) {
   StepSizes z;
   const int64_t Ks[kStepOps] = {H, H, H, F};
   // tagged words (bf16 pairs) a row workgroup reads back
@@ -713,7 +719,7 @@ static StepSizes step_sizes(int64_t H, int64_t F, int64_t NQKV, int64_t L) {
     off += round_up(32 * words[j] * 8, 4096);
   }
   z.layer_bytes = round_up(off, 65536);
-  z.total = kStHeader + z.layer_bytes * L;
+  z.total = kStHeader + z.layer_bytes;
   return z;
 }
 
@@ -755,7 +761,7 @@ extern "C" {
 
 int64_t btl_decode_step_workspace_bytes(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L) {
   if (M <= 0 || M > 32 || H <= 0 || F <= 0 || NQKV <= 0 || L <= 0 || L > kStepMaxLayers) return 0;
-  return step_sizes(H, F, NQKV, L).total;
+  return step_sizes(H, F, NQKV).total;
 }
 
 int64_t btl_decode_step_error_offset(void) { return kStError; }
@@ -767,7 +773,7 @@ int btl_decode_step_prepare(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64
   if (rc) return rc;
   if (!weights || !workspace) return set_error(BTL_ERR_NULL, "btl_decode_step_prepare: null pointer");
   if (!aligned(workspace, 256)) return set_error(BTL_ERR_ALIGN, "btl_decode_step_prepare: workspace must be 256-byte aligned");
-  const StepSizes z = step_sizes(H, F, NQKV, L);
+  const StepSizes z = step_sizes(H, F, NQKV);
   if ((int64_t)workspace_bytes < z.total)
     return set_error(BTL_ERR_WORKSPACE, "btl_decode_step_prepare: workspace %zu < %lld bytes", workspace_bytes,
                      (long long)z.total);
@@ -826,7 +832,7 @@ int btl_decode_step(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, fl
   if (!aligned(attn, 16) || !aligned(hidden, 16) || !aligned(workspace, 256) || !aligned(qkv_out, 2) ||
       !aligned(ffn_h, 2))
     return set_error(BTL_ERR_ALIGN, "btl_decode_step: attn/hidden must be 16-byte aligned, workspace 256");
-  const StepSizes z = step_sizes(H, F, NQKV, L);
+  const StepSizes z = step_sizes(H, F, NQKV);
   if ((int64_t)workspace_bytes < z.total)
     return set_error(BTL_ERR_WORKSPACE, "btl_decode_step: workspace %zu < %lld bytes", workspace_bytes,
                      (long long)z.total);
@@ -848,7 +854,6 @@ int btl_decode_step(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, fl
   a.epoch = reinterpret_cast<uint32_t*>(ws + kStEpoch);
   a.error = reinterpret_cast<uint32_t*>(ws + kStError);
   a.layers = ws + kStHeader;
-  a.layer_stride = getenv("BTL_STEP_LAYER_REGIONS") ? z.layer_bytes : 0;
   for (int j = 0; j < kStepOps; ++j) {
     a.off_xa[j] = z.off_xa[j];
     a.off_out[j] = z.off_out[j];

@@ -257,7 +257,9 @@ int btl_decode_layer(int64_t M, int64_t H, int64_t Q, int64_t F, int64_t NQKV, c
  * of the RMSNorm in front of each (qkv: three segments ending at Q, Q+KV,
  * NQKV; gate_up: two segments split at F).  Shapes: M <= 32 rows, H = the
  * attention width (o_proj is H -> H), H and F multiples of 128, H <= 3072,
- * F <= 8192, NQKV <= 4096.  attn [M,H], hidden [M,H] (in/out), qkv_out
+ * F <= 7168, NQKV <= 4096 (a multiple of 64), L <= 64, and the GEMM units
+ * max(NQKV/32, H/16, F/32) at most the CU count minus 32 (224 on a 256-CU
+ * MI355X).  attn [M,H], hidden [M,H] (in/out), qkv_out
  * [M,NQKV] and ffn_h [M,F] bf16 (the last layer's values).
  *
  * Workspace (256-byte aligned): btl_decode_step_workspace_bytes(...) bytes,

@@ -190,6 +190,32 @@ def test_decode_layer_sizes_and_argument_checks(L):
 
 
 
+def test_decode_step_sizes_and_argument_checks(L):
+    # one hand-off region reused by every layer: the workspace does not grow with L
+    ws1 = L.btl_decode_step_workspace_bytes(32, 2560, 6912, 3840, 1)
+    ws30 = L.btl_decode_step_workspace_bytes(32, 2560, 6912, 3840, 30)
+    tiles = 32 * (3 * 2560 + 6912)
+    words = 32 * (3840 + 2560 + 6912 + 2560) // 2 * 8
+    assert ws1 == ws30 and ws30 >= tiles + words + 4 * 32 * 128
+    assert L.btl_decode_step_workspace_bytes(33, 2560, 6912, 3840, 30) == 0
+    assert L.btl_decode_step_workspace_bytes(32, 2560, 6912, 3840, 65) == 0
+    assert L.btl_decode_step_error_offset() % 4 == 0 and 0 < L.btl_decode_step_error_offset() < ws30
+
+    def step(M=32, H=2560, F=6912, NQ=3840, nl=30, attn=FAKE, ws_bytes=1 << 28):
+        return L.btl_decode_step(M, H, F, NQ, nl, 1e-5, _p(attn) if attn else None, _p(FAKE), _p(FAKE), _p(FAKE),
+                                 _p(FAKE), ws_bytes, None)
+
+    # every case below fails a shape check that runs before the library touches HIP
+    assert step(M=0) == 2 and step(M=33) == 2
+    assert step(nl=0) == 2 and step(nl=65) == 2
+    assert step(H=2500) == 2 and step(NQ=3850) == 2
+    assert step(F=8192) == 2  # 64 superblocks of K = F exceed the down projection's weight registers
+    assert "weight registers" in N.last_error()
+    assert step(H=3200) == 2  # 25 superblocks of K = H exceed three register slots
+    table = (N.LayerWeight * 4)()
+    assert L.btl_decode_step_prepare(0, 2560, 6912, 3840, 1, table, _p(FAKE), 1 << 28) == 2
+
+
 def test_lm_head_sizes_and_argument_checks(L):
     # 16 vocab rows x 32 k per KiB, K padded to the supported multiple of 256
     assert L.btl_lm_head_weight_bytes(128256, 2560) == 128256 * 2560 * 2
