@@ -58,6 +58,8 @@ def parse():
     ap.add_argument("--cpu-reps", type=int, default=20, help="timed CPU-baseline steps (after 3 warm-ups)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="run only the workload of the rocprofv3 --pmc traffic runs and exit")
+    ap.add_argument("--prefill-pmc-pass", action="store_true",
+                    help="run only the prefill GEMMs (5 launches per configured shape) for rocprofv3 --pmc and exit")
     return ap.parse_args()
 
 
@@ -254,7 +256,7 @@ def graph_time_us(torch, dev, launch, reps=20, warm=3):
     return us
 
 
-def prefill_mfma(torch, N, dev, shapes=PREFILL_SHAPES):
+def prefill_mfma(torch, N, dev, shapes=PREFILL_SHAPES, pmc_reps=0):
     """MFMA-i8 utilisation of the prefill BitLinear at the configured shapes.
 
     Inputs as the prefill configuration states them: x bf16 ~N(0, 1) with 1 %
@@ -262,7 +264,10 @@ def prefill_mfma(torch, N, dev, shapes=PREFILL_SHAPES):
     seeded N(0, 0.02) latents (4 copies with distinct latents, cycled).  Two
     figures per shape: the GEMM alone (btl_gemm_i8t2 on the activation
     kernel's int8 operand, scales and row sums) and the whole BitLinear
-    (btl_bitlinear_fused: RMSNorm + absmax activation kernel, then the GEMM)."""
+    (btl_bitlinear_fused: RMSNorm + absmax activation kernel, then the GEMM).
+    With pmc_reps > 0 nothing is timed: each shape's GEMM runs pmc_reps times
+    eagerly, in the order of `shapes` (the workload of the rocprofv3 --pmc
+    MFMA counter runs)."""
     from bitnet_tt.layers.bitlinear import pack_for_device
     from bitnet_tt.ternary_matmul import ternary_matmul_into
     from bitnet_tt.utils.quantization import weight_quant_ternary
@@ -303,6 +308,14 @@ def prefill_mfma(torch, N, dev, shapes=PREFILL_SHAPES):
         def bitlinear(i):
             ternary_matmul_into(x, pws[i % copies], o, norm_weight=gamma, norm_epsilon=1e-5)
 
+        if pmc_reps:
+            for i in range(pmc_reps):
+                gemm(i)
+            torch.cuda.synchronize()
+            log(f"[bench] prefill pmc pass: M={M} K={K} N={Nf}: {pmc_reps} GEMM launches")
+            out.append({"M": M, "K": K, "N": Nf})
+            del pws
+            continue
         us = graph_time_us(torch, dev, gemm)
         us_bl = graph_time_us(torch, dev, bitlinear)
         ops = 2.0 * M * K * Nf
@@ -578,6 +591,9 @@ def main():
     N.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.prefill_pmc_pass:
+        prefill_mfma(torch, N, dev, pmc_reps=5)
+        return
     cfg = BitNet2B4TConfig()
     t0 = time.time()
     step = BitLinearDecodeStep.random_init(cfg, dev, seed=args.seed, num_layers=args.layers).alloc_buffers(seed=1)
