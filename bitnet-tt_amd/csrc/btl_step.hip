@@ -624,6 +624,11 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
       }
     }
     lds_barrier();  // LDS free for the next BitLinear
+    // The a/127 loads (long done) are collected here, before the first store:
+    // stores share the in-order vector-memory counter with loads, and with the
+    // stores under lane masks the compiler would otherwise wait for all of
+    // them, coherent write acknowledgements included, before the second row.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     const int jc = lane & 31;
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
