@@ -152,6 +152,18 @@ __device__ __forceinline__ uint64_t* out_of(const StepArgs& p, int l, int j) {
   return reinterpret_cast<uint64_t*>(layer_base(p, l) + p.off_out[j]);
 }
 
+// Loads of an operand tile.  Every layer reuses the tile's addresses, and a
+// CU's L1 may still hold lines it read one layer earlier, so the loads are
+// device-scope (sc1): they bypass the L1 and read the L2, which the rows'
+// device-coherent stores keep current.  Lane offset in a VGPR, the rest in an
+// SGPR.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const int8_t* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(base), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ v4i ld_tile(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 16));
+}
+
 __device__ __forceinline__ float op_seg_scale(const StepOp& op, int n) {
   float s = op.seg_scale[0];
 #pragma unroll
@@ -510,7 +522,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
                              const v4i (&w)[kStepWSlots], v4i (&wn)[kStepWSlots], int nl, int32_t* lds,
                              WaitState& ws) {
   constexpr int TPW = OpShape<J>::TPW, MODE = OpShape<J>::MODE;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   if (gi >= op_units<J>(p)) {
     if (nl < p.L) load_unit_weights<NJ, NNSW>(p, sops, nl, gi, wn);
     return;
@@ -527,7 +539,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
   if (wv == kStepPollWave) wait_flags(p, l, J, 16 * h, NR, want, s_rsum, ws);
   lds_barrier();  // the operand rows are out (no wait for loads in flight)
   STEP_TRACE(l, 8 + 2 * J);
-  const int8_t* xa = tile_of(p, l, J);
+  const __amdgpu_buffer_rsrc_t xa = tile_rsrc(tile_of(p, l, J), 32 * op_ks(p, J) * 128);
   const float* adq = adq_of(p, l, J);
   uint64_t* outw = out_of(p, l, J);
   const int n_out = J == S_QKV ? p.NQKV : J == S_GU ? p.F : p.H;
@@ -549,7 +561,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     for (int i = 0; i < NSW; ++i)
       if (i < cnt)
 #pragma unroll
-        for (int pp = 0; pp < 2; ++pp) a[i][pp] = ld128(xa + (((wb + i) * 4 + 2 * pp + a_step) * 64 + a_lane) * 16);
+        for (int pp = 0; pp < 2; ++pp) a[i][pp] = ld_tile(xa, (a_step * 64 + a_lane) * 16, ((wb + i) * 4 + 2 * pp) * 1024);
     v4i acc[2] = {(v4i){0, 0, 0, 0}, (v4i){0, 0, 0, 0}};
 #pragma unroll
     for (int i = 0; i < NSW; ++i)
@@ -592,7 +604,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     for (int i = 0; i < NSW; ++i)
       if (i < cnt)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) a[i][q] = ld128(xa + (((wb + i) * 4 + q) * 64 + lane) * 16);
+        for (int q = 0; q < 4; ++q) a[i][q] = ld_tile(xa, lane * 16, ((wb + i) * 4 + q) * 1024);
     v16i acc[TPW];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) acc[t] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
