@@ -663,6 +663,13 @@ def main():
     del graph_l
     log(f"[bench] per-BitLinear launches: {us_per_call:.1f} us per step; per-layer launches: "
         f"{us_layers:.1f} us per step")
+    # the latency floor of the persistent step's launch structure: the same
+    # waits and hand-off stores with no arithmetic and no weight traffic
+    graph_f = capture(step.step_floor)
+    us_floor, _ = timed(graph_f, args.steps)
+    step.check()
+    del graph_f
+    log(f"[bench] hand-off floor of the persistent step (waits and hand-off stores only): {us_floor:.1f} us per step")
 
     # the three launch structures compute the same bits from the same input
     outs = {}
@@ -759,6 +766,7 @@ def main():
             "us_per_step_event": round(us_event, 1),
             "us_per_step_per_bitlinear_launches": round(us_per_call, 1),
             "us_per_step_layer_launches": round(us_layers, 1),
+            "us_per_step_handoff_floor": round(us_floor, 1),
             "launch_structures_bits_equal": same_bits,
             "us_per_bitlinear_launch": kernel_us,
             "roofline_frac_per_launch": kernel_frac,

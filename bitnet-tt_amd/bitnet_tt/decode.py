@@ -448,6 +448,25 @@ class BitLinearDecodeStep:
         )
         return self.hidden
 
+    def step_floor(self):
+        """btl_decode_step_floor on this stream's step workspace: the persistent
+        step's launch structure (waits and hand-off stores) with no
+        arithmetic, whose time is the latency floor of the step's chain of
+        dependent hand-offs.  Changes no tensor of the step."""
+        c = self.config
+        B, H, F = self.batch, c.hidden_size, c.intermediate_size
+        nl = len(self.layers)
+        L = N.lib()
+        dev = self.hidden.device
+        nbytes = int(L.btl_decode_step_workspace_bytes(B, H, F, c.qkv_dim, nl))
+        import torch
+
+        if torch.cuda.is_current_stream_capturing() and not N.has_workspace(dev, nbytes, "step"):
+            raise RuntimeError("run one eager decode step on this stream before capturing it in a graph")
+        ws = N.workspace(dev, nbytes, kind="step", error_offset=int(L.btl_decode_step_error_offset()))
+        N.check(L.btl_decode_step_floor(B, H, F, c.qkv_dim, nl, N.ptr(ws), ws.numel(), N.stream_of(dev)),
+                "btl_decode_step_floor")
+
     def step(self):
         return self.step_per_call()
 

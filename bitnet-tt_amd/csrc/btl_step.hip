@@ -712,6 +712,81 @@ __global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
   if (threadIdx.x == 0) p.epoch[b] = E;
 }
 
+// ------------------------------------------------------- hand-off floor ----
+// The step's launch structure with no arithmetic, for measurement: per
+// BitLinear the row workgroups wait for every word of their row of the
+// previous BitLinear's output (as the step does), then set their flag; each
+// GEMM unit waits for its rows' flags (as the step does), then writes its
+// tagged words (zero payload) in the step's store pattern.  No weight,
+// operand tile, gain or norm is touched and nothing is computed, so its time
+// is the latency floor that the chain of 120 dependent hand-off pairs sets.
+template <int CF>
+__device__ void floor_row(const StepArgs& p, int m, uint32_t E) {
+  WaitState ws{false};
+  for (int l = 0; l < p.L; ++l)
+    for (int j = 0; j < kStepOps; ++j) {
+      if (l > 0 || j > 0) {  // the words this row stage waits for in the step
+        const int pj = j > 0 ? j - 1 : S_DN, pl = j > 0 ? l : l - 1;
+        const int ncols = pj == S_QKV ? p.NQKV : pj == S_GU ? p.F : p.H;
+        uint32_t pr[CF][4];
+        if (pj == S_GU)
+          wait_row_words<CF>(p, out_of(p, pl, pj) + (int64_t)m * (ncols >> 1), ncols, step_tag(E, pl, pj), pr, ws);
+        else
+          wait_row_words<1>(p, out_of(p, pl, pj) + (int64_t)m * (ncols >> 1), ncols, step_tag(E, pl, pj),
+                            reinterpret_cast<uint32_t(&)[1][4]>(pr), ws);
+      }
+      __syncthreads();
+      if (threadIdx.x == 0) st_coherent(flag_of(p, l, j, m), (uint64_t)step_tag(E, l, j) << 32);
+    }
+  uint32_t pr[1][4];  // the last down projection's words end the row's step
+  wait_row_words<1>(p, out_of(p, p.L - 1, S_DN) + (int64_t)m * (p.H >> 1), p.H, step_tag(E, p.L - 1, S_DN), pr, ws);
+}
+
+template <int J>
+__device__ __forceinline__ void floor_gemm_op(const StepArgs& p, int l, int gi, uint32_t E, int32_t* s_rsum,
+                                              WaitState& ws) {
+  if (gi >= op_units<J>(p)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  int tile0, h;
+  unit_of<J>(p, gi, tile0, h);
+  const uint32_t want = step_tag(E, l, J);
+  constexpr int NR = OpShape<J>::HALF ? 16 : 32;
+  if (wv == kStepPollWave) wait_flags(p, l, J, 16 * h, NR, want, s_rsum, ws);
+  lds_barrier();
+  uint64_t* outw = out_of(p, l, J);
+  const int n_out = J == S_QKV ? p.NQKV : J == S_GU ? p.F : p.H;
+  if constexpr (OpShape<J>::HALF) {
+    const int er = tid >> 5, ec = tid & 31, row = 16 * h + er, n = tile0 * 32 + ec;
+    if ((ec & 1) == 0) st_coherent(outw + (int64_t)row * (n_out >> 1) + (n >> 1), (uint64_t)want << 32);
+  } else {
+    const int jc = lane & 31, n = tile0 * 32 + jc;
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int i = acc_row(wv + kStepWaves * rr, lane);
+      if ((jc & 1) == 0) st_coherent(outw + (int64_t)i * (n_out >> 1) + (n >> 1), (uint64_t)want << 32);
+    }
+  }
+}
+
+template <int CF>
+__global__ __launch_bounds__(512) void k_decode_step_floor(StepArgs p) {
+  __shared__ int32_t s_rsum[32];
+  const int b = blockIdx.x;
+  const uint32_t E = p.epoch[b] + 1u;
+  if (b < kStepRows) {
+    floor_row<CF>(p, b, E);
+  } else {
+    WaitState ws{false};
+    for (int l = 0; l < p.L; ++l) {
+      floor_gemm_op<S_QKV>(p, l, b - kStepRows, E, s_rsum, ws);
+      floor_gemm_op<S_O>(p, l, b - kStepRows, E, s_rsum, ws);
+      floor_gemm_op<S_GU>(p, l, b - kStepRows, E, s_rsum, ws);
+      floor_gemm_op<S_DN>(p, l, b - kStepRows, E, s_rsum, ws);
+    }
+  }
+  if (threadIdx.x == 0) p.epoch[b] = E;
+}
+
 // ---------------------------------------------------------------- host ----
 struct StepSizes {
   int64_t off_xa[kStepOps], off_adq, off_flag, off_out[kStepOps], layer_bytes, total;
@@ -888,6 +963,45 @@ int btl_decode_step(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, fl
   else
     return set_error(BTL_ERR_SHAPE, "btl_decode_step: no kernel instance for H=%lld F=%lld", (long long)H, (long long)F);
   return check_launch("decode step");
+}
+
+int btl_decode_step_floor(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, void* workspace,
+                          size_t workspace_bytes, btl_stream_t stream) {
+  clear_error();
+  int rc = step_check_shape(M, H, F, NQKV, L);
+  if (rc) return rc;
+  if (!workspace) return set_error(BTL_ERR_NULL, "btl_decode_step_floor: null workspace");
+  if (!aligned(workspace, 256)) return set_error(BTL_ERR_ALIGN, "btl_decode_step_floor: workspace must be 256-byte aligned");
+  const StepSizes z = step_sizes(H, F, NQKV);
+  if ((int64_t)workspace_bytes < z.total)
+    return set_error(BTL_ERR_WORKSPACE, "btl_decode_step_floor: workspace %zu < %lld bytes", workspace_bytes,
+                     (long long)z.total);
+  char* ws = (char*)workspace;
+  StepArgs a = {};
+  a.L = (int)L;
+  a.M = (int)M;
+  a.H = (int)H;
+  a.F = (int)F;
+  a.NQKV = (int)NQKV;
+  a.KSH = (int)ksb(H);
+  a.KSF = (int)ksb(F);
+  a.epoch = reinterpret_cast<uint32_t*>(ws + kStEpoch);
+  a.error = reinterpret_cast<uint32_t*>(ws + kStError);
+  a.layers = ws + kStHeader;
+  for (int j = 0; j < kStepOps; ++j) {
+    a.off_xa[j] = z.off_xa[j];
+    a.off_out[j] = z.off_out[j];
+  }
+  a.off_adq = z.off_adq;
+  a.off_flag = z.off_flag;
+  a.spin_limit = 1u << 18;
+  const int grid = step_grid();
+  hipStream_t s = (hipStream_t)stream;
+  if (act_cpt(F) == 1)
+    hipLaunchKernelGGL((k_decode_step_floor<1>), dim3(grid), dim3(512), 0, s, a);
+  else
+    hipLaunchKernelGGL((k_decode_step_floor<2>), dim3(grid), dim3(512), 0, s, a);
+  return check_launch("decode step floor");
 }
 
 }  // extern "C"

@@ -277,6 +277,19 @@ int btl_decode_step(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, fl
                     uint16_t* hidden, uint16_t* qkv_out, uint16_t* ffn_h, void* workspace, size_t workspace_bytes,
                     btl_stream_t stream);
 
+/* Measurement aid with no counterpart in the reference: btl_decode_step's
+ * launch structure with no arithmetic.  The same workgroups, waits and
+ * hand-off stores (row workgroups wait for every word of their row of the
+ * previous BitLinear's output and set their flags; GEMM units wait for their
+ * rows' flags and write their tagged output words), but no weight, operand
+ * tile, gain or norm is read and nothing is computed: the launch time is the
+ * latency floor of the step's 4L dependent hand-off pairs.  Same shapes and
+ * workspace as btl_decode_step (it may be interleaved with btl_decode_step
+ * calls on that workspace; it needs no btl_decode_step_prepare); writes only
+ * the workspace. */
+int btl_decode_step_floor(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, void* workspace,
+                          size_t workspace_bytes, btl_stream_t stream);
+
 /* ---- LM head (final norm is btl_rmsnorm) ------------------------------
  * Replaces the head matmul of src/bitnet_tt/inference/generator_batch32.py:
  * 768-811 (ttnn.matmul of the normed hidden state with the head weight that

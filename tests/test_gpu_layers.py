@@ -297,6 +297,32 @@ def test_persistent_step_mini_matches_per_call(orc, batch, layers):
         assert np.array_equal(H.bits_of(step.ffn_h), ref_ffn), f"launch {rep}: ffn_h"
 
 
+def test_handoff_floor_interleaves_with_the_step(orc):
+    """btl_decode_step_floor (the persistent step's waits and hand-off stores
+    with no arithmetic) runs on the step's workspace without a timed-out
+    wait, and persistent steps launched after it on that workspace still
+    equal the oracle chain bit for bit."""
+    cfg = BitNetMiniConfig(num_layers=2)
+    step = BitLinearDecodeStep.random_init(cfg, H.dev(), seed=51).alloc_buffers(seed=52)
+    hid, attn = H.bits_of(step.hidden0), H.bits_of(step.attn_out)
+    for i in range(2):
+        hid, qkv = oracle_layer(orc, step, i, hid, attn)
+    step.step_persistent()
+    step.check()
+    assert np.array_equal(H.bits_of(step.hidden), hid)
+    for rep in range(3):
+        print(f"hand-off floor launch {rep}", flush=True)
+        before = H.bits_of(step.hidden)
+        step.step_floor()
+        step.check()
+        assert np.array_equal(H.bits_of(step.hidden), before), "the floor launch changed hidden"
+        step.reset_hidden()
+        step.step_persistent()
+        step.check()
+        assert np.array_equal(H.bits_of(step.hidden), hid), f"step after floor launch {rep}"
+        assert np.array_equal(H.bits_of(step.qkv_out), qkv), f"qkv after floor launch {rep}"
+
+
 def test_persistent_step_graph_replay(orc):
     """The one-launch step captured in a HIP graph: every replay, with eager
     work between replays, equals the eager launch."""
