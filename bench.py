@@ -575,6 +575,73 @@ def cpu_baseline(step, torch, gpu_hidden, reps=20, warmup=3):
     }
 
 
+def dot4_variant_timing(step, torch, N, reps=10):
+    """The decode GEMM of each BitLinear kind at M = 32 as the library runs it
+    (btl_gemm_i8t2: MFMA) and formulated on the VALU (btl_gemm_i8t2_dot4:
+    v_dot4_i32_i8), on the same int8 operand tile and the 30 layers' weights:
+    a graph of 30 launches per kernel, timed with events on its stream, in us
+    per launch (median of reps).  The GEMM alone: the operand tile comes from
+    one btl_quant_absmax call made beforehand."""
+    L = N.lib()
+    dev = step.device
+    c = step.config
+    H_, F_ = c.hidden_size, c.intermediate_size
+    shapes = {"qkv": (H_, c.qkv_dim), "o_proj": (H_, H_), "gate_up": (H_, 2 * F_), "down": (F_, H_)}
+    s = torch.cuda.Stream(device=dev)
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(53)
+    res = {}
+    for kind, (K, Nn) in shapes.items():
+        x = torch.randn(32, K, generator=gen).to(torch.bfloat16).to(dev)
+        xa = torch.empty(int(L.btl_act_bytes(32, K)), dtype=torch.uint8, device=dev)
+        a_dq = torch.empty(32, dtype=torch.float32, device=dev)
+        rs = torch.empty(32, dtype=torch.int32, device=dev)
+        N.check(L.btl_quant_absmax(N.ptr(x), 32, K, K, None, 0.0, N.ptr(xa), N.ptr(a_dq), N.ptr(rs), None, None,
+                                   None, N.stream_of(dev)), "btl_quant_absmax")
+        out = torch.empty(32, Nn, dtype=torch.bfloat16, device=dev)
+        acc = torch.zeros(32, Nn, dtype=torch.int32, device=dev)
+        wsb = int(L.btl_gemm_workspace_bytes(32, K, Nn, 0, 0))
+        ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
+        sc, en, nseg = N.segments_arrays([1.0], [Nn])
+        ws_ = [getattr(Lr, KIND_ATTR[kind]).data for Lr in step.layers]
+
+        def mfma(w):
+            N.check(L.btl_gemm_i8t2(N.ptr(xa), N.ptr(a_dq), N.ptr(rs), 32, K, Nn, N.ptr(w), sc, en, nseg, 0, None,
+                                    N.ptr(out), None, N.ptr(ws), ws.numel(), 0, N.stream_of(dev)), "btl_gemm_i8t2")
+
+        def dot4(w):  # accumulates into acc (no clearing inside the timed graph)
+            N.check(L.btl_gemm_i8t2_dot4(N.ptr(xa), N.ptr(rs), 32, K, Nn, N.ptr(w), N.ptr(acc), N.stream_of(dev)),
+                    "btl_gemm_i8t2_dot4")
+
+        res[kind] = {"K": K, "N": Nn}
+        for name, fn in (("us_mfma", mfma), ("us_dot4", dot4)):
+            torch.cuda.synchronize()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                for w in ws_:
+                    fn(w)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                for w in ws_:
+                    fn(w)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            times = []
+            with torch.cuda.stream(s):
+                g.replay()
+                for _ in range(reps):
+                    e0.record(s)
+                    g.replay()
+                    e1.record(s)
+                    e1.synchronize()
+                    times.append(e0.elapsed_time(e1) * 1e3 / len(ws_))
+            torch.cuda.synchronize()
+            times.sort()
+            res[kind][name] = round(times[len(times) // 2], 2)
+            del g
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -693,6 +760,10 @@ def main():
             f"{full['attention_us_per_layer']:.2f} us per layer, {full['attention_GBps']:.0f} GB/s, "
             f"{100 * full['attention_roofline_frac']:.1f} % of HBM")
 
+    dot4 = dot4_variant_timing(step, torch, N, args.kernel_reps)
+    for kind, r in dot4.items():
+        log(f"[bench] decode GEMM {kind} ({r['K']}->{r['N']}): MFMA {r['us_mfma']} us, v_dot4 on the VALU "
+            f"{r['us_dot4']} us per launch")
     kt = kernel_event_timing(step, torch, args.kernel_reps)
     for name, r in kt.items():
         log(f"[bench] {name}: {r['us_per_launch_median']:.2f} us per launch (median of {args.kernel_reps})")
@@ -772,13 +843,14 @@ def main():
             "roofline_frac_per_launch": kernel_frac,
             "per_kind_rotation_bytes": {k: v["distinct_weight_bytes"] for k, v in kt.items()},
             "seeds": {"weights": args.seed, "activations": 1, "kv_cache": 3, "prefill": PREFILL_SEED,
-                      "lm_head": 31},
+                      "lm_head": 31, "dot4_variant": 53},
         },
         "roofline": roofline,
         "cpu_baseline": cpu,
         "prefill_mfma": prefill,
         "lm_head": head,
         "full_step": full,
+        "decode_gemm_dot4_vs_mfma": dot4,
     }
     print(json.dumps(line), flush=True)
 

@@ -150,6 +150,15 @@ int btl_gemm_i8t2(const int8_t* xa, const float* a_dq, const int32_t* rowsum, in
                   const float* seg_scale, const int64_t* seg_end, int nseg, int epilogue, const uint16_t* residual, uint16_t* out, int32_t* acc_out, void* workspace,
                   size_t workspace_bytes, int splitk, btl_stream_t stream);
 
+/* The decode GEMM on the VALU (v_dot4_i32_i8) instead of MFMA: a measured
+ * alternative, with no counterpart in the reference, kept to show the cost of
+ * that formulation on MI355X (bench.py times it beside btl_gemm_i8t2).
+ * acc_out[M, N] (int32, zero-filled by the caller) += the exact accumulators
+ * of q @ w, q the int8 operand tile xa of btl_quant_absmax, w the device
+ * layout, rowsum[M] = sum_k q.  M <= 32, K a multiple of 128, N of 32. */
+int btl_gemm_i8t2_dot4(const int8_t* xa, const int32_t* rowsum, int64_t M, int64_t K, int64_t N,
+                       const uint32_t* wdev, int32_t* acc_out, btl_stream_t stream);
+
 /* Byte offset, inside a btl_bitlinear_fused workspace, of the 32-bit word
  * that is non-zero when a bounded wait of the single-launch decode kernel
  * ran out (the outputs of that call are then invalid).  The first 8192 bytes

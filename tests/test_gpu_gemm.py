@@ -97,6 +97,26 @@ def test_decode_gemm_bit_exact(orc, m, k, n, splitk):
     assert clean, "split-K counters must be left at zero"
 
 
+@pytest.mark.parametrize("m,k,n", [(32, 2560, 2560), (7, 640, 96), (32, 6912, 256), (1, 128, 32)])
+def test_dot4_variant_bit_exact(orc, m, k, n):
+    """The VALU (v_dot4) formulation of the decode GEMM gives the oracle's
+    int32 accumulators."""
+    print(f"dot4 gemm m={m} k={k} n={n}", flush=True)
+    L = N.lib()
+    d = H.dev()
+    rng = np.random.default_rng(m + 3 * k + n)
+    q = rng.integers(-127, 128, size=(m, k)).astype(np.int8)
+    w = H.ternary(k, n, seed=2 * k + n)
+    xa = H.to_dev(H.rowmajor_to_xa(q))
+    wdev = device_weight(orc, w)
+    rs = H.to_dev(q.astype(np.int64).sum(1).astype(np.int32))
+    acc = torch.zeros((m, n), dtype=torch.int32, device=d)
+    N.check(L.btl_gemm_i8t2_dot4(N.ptr(xa), N.ptr(rs), m, k, n, N.ptr(wdev), N.ptr(acc), N.stream_of(d)),
+            "btl_gemm_i8t2_dot4")
+    torch.cuda.synchronize()
+    assert np.array_equal(acc.cpu().numpy(), orc.gemm_i8t(q, w))
+
+
 def test_extreme_accumulators(orc):
     # |acc| = 128 * K at its largest: all -128 against all -1 / +1
     k = 16384
