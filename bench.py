@@ -58,6 +58,10 @@ def parse():
     ap.add_argument("--cpu-reps", type=int, default=20, help="timed CPU-baseline steps (after 3 warm-ups)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="run only the workload of the rocprofv3 --pmc traffic runs and exit")
+    ap.add_argument("--step-trace", action="store_true",
+                    help="load the -DBTL_TRACE build (bitnet_tt/_lib/libbtl_trace.so, from "
+                         "python bitnet-tt_amd/bitnet_tt/_build.py --trace), run persistent steps and print the "
+                         "phase table of layer 10, then exit")
     ap.add_argument("--prefill-pmc-pass", action="store_true",
                     help="run only the prefill GEMMs (5 launches per configured shape) for rocprofv3 --pmc and exit")
     return ap.parse_args()
@@ -642,6 +646,59 @@ def dot4_variant_timing(step, torch, N, reps=10):
     return res
 
 
+STEP_TRACE_EVENTS = {
+    # row workgroups (wave 0): event -> name
+    0: "row: QKV row stage starts", 1: "row: QKV flag set", 2: "row: QKV words in", 3: "row: o_proj flag set",
+    4: "row: o_proj words in", 5: "row: gate||up flag set", 6: "row: gate||up words in", 7: "row: down flag set",
+    # GEMM workgroups (wave 0)
+    8: "GEMM: QKV rows seen", 9: "GEMM: QKV outputs stored", 10: "GEMM: o_proj rows seen",
+    11: "GEMM: o_proj outputs stored", 12: "GEMM: gate||up rows seen", 13: "GEMM: gate||up outputs stored",
+    14: "GEMM: down rows seen", 15: "GEMM: down outputs stored",
+}
+STEP_TRACE_ORDER = (0, 1, 8, 9, 2, 3, 10, 11, 4, 5, 12, 13, 6, 7, 14, 15)
+
+
+def step_trace(step, torch, N, runs=5):
+    """Phase timestamps (s_memrealtime, 100 MHz) of layer 10 of the persistent
+    step from the -DBTL_TRACE build: per event, min / median / max over the
+    workgroups that record it, in us from the first row workgroup's start;
+    the median over `runs` launches of each statistic."""
+    import ctypes
+
+    import numpy as np
+
+    L = N.lib()
+    rd = L.btl_trace_read_step
+    rd.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    rd.restype = ctypes.c_int
+    buf = np.zeros((2048, 16, 16), dtype=np.uint64)
+    for _ in range(3):
+        step.step_persistent()
+    torch.cuda.synchronize()
+    rd(buf.ctypes.data, buf.nbytes)  # clears the table
+    stats = {ev: [] for ev in STEP_TRACE_ORDER}
+    for _ in range(runs):
+        step.step_persistent()
+        torch.cuda.synchronize()
+        rd(buf.ctypes.data, buf.nbytes)
+        t0 = int(buf[:32, 0, 0][buf[:32, 0, 0] > 0].min())
+        for ev in STEP_TRACE_ORDER:
+            v = buf[:32, 0, ev] if ev < 8 else buf[32:, 0, ev]
+            v = v[v > 0].astype(np.int64)
+            if len(v):
+                d = (v - t0) / 100.0
+                stats[ev].append((d.min(), np.median(d), d.max(), len(v)))
+    step.check()
+    rows = []
+    for ev in STEP_TRACE_ORDER:
+        if stats[ev]:
+            a = np.array(stats[ev])
+            rows.append({"event": STEP_TRACE_EVENTS[ev], "workgroups": int(a[0, 3]),
+                         "min_us": round(float(np.median(a[:, 0])), 2), "median_us": round(float(np.median(a[:, 1])), 2),
+                         "max_us": round(float(np.median(a[:, 2])), 2)})
+    return rows
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -655,6 +712,12 @@ def main():
     from bitnet_tt.config import BitNet2B4TConfig
     from bitnet_tt.decode import BitLinearDecodeStep
 
+    if args.step_trace:
+        from bitnet_tt import _build
+
+        if not os.path.exists(_build.OUT_TRACE):
+            raise SystemExit(f"{_build.OUT_TRACE} is not built: python bitnet-tt_amd/bitnet_tt/_build.py --trace")
+        N.LIB_PATH = _build.OUT_TRACE
     N.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -670,6 +733,12 @@ def main():
 
     if args.pmc_pass:
         pmc_pass(step, torch)
+        return
+    if args.step_trace:
+        rows = step_trace(step, torch, N)
+        print(f"{'event (layer 10)':36s} {'WGs':>4s} {'min':>7s} {'median':>7s} {'max':>7s}  (us)")
+        for r in rows:
+            print(f"{r['event']:36s} {r['workgroups']:4d} {r['min_us']:7.2f} {r['median_us']:7.2f} {r['max_us']:7.2f}")
         return
 
     s = torch.cuda.Stream(device=dev)

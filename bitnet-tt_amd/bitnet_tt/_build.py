@@ -17,6 +17,9 @@ _REPO = os.path.dirname(_ROOT)
 CSRC = os.path.join(_ROOT, "csrc")
 INCLUDE = os.path.join(_REPO, "include")
 OUT = os.path.join(_PKG, "_lib", "libbtl.so")
+# Measurement build: the same sources with -DBTL_TRACE (phase timestamps of the
+# persistent decode step, read by bench.py --step-trace).  Not loaded otherwise.
+OUT_TRACE = os.path.join(_PKG, "_lib", "libbtl_trace.so")
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -43,13 +46,16 @@ def hipcc() -> str:
     return "hipcc"
 
 
-def build_native(verbose: bool = False) -> str:
+def build_native(verbose: bool = False, trace: bool = False) -> str:
+    """Compile libbtl.so (trace=True: the -DBTL_TRACE measurement build,
+    libbtl_trace.so)."""
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    os.makedirs(os.path.dirname(OUT), exist_ok=True)
-    tmp = OUT + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-o", tmp, *sources]
+    out = OUT_TRACE if trace else OUT
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    tmp = out + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, *(["-DBTL_TRACE"] if trace else []), f"-I{INCLUDE}", "-o", tmp, *sources]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     errs = "\n".join(ln for ln in proc.stderr.splitlines() if noise not in ln)
@@ -57,9 +63,11 @@ def build_native(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{' '.join(cmd)}\n{errs}")
     if verbose and errs.strip():
         print(errs)
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build_native(verbose=True))
+    import sys
+
+    print(build_native(verbose=True, trace="--trace" in sys.argv[1:]))
