@@ -224,24 +224,63 @@ __device__ __forceinline__ float row_rms_inv(const float (&v)[CPT][8], int nch, 
   return 1.0f / sqrtf(var + eps);
 }
 
-// y = bf16(gamma * bf16(x * r)) (or bf16(x * r) without gamma), in place.
+// The two bf16 halves of a word as floats.
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// A row's gains, bf16 pairs as loaded, as floats.
 template <int CPT>
-__device__ __forceinline__ void row_apply_norm(float (&v)[CPT][8], const uint4 (&graw)[CPT], bool has_gamma,
-                                               float r, int nch, int tid) {
+__device__ __forceinline__ void gains_to_floats(const uint4 (&graw)[CPT], float (&g)[CPT][8]) {
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const uint32_t g4[4] = {graw[i].x, graw[i].y, graw[i].z, graw[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      g[i][2 * j] = bf_lo(g4[j]);
+      g[i][2 * j + 1] = bf_hi(g4[j]);
+    }
+  }
+}
+
+// y = bf16(g * bf16(x * r)), in place, with the gains as floats.  Each
+// v_cvt_pk_bf16_f32 rounds two values, each exactly as f2bf.
+template <int CPT>
+__device__ __forceinline__ void row_apply_norm_f(float (&v)[CPT][8], const float (&g)[CPT][8], float r, int nch,
+                                                 int tid) {
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int c = tid + kActThreads * i;
     if (tid < kActThreads && c < nch) {
-      const uint32_t g4[4] = {graw[i].x, graw[i].y, graw[i].z, graw[i].w};
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float t = bf2f(f2bf(v[i][j] * r));
-        if (has_gamma) {
-          const float g = bf2f((uint16_t)((j & 1) ? (g4[j >> 1] >> 16) : (g4[j >> 1] & 0xffffu)));
-          v[i][j] = bf2f(f2bf(g * t));
-        } else {
-          v[i][j] = t;
-        }
+      for (int j = 0; j < 8; j += 2) {
+        const uint32_t t = f2bf_pair(v[i][j] * r, v[i][j + 1] * r);
+        const uint32_t y = f2bf_pair(g[i][j] * bf_lo(t), g[i][j + 1] * bf_hi(t));
+        v[i][j] = bf_lo(y);
+        v[i][j + 1] = bf_hi(y);
+      }
+    }
+  }
+}
+
+// y = bf16(gamma * bf16(x * r)) (or bf16(x * r) without gamma), in place.
+template <int CPT>
+__device__ __forceinline__ void row_apply_norm(float (&v)[CPT][8], const uint4 (&graw)[CPT], bool has_gamma,
+                                               float r, int nch, int tid) {
+  if (has_gamma) {
+    float g[CPT][8];
+    gains_to_floats<CPT>(graw, g);
+    row_apply_norm_f<CPT>(v, g, r, nch, tid);
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = tid + kActThreads * i;
+    if (tid < kActThreads && c < nch) {
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        const uint32_t t = f2bf_pair(v[i][j] * r, v[i][j + 1] * r);
+        v[i][j] = bf_lo(t);
+        v[i][j + 1] = bf_hi(t);
       }
     }
   }
@@ -269,22 +308,28 @@ __device__ __forceinline__ float row_absmax(const float (&v)[CPT][8], int nch, f
   return a > act_eps ? a : act_eps;
 }
 
-// Eight quantised values packed little-endian into two words; rs += their sum.
+// Eight quantised values q = clip(rne(v * scale), -128, 127) packed
+// little-endian into two words; rs += their sum.  Every caller passes
+// scale = 127/a with a >= max|v| over the row (a = max(max|v|, 1e-5)), so
+// |fl(v * scale)| <= 127 (1 + 2^-24)^2 < 127.5 for finite v and the clip never
+// binds.  For |t| < 2^22, fl(t + 1.5 * 2^23) is 1.5 * 2^23 + rne(t) (ties to
+// even, as rintf), whose bit pattern is 0x4B400000 + rne(t): its low byte is
+// the two's complement int8 code.  v_perm_b32 gathers the four low bytes of a
+// word, and v_dot4 against 0x01010101 sums its four signed bytes.
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+  return __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u) | __builtin_amdgcn_perm(b3, b2, 0x04000c0cu);
+}
 __device__ __forceinline__ void quant8(const float (&v)[8], float scale, uint32_t& lo, uint32_t& hi, int& rs) {
-  lo = 0u;
-  hi = 0u;
+  uint32_t b[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    float t = rintf(v[j] * scale);
-    t = fminf(fmaxf(t, -128.0f), 127.0f);
-    const int qi = (int)t;
-    rs += qi;
-    const uint32_t b = (uint32_t)(qi & 0xff);
-    if (j < 4)
-      lo |= b << (8 * j);
-    else
-      hi |= b << (8 * (j - 4));
+    const float t = v[j] * scale;
+    b[j] = __float_as_uint(t + 12582912.0f);
   }
+  lo = pack_low_bytes(b[0], b[1], b[2], b[3]);
+  hi = pack_low_bytes(b[4], b[5], b[6], b[7]);
+  rs = __builtin_amdgcn_sdot4((int)lo, 0x01010101, rs, false);
+  rs = __builtin_amdgcn_sdot4((int)hi, 0x01010101, rs, false);
 }
 
 // Row m of the activation prologue.  Threads 0..255 do the work; any further

@@ -244,18 +244,22 @@ __device__ void wait_row_words(const StepArgs& p, const uint64_t* row, int ncols
   }
 }
 
+// The row's gains as floats, loaded and converted before the wait for the
+// stage's inputs, so the conversion is off the row's critical path.
 template <int C>
-__device__ __forceinline__ void load_gain(const uint16_t* gamma, int nch, uint4 (&g)[C]) {
+__device__ __forceinline__ void load_gain(const uint16_t* gamma, int nch, float (&g)[C][8]) {
   const int tid = threadIdx.x;
+  uint4 raw[C];
 #pragma unroll
   for (int i = 0; i < C; ++i) {
     const int c = tid + kActThreads * i;
-    g[i] = make_uint4(0u, 0u, 0u, 0u);
+    raw[i] = make_uint4(0u, 0u, 0u, 0u);
     if (c < nch) {
       const v4i t = ldg128(gamma + 8 * c);
-      g[i] = make_uint4((uint32_t)t.x, (uint32_t)t.y, (uint32_t)t.z, (uint32_t)t.w);
+      raw[i] = make_uint4((uint32_t)t.x, (uint32_t)t.y, (uint32_t)t.z, (uint32_t)t.w);
     }
   }
+  gains_to_floats<C>(raw, g);
 }
 
 template <int C>
@@ -279,7 +283,7 @@ struct RowStats {
 // sum.  Rows m >= M publish zeros.  The same row code as btl_bitlinear_fused.
 template <int C>
 __device__ RowStats publish_row(const StepArgs& p, int l, int j, int m, int K, int KS, float (&v)[C][8],
-                                const uint4 (&g)[C], uint32_t want, float* s_sum, float* s_max, int* s_rs) {
+                                const float (&g)[C][8], uint32_t want, float* s_sum, float* s_max, int* s_rs) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nch = K >> 3, nchp = KS * 16;
   int8_t* xa = tile_of(p, l, j);
@@ -288,7 +292,7 @@ __device__ RowStats publish_row(const StepArgs& p, int l, int j, int m, int K, i
   int rs = 0;
   if (m < p.M) {
     const float r = row_rms_inv<C>(v, nch, K, p.eps, tid, s_sum);
-    row_apply_norm<C>(v, g, true, r, nch, tid);
+    row_apply_norm_f<C>(v, g, r, nch, tid);
     const float a = row_absmax<C>(v, nch, 1e-5f, tid, s_max);
     const float scale = 127.0f / a;
     st.adq = a / 127.0f;
@@ -328,9 +332,8 @@ __device__ RowStats publish_row(const StepArgs& p, int l, int j, int m, int K, i
 __device__ __forceinline__ void residual_add(uint32_t (&hid)[4], const uint32_t (&o)[4], bool live) {
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const uint32_t lo = f2bf(bf2f((uint16_t)(hid[k] & 0xffffu)) + bf2f((uint16_t)(o[k] & 0xffffu)));
-    const uint32_t hi = f2bf(bf2f((uint16_t)(hid[k] >> 16)) + bf2f((uint16_t)(o[k] >> 16)));
-    hid[k] = live ? (lo | (hi << 16)) : 0u;
+    const uint32_t s = f2bf_pair(bf_lo(hid[k]) + bf_lo(o[k]), bf_hi(hid[k]) + bf_hi(o[k]));
+    hid[k] = live ? s : 0u;
   }
 }
 
@@ -354,24 +357,21 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
     hid[0][3] = raw.w;
   }
   // gains of the next QKV stage: loaded ahead, during the wait before it
-  uint4 g_qkv[CH];
+  float g_qkv[CH][8];
   load_gain<CH>(sops[S_QKV].gamma, nh, g_qkv);
   for (int l = 0; l < p.L; ++l) {
     const StepOp* ops = sops + l * kStepOps;
     // ---- QKV: RMSNorm(h; input_layernorm)
     {
       float v[CH][8];
-      uint4 g[CH];
-#pragma unroll
-      for (int i = 0; i < CH; ++i) g[i] = g_qkv[i];
       pairs_to_floats<CH>(hid, v);
       STEP_TRACE(l, 0);
-      publish_row<CH>(p, l, S_QKV, m, p.H, p.KSH, v, g, step_tag(E, l, S_QKV), s_sum, s_max, s_rs);
+      publish_row<CH>(p, l, S_QKV, m, p.H, p.KSH, v, g_qkv, step_tag(E, l, S_QKV), s_sum, s_max, s_rs);
       STEP_TRACE(l, 1);
     }
     // ---- O: the user's QKV row, then RMSNorm(attn; attn_sub_norm)
     {
-      uint4 g[CH];
+      float g[CH][8];
       load_gain<CH>(ops[S_O].gamma, nh, g);
       // the attention output row: an input of the step, loaded before the wait
       uint4 raw = make_uint4(0u, 0u, 0u, 0u);
@@ -390,7 +390,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
     }
     // ---- GU: h = bf16(h + o); RMSNorm(h; post_attention_layernorm)
     {
-      uint4 g[CH];
+      float g[CH][8];
       load_gain<CH>(ops[S_GU].gamma, nh, g);
       uint32_t pr[CH][4];
       wait_row_words<CH>(p, out_of(p, l, S_O) + (int64_t)m * (p.H >> 1), p.H, step_tag(E, l, S_O), pr, ws);
@@ -403,7 +403,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
     }
     // ---- DN: RMSNorm(relu(g)^2 * u; ffn_sub_norm)
     {
-      uint4 g[CF];
+      float g[CF][8];
       load_gain<CF>(ops[S_DN].gamma, nf, g);
       uint32_t pr[CF][4];
       wait_row_words<CF>(p, out_of(p, l, S_GU) + (int64_t)m * (p.F >> 1), p.F, step_tag(E, l, S_GU), pr, ws);
