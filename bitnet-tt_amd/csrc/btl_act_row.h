@@ -165,15 +165,6 @@ __device__ __forceinline__ float wave_xor_sum(float s) {
   s = s + xor_partner<1>(s);
   return s;
 }
-__device__ __forceinline__ float wave_xor_max(float m) {
-  m = fmaxf(m, xor_partner<32>(m));
-  m = fmaxf(m, xor_partner<16>(m));
-  m = fmaxf(m, xor_partner<8>(m));
-  m = fmaxf(m, xor_partner<4>(m));
-  m = fmaxf(m, xor_partner<2>(m));
-  m = fmaxf(m, xor_partner<1>(m));
-  return m;
-}
 
 template <bool COHERENT>
 __device__ __forceinline__ void store8(int8_t* p, uint32_t lo, uint32_t hi) {
@@ -286,7 +277,10 @@ __device__ __forceinline__ void row_apply_norm(float (&v)[CPT][8], const uint4 (
   }
 }
 
-// a = max(max|v|, act_eps) over the row (one barrier).
+// a = max(max|v|, act_eps) over the row (one barrier).  Past the thread's own
+// elements the maxima are taken on the bit patterns: for non-negative floats
+// the unsigned order is the float order, and integer max needs none of the
+// NaN canonicalisation fmaxf adds to every step.
 template <int CPT>
 __device__ __forceinline__ float row_absmax(const float (&v)[CPT][8], int nch, float act_eps, int tid,
                                             float* s_max) {
@@ -299,12 +293,20 @@ __device__ __forceinline__ float row_absmax(const float (&v)[CPT][8], int nch, f
 #pragma unroll
       for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[i][j]));
     }
-  amax = wave_xor_max(amax);
-  if (active && lane == 0) s_max[wv] = amax;
+  uint32_t u = __float_as_uint(amax);
+  u = max(u, xor_partner_u<32>(u));
+  u = max(u, xor_partner_u<16>(u));
+  u = max(u, xor_partner_u<8>(u));
+  u = max(u, xor_partner_u<4>(u));
+  u = max(u, xor_partner_u<2>(u));
+  u = max(u, xor_partner_u<1>(u));
+  uint32_t* s_maxu = reinterpret_cast<uint32_t*>(s_max);
+  if (active && lane == 0) s_maxu[wv] = u;
   __syncthreads();
-  float a = s_max[0];
+  uint32_t m = s_maxu[0];
 #pragma unroll
-  for (int w = 1; w < kActWaves; ++w) a = fmaxf(a, s_max[w]);
+  for (int w = 1; w < kActWaves; ++w) m = max(m, s_maxu[w]);
+  const float a = __uint_as_float(m);
   return a > act_eps ? a : act_eps;
 }
 

@@ -193,22 +193,46 @@ __device__ __forceinline__ bool should_stop(const StepArgs& p, unsigned n, WaitS
 // ------------------------------------------------------------------ rows ----
 // Chunk c = tid + 512 i of a row holds its elements 8c .. 8c + 7.
 
-// Waits for the tagged bf16-pair words of row m of an output with `ncols`
-// columns and returns this thread's chunks as bf16 pairs (pr[i][0..3]).  Each
-// thread polls its own words and re-reads only the ones whose tag is not
-// there yet.
 // Sleep between two polls of a bounded wait (s_sleep units of 64 clocks).
 #ifndef BTL_STEP_POLL_SLEEP
 #define BTL_STEP_POLL_SLEEP 1
 #endif
 
+// One poll round: this thread's words, all of them, unconditionally (a chunk
+// past the row's end reads the last chunk, and nothing takes it).  Loads under
+// per-word lane masks would let the register allocator reuse a destination
+// before the round ends, and the wait that reuse needs would split the round
+// into several memory round trips.
+template <int C>
+__device__ __forceinline__ void issue_words(const uint64_t* row, int nch, uint64_t (&d)[C][4]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    const int c = min(tid + kActThreads * i, nch - 1);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) d[i][k] = ld_coherent(row + 4 * c + k);
+  }
+}
+// Takes the words of a round (issued for `pend`) that carry the tag.
+template <int C>
+__device__ __forceinline__ void take_words(const uint64_t (&d)[C][4], unsigned pend, uint32_t want, unsigned& pending,
+                                           uint32_t (&pr)[C][4]) {
+#pragma unroll
+  for (int i = 0; i < C; ++i)
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if ((pend & pending & (1u << (4 * i + k))) && (uint32_t)(d[i][k] >> 32) == want) {
+        pr[i][k] = (uint32_t)d[i][k];
+        pending &= ~(1u << (4 * i + k));
+      }
+}
+
 // Waits for the tagged bf16-pair words of row m of an output with `ncols`
 // columns and returns this thread's chunks as bf16 pairs (pr[i][0..3]).  Each
-// thread polls its own words and re-reads only the ones whose tag is not
-// there yet.  Every load of a round is issued before the first tag is
-// checked (a check between two loads would make each wait for the one
-// before); one round is in flight at a time (more polling traffic slows the
-// stores being waited for more than it speeds up their detection).
+// thread polls its own words until each has shown the tag.  One round is in
+// flight at a time (a second round in flight doubles the polling traffic, which
+// slows the stores being waited for more than it speeds up their detection);
+// every load of a round is issued before any tag of it is checked.
 template <int C>
 __device__ void wait_row_words(const StepArgs& p, const uint64_t* row, int ncols, uint32_t want, uint32_t (&pr)[C][4],
                                WaitState& ws) {
@@ -221,31 +245,18 @@ __device__ void wait_row_words(const StepArgs& p, const uint64_t* row, int ncols
     for (int k = 0; k < 4; ++k) pr[i][k] = 0u;
     if (tid + kActThreads * i < nch) pending |= 0xFu << (4 * i);
   }
+  if (!pending || ws.dead) return;
   unsigned n = 0;
-  while (pending && !ws.dead) {
+  while (true) {
     uint64_t d[C][4];
     const unsigned pend = pending;
-#pragma unroll
-    for (int i = 0; i < C; ++i)
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        d[i][k] = (pend & (1u << (4 * i + k))) ? ld_coherent(row + 4 * (tid + kActThreads * i) + k) : 0;
-#pragma unroll
-    for (int i = 0; i < C; ++i)
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if ((pend & (1u << (4 * i + k))) && (uint32_t)(d[i][k] >> 32) == want) {
-          pr[i][k] = (uint32_t)d[i][k];
-          pending &= ~(1u << (4 * i + k));
-        }
-    if (!pending) break;
-    if (should_stop(p, ++n, ws)) break;
+    issue_words<C>(row, nch, d);
+    take_words<C>(d, pend, want, pending, pr);
+    if (!pending || should_stop(p, ++n, ws)) break;
     __builtin_amdgcn_s_sleep(BTL_STEP_POLL_SLEEP);
   }
 }
 
-// The row's gains as floats, loaded and converted before the wait for the
-// stage's inputs, so the conversion is off the row's critical path.
 template <int C>
 __device__ __forceinline__ void load_gain(const uint16_t* gamma, int nch, float (&g)[C][8]) {
   const int tid = threadIdx.x;
