@@ -564,6 +564,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     // C: lane l, element j is row 4 (l >> 4) + j, column l & 15.
     const int er = tid >> 5, ec = tid & 31;
     const int row = 16 * h + er;
+    const float sc = op_seg_scale(op, tile0 * 32 + ec);  // LDS reads, early: off the epilogue's path
     const float ad = ld_coherent(adq + row);
     const int a_lane = 16 * h + (lane & 15) + 32 * ((lane >> 4) & 1);
     const int a_step = lane >> 5;
@@ -597,11 +598,15 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     for (int v2 = 0; v2 < kStepWaves; ++v2) sum += red[(v2 * 8 + reg) * 64 + src];
     lds_barrier();  // LDS free for the next BitLinear
     const int n = tile0 * 32 + ec;
-    const uint32_t o = f2bf((float)sum * (op_seg_scale(op, n) * ad));
-    const uint32_t pair = o | ((uint32_t)__shfl_down((int)o, 1, 64) << 16);  // lanes ec, ec+1 share the row
+    const uint32_t o = f2bf((float)sum * (sc * ad));
+    const uint32_t pair = o | (xor_partner_u<1>(o) << 16);  // lanes ec, ec+1 share the row (a DPP swap)
     if ((ec & 1) == 0) st_coherent(outw + (int64_t)row * (n_out >> 1) + (n >> 1), ((uint64_t)want << 32) | pair);
   } else {
     // ---- all 32 rows on v_mfma_i32_32x32x32_i8 ----
+    const int jc = lane & 31;
+    // segment scales: LDS reads of the op table, issued early, off the epilogue's path
+    const float sc0 = op_seg_scale(op, tile0 * 32 + jc);
+    const float sc1 = MODE == MODE_SCALE ? sc0 : op_seg_scale(op, unit_tile<J>(p, tile0, 1) * 32 + jc);
     float ad_r[2];
     int32_t rs_r[2];
 #pragma unroll
@@ -652,23 +657,21 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     // stores under lane masks the compiler would otherwise wait for all of
     // them, coherent write acknowledgements included, before the second row.
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    const int jc = lane & 31;
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
       const int i = acc_row(wv + kStepWaves * rr, lane);
       const int n = tile0 * 32 + jc;
       uint32_t o;
       if (MODE == MODE_SCALE) {
-        o = f2bf((float)v[0][rr] * (op_seg_scale(op, n) * ad_r[rr]));
+        o = f2bf((float)v[0][rr] * (sc0 * ad_r[rr]));
       } else {
-        const int nu = unit_tile<J>(p, tile0, 1) * 32 + jc;
-        const float gg = bf2f(f2bf((float)v[0][rr] * (op_seg_scale(op, n) * ad_r[rr])));
-        const float uu = bf2f(f2bf((float)v[TPW - 1][rr] * (op_seg_scale(op, nu) * ad_r[rr])));
+        const float gg = bf2f(f2bf((float)v[0][rr] * (sc0 * ad_r[rr])));
+        const float uu = bf2f(f2bf((float)v[TPW - 1][rr] * (sc1 * ad_r[rr])));
         const float gr = gg > 0.0f ? gg : 0.0f;
         const float sq = bf2f(f2bf(gr * gr));
         o = f2bf(sq * uu);
       }
-      const uint32_t pair = o | ((uint32_t)__shfl_down((int)o, 1, 64) << 16);  // lanes jc, jc+1 share the row
+      const uint32_t pair = o | (xor_partner_u<1>(o) << 16);  // lanes jc, jc+1 share the row (a DPP swap)
       if ((jc & 1) == 0) st_coherent(outw + (int64_t)i * (n_out >> 1) + (n >> 1), ((uint64_t)want << 32) | pair);
       if (J == S_QKV && i < p.M) p.qkv_out[(int64_t)i * p.NQKV + n] = (uint16_t)o;
       if (J == S_GU && i < p.M) p.ffn_h[(int64_t)i * p.F + n] = (uint16_t)o;
