@@ -218,8 +218,18 @@ _error_words: dict = {}
 _prepared_for: dict = {}
 
 
+# Host-side set-up to redo after a workspace has been zero-filled by
+# check_errors (data_ptr -> callable), for workspaces whose start state is not
+# all zeros (the decode step's weight table and operand tiles).
+_reset_hooks: dict = {}
+
+
 def workspace_prepared_for(buf):
     return _prepared_for.get(buf.data_ptr())
+
+
+def set_workspace_reset(buf, fn) -> None:
+    _reset_hooks[buf.data_ptr()] = fn
 
 
 def set_workspace_prepared_for(buf, owner) -> None:
@@ -252,9 +262,11 @@ def workspace(device, nbytes: int, kind: str = "bitlinear", error_offset: int | 
     if buf is None or buf.numel() < nbytes:
         if buf is not None:
             _prepared_for.pop(buf.data_ptr(), None)
+            _reset_hooks.pop(buf.data_ptr(), None)
         size = max(int(nbytes), 1 << 20)
         buf = torch.zeros(size, dtype=torch.uint8, device=device)
         _prepared_for.pop(buf.data_ptr(), None)
+        _reset_hooks.pop(buf.data_ptr(), None)
         _workspaces[key] = buf
     if error_offset is not None:
         _error_words.setdefault(key, set()).add(int(error_offset))
@@ -270,9 +282,11 @@ def check_errors(device=None) -> None:
     workspace and the kernel finishes with invalid outputs.  This reads every
     registered error word of the device's workspaces (all streams) after a
     device synchronisation.  When one is set, the affected workspaces are
-    zero-filled in place (the start state of their launch counters, so later
-    calls and graphs captured on them work again) and RuntimeError names
-    them: the outputs of the calls since the last check are not valid."""
+    zero-filled in place (the start state of their launch counters) and the
+    host-side set-up registered for them (set_workspace_reset: the decode
+    step's weight table and operand tiles) is redone, so later calls and
+    graphs captured on them work again; RuntimeError names them: the outputs
+    of the calls since the last check are not valid."""
     import torch
 
     dev = _device_key(device if device is not None else "cuda")
@@ -291,7 +305,12 @@ def check_errors(device=None) -> None:
         return
     for key in {b[0] for b in bad}:
         _workspaces[key].zero_()
-        _prepared_for.pop(_workspaces[key].data_ptr(), None)
+        torch.cuda.synchronize(dev)
+        hook = _reset_hooks.get(_workspaces[key].data_ptr())
+        if hook is not None:
+            hook()
+        else:
+            _prepared_for.pop(_workspaces[key].data_ptr(), None)
     torch.cuda.synchronize(dev)
     what = ", ".join(f"{k[0]} workspace (stream {k[2]:#x}) word at byte {off} = {w}" for k, off, w in bad)
     raise RuntimeError(

@@ -438,9 +438,14 @@ class BitLinearDecodeStep:
             if capturing:
                 raise RuntimeError("run one eager decode step on this stream before capturing it in a graph")
             torch.cuda.current_stream(dev).synchronize()  # earlier launches on this workspace are done
-            N.check(L.btl_decode_step_prepare(B, H, F, c.qkv_dim, nl, table, N.ptr(ws), ws.numel()),
-                    "btl_decode_step_prepare")
-            N.set_workspace_prepared_for(ws, table)
+
+            def prepare():
+                N.check(L.btl_decode_step_prepare(B, H, F, c.qkv_dim, nl, table, N.ptr(ws), ws.numel()),
+                        "btl_decode_step_prepare")
+                N.set_workspace_prepared_for(ws, table)
+
+            prepare()
+            N.set_workspace_reset(ws, prepare)
         N.check(
             L.btl_decode_step(B, H, F, c.qkv_dim, nl, float(self.eps), N.ptr(self.attn_out), N.ptr(self.hidden),
                               N.ptr(self.qkv_out), N.ptr(self.ffn_h), N.ptr(ws), ws.numel(), N.stream_of(dev)),

@@ -29,10 +29,14 @@
 // launches.
 //
 // Hand-offs (every one crosses XCDs; a coherent hop costs ~0.45 us each way):
-//   row -> GEMM: the row's int8 operand bytes and a/127 with device-coherent
-//     stores, a wait for their acknowledgement, then the row's flag; a GEMM
-//     unit polls the flags of its 16 (or 32) rows and reads the tile with
-//     plain loads (each tile is written once per launch, before its flags).
+//   row -> GEMM: the row's int8 operand bytes with device-coherent 8-byte
+//     stores, then, without waiting for their acknowledgement, the row's flag
+//     (two tagged words: the row's sum of quantised values and a/127).  A
+//     GEMM unit polls the flags of its 16 (or 32) rows, then reads its operand
+//     tile with L1-bypassing loads and checks it: between two uses every row
+//     overwrites its slice of a tile with the sentinel byte 0x80, which no
+//     quantised value takes (|q| <= 127), so operand bytes that have not landed
+//     yet are recognised and read again.
 //   GEMM -> row: 8-byte words holding two bf16 outputs and a 32-bit tag, each
 //     one device-coherent store; the row workgroup polls the words it needs
 //     (the data is its own flag: no acknowledgement wait, no flag hop).
@@ -59,14 +63,30 @@ constexpr int kStepMaxGrid = 1024;
 constexpr int kStepWSlots = 7;      // weight registers (16 B each) per wave and buffer
 enum { S_QKV = 0, S_O = 1, S_GU = 2, S_DN = 3, kStepOps = 4 };
 
-// Workspace: header, op table, then one hand-off region (operand tiles, a/127,
-// row flags, tagged output words) that every layer reuses.  Reuse is safe by
-// the dependency chain: row m overwrites its slice of (layer l+1, BitLinear j)
-// only after it has received all of its outputs of (l, j) -- and every unit
-// that reads row m's slice of tile (l, j) or polls its flag writes row m's
-// outputs of (l, j) only after those reads -- and a GEMM unit overwrites the
-// tagged words of (l+1, j) only after every row it covers has published
+// Workspace: header, op table, then one hand-off region (operand tiles, row
+// flags, tagged output words) that every layer reuses.  Reuse is safe by the
+// dependency chain: row m clears (sentinel) and later overwrites its slice of
+// tile j only after it has received all of its outputs of (l, j) -- and every
+// unit that reads row m's slice of tile (l, j) or polls its flag writes row
+// m's outputs of (l, j) only after those reads -- and a GEMM unit overwrites
+// the tagged words of (l+1, j) only after every row it covers has published
 // (l+1, j), which each row does after reading its words of (l, j).
+//
+// Operand tiles between uses.  Row m writes its slice of tile j for (l, j)
+// (8-byte coherent stores, no acknowledgement wait).  Right after publishing
+// (l, j + 1), when it has all of its outputs of (l, j), it clears a share of
+// tile j to the sentinel in whole lines: any 1/32 of a tile whose units all
+// cover the 32 rows (every unit has then read the whole tile), 1/16 of its
+// half's lines of a tile of 16-row units.  Every row stage starts with a wait
+// for all of the row's earlier memory operations (microseconds old by then,
+// so it costs nothing), so a clear is performed before the row publishes
+// anything later, and every row's next flag of tile j causally follows the
+// publications of every row (through the 32-row units in between).  A unit
+// that has seen the flags of (l + 1, j) therefore reads, for every 8-byte
+// piece, either the sentinel or the new bytes, never bytes of (l, j); seeing
+// the sentinel it waits for the piece and reads again.  Tiles start
+// (btl_decode_step_prepare) and end (the last row stage clears the last tile)
+// every launch as the sentinel.
 constexpr int64_t kStEpoch = 0;          // [kStepMaxGrid] u32
 constexpr int64_t kStError = 4096;       // u32
 constexpr int64_t kStTable = 8192;       // StepOp[L][4]
@@ -120,9 +140,15 @@ struct StepArgs {
   uint32_t* epoch;
   uint32_t* error;
   char* layers;          // the hand-off region
-  int64_t off_xa[kStepOps], off_adq, off_flag, off_out[kStepOps];
+  int64_t off_xa[kStepOps], off_flag, off_out[kStepOps];
   unsigned spin_limit;
 };
+
+// Operand-tile byte between two uses: -128, which absmax quantisation never
+// produces.  A 16-bit lane of an operand dword holding quantised bytes is
+// >= -127 * 256 = -32512; one of a cleared 8-byte piece is 0x8080 = -32640.
+constexpr uint32_t kTileSentinel = 0x80808080u;
+constexpr int kTileSentinelMax16 = -32513;  // a 16-bit lane at or below this is the sentinel
 
 __device__ __forceinline__ uint32_t step_tag(uint32_t E, int l, int j) { return (E << 8) | (uint32_t)(l * 4 + j); }
 
@@ -139,11 +165,8 @@ __device__ __forceinline__ char* layer_base(const StepArgs& p, int) { return p.l
 __device__ __forceinline__ int8_t* tile_of(const StepArgs& p, int l, int j) {
   return reinterpret_cast<int8_t*>(layer_base(p, l) + p.off_xa[j]);
 }
-__device__ __forceinline__ float* adq_of(const StepArgs& p, int l, int j) {
-  return reinterpret_cast<float*>(layer_base(p, l) + p.off_adq) + j * 32;
-}
-// Row m's flag of (l, j), on its own 128-byte line: tag << 32 | the row's
-// sum of its quantised values.
+// Row m's flag of (l, j), on its own 128-byte line: word 0 = tag << 32 | the
+// row's sum of its quantised values, word 1 = tag << 32 | the bits of a/127.
 __device__ __forceinline__ uint64_t* flag_of(const StepArgs& p, int l, int j, int m) {
   return reinterpret_cast<uint64_t*>(layer_base(p, l) + p.off_flag) + (j * 32 + m) * 16;
 }
@@ -177,9 +200,18 @@ __device__ __forceinline__ float op_seg_scale(const StepOp& op, int n) {
 struct WaitState {
   bool dead;
 };
-__device__ __forceinline__ bool should_stop(const StepArgs& p, unsigned n, WaitState& ws) {
+// The error word names the first wait that ran out: kind (1 row words, 2 row
+// flags, 3 operand tile) | (layer*4 + BitLinear) << 8 | workgroup << 16.
+enum { WAIT_WORDS = 1, WAIT_FLAGS = 2, WAIT_TILE = 3 };
+__device__ __forceinline__ void set_error_word(const StepArgs& p, int kind, uint32_t want) {
+  uint32_t expected = 0u;
+  const uint32_t code = (uint32_t)kind | ((want & 0xffu) << 8) | (blockIdx.x << 16);
+  __hip_atomic_compare_exchange_strong(p.error, &expected, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool should_stop(const StepArgs& p, unsigned n, WaitState& ws, int kind, uint32_t want) {
   if (n > p.spin_limit) {
-    st_coherent(p.error, 1u);
+    set_error_word(p, kind, want);
     ws.dead = true;
     return true;
   }
@@ -252,7 +284,7 @@ __device__ void wait_row_words(const StepArgs& p, const uint64_t* row, int ncols
     const unsigned pend = pending;
     issue_words<C>(row, nch, d);
     take_words<C>(d, pend, want, pending, pr);
-    if (!pending || should_stop(p, ++n, ws)) break;
+    if (!pending || should_stop(p, ++n, ws, WAIT_WORDS, want)) break;
     __builtin_amdgcn_s_sleep(BTL_STEP_POLL_SLEEP);
   }
 }
@@ -284,43 +316,32 @@ __device__ __forceinline__ void pairs_to_floats(const uint32_t (&pr)[C][4], floa
     }
 }
 
-struct RowStats {
-  float adq;   // a/127
-  int32_t rs;  // sum of the row's quantised values
-};
-
-// RMSNorm with gain g, absmax int8 quantisation into the tile of (l, j), a/127,
-// then the row's flag (after the stores are acknowledged) carrying the row
-// sum.  Rows m >= M publish zeros.  The same row code as btl_bitlinear_fused.
+// RMSNorm with gain g, absmax int8 quantisation into the tile of (l, j), then
+// the row's flag (row sum and a/127), issued right behind the operand stores
+// with no wait for their acknowledgement (a GEMM unit checks the bytes it
+// reads against the sentinel).  Rows m >= M publish zeros.  The same row code
+// as btl_bitlinear_fused.  K is a multiple of 128 (checked on the host), so
+// the row's chunks fill its slice of the tile.
 template <int C>
-__device__ RowStats publish_row(const StepArgs& p, int l, int j, int m, int K, int KS, float (&v)[C][8],
-                                const float (&g)[C][8], uint32_t want, float* s_sum, float* s_max, int* s_rs) {
+__device__ void publish_row(const StepArgs& p, int l, int j, int m, int K, int KS, float (&v)[C][8],
+                            const float (&g)[C][8], uint32_t want, float* s_sum, float* s_max, int* s_rs) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int nch = K >> 3, nchp = KS * 16;
+  const int nch = K >> 3;
   int8_t* xa = tile_of(p, l, j);
-  float* adq = adq_of(p, l, j);
-  RowStats st{0.0f, 0};
+  float adq = 0.0f;
   int rs = 0;
+  uint32_t qlo[C], qhi[C];
+#pragma unroll
+  for (int i = 0; i < C; ++i) qlo[i] = qhi[i] = 0u;
   if (m < p.M) {
     const float r = row_rms_inv<C>(v, nch, K, p.eps, tid, s_sum);
     row_apply_norm_f<C>(v, g, r, nch, tid);
     const float a = row_absmax<C>(v, nch, 1e-5f, tid, s_max);
     const float scale = 127.0f / a;
-    st.adq = a / 127.0f;
-    if (tid == 0) st_coherent(adq + m, st.adq);
+    adq = a / 127.0f;
 #pragma unroll
-    for (int i = 0; i < C; ++i) {
-      const int c = tid + kActThreads * i;
-      if (c < nch) {
-        uint32_t lo, hi;
-        quant8(v[i], scale, lo, hi, rs);
-        store_chunk<true>(xa, m, c, KS, lo, hi);
-      }
-    }
-    for (int c = nch + tid; c < nchp; c += kActThreads) store8<true>(xa + xa_offset(m, 8 * c, KS), 0u, 0u);
-  } else {
-    for (int c = tid; c < nchp; c += kActThreads) store8<true>(xa + xa_offset(m, 8 * c, KS), 0u, 0u);
-    if (tid == 0) st_coherent(adq + m, 0.0f);
+    for (int i = 0; i < C; ++i)
+      if (tid + kActThreads * i < nch) quant8(v[i], scale, qlo[i], qhi[i], rs);
   }
   rs += (int)xor_partner_u<32>((uint32_t)rs);
   rs += (int)xor_partner_u<16>((uint32_t)rs);
@@ -329,12 +350,49 @@ __device__ RowStats publish_row(const StepArgs& p, int l, int j, int m, int K, i
   rs += (int)xor_partner_u<2>((uint32_t)rs);
   rs += (int)xor_partner_u<1>((uint32_t)rs);
   if (lane == 0) s_rs[wv] = rs;
-  wait_memory();
-  __syncthreads();
+  // The operand bytes go out last: nothing after them in this stage reuses
+  // their registers or waits on the vector-memory counter.
 #pragma unroll
-  for (int w = 0; w < kActWaves; ++w) st.rs += s_rs[w];
-  if (tid == 0) st_coherent(flag_of(p, l, j, m), ((uint64_t)want << 32) | (uint32_t)st.rs);
-  return st;
+  for (int i = 0; i < C; ++i) {
+    const int c = tid + kActThreads * i;
+    if (c < nch) store_chunk<true>(xa, m, c, KS, qlo[i], qhi[i]);
+  }
+  lds_barrier();
+  if (tid == 0) {
+    int32_t tot = 0;
+#pragma unroll
+    for (int w = 0; w < kActWaves; ++w) tot += s_rs[w];
+    uint64_t* f = flag_of(p, l, j, m);
+    st_coherent(f, ((uint64_t)want << 32) | (uint32_t)tot);
+    st_coherent(f + 1, ((uint64_t)want << 32) | __float_as_uint(adq));
+  }
+}
+
+// Row m's share of a tile back to the sentinel, in whole 128-byte lines (a
+// wave's store instruction writes four full lines).  When every unit of the
+// tile covers all 32 rows, any row that has all of its outputs knows that the
+// whole tile has been read, and the tile is split into 32 contiguous shares.
+// A tile of 16-row units (half) is split among the 16 rows of each half, over
+// the lines that hold only that half's operand bytes: in each 1 KiB k-step
+// block, lines 0, 1, 4, 5 (rows 0-15) and 2, 3, 6, 7 (rows 16-31).  Row m's
+// share is KS lines (KS * 16 8-byte pieces; CP pieces per thread cover it).
+template <int CP>
+__device__ __forceinline__ void clear_tile_share(int8_t* xa, int m, int KS, bool half) {
+  const int tid = threadIdx.x, npieces = KS * 16;
+#pragma unroll
+  for (int i = 0; i < CP; ++i) {
+    const int pc = tid + kActThreads * i;
+    if (pc < npieces) {
+      int64_t off;
+      if (!half) {
+        off = (int64_t)m * KS * 128 + pc * 8;
+      } else {
+        const int li = (m & 15) * KS + (pc >> 4), sub = li & 3;
+        off = (int64_t)(li >> 2) * 1024 + ((sub & 1) + ((sub >> 1) << 2) + 2 * (m >> 4)) * 128 + (pc & 15) * 8;
+      }
+      st_coherent(reinterpret_cast<uint64_t*>(xa + off), ((uint64_t)kTileSentinel << 32) | kTileSentinel);
+    }
+  }
 }
 
 // h = bf16(h + o) for this thread's chunk (one chunk per thread), o the
@@ -349,7 +407,10 @@ __device__ __forceinline__ void residual_add(uint32_t (&hid)[4], const uint32_t 
 }
 
 // CF: chunks per thread of a row of F (a row of H, and of the QKV output,
-// is one chunk per thread: H, NQKV <= 4096).
+// is one chunk per thread: H, NQKV <= 4096).  Each stage: wait for the row's
+// words of the previous BitLinear, then for every earlier memory operation of
+// this thread (the last tile clear among them), publish, then clear the
+// previous BitLinear's tile slice, whose readers are all done.
 template <int CF>
 __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t E, float* s_sum, float* s_max,
                          int* s_rs) {
@@ -379,6 +440,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       STEP_TRACE(l, 0);
       publish_row<CH>(p, l, S_QKV, m, p.H, p.KSH, v, g_qkv, step_tag(E, l, S_QKV), s_sum, s_max, s_rs);
       STEP_TRACE(l, 1);
+      if (l > 0) clear_tile_share<CF>(tile_of(p, l - 1, S_DN), m, p.KSF, true);
     }
     // ---- O: the user's QKV row, then RMSNorm(attn; attn_sub_norm)
     {
@@ -389,6 +451,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       if (live && tid < nh) raw = *reinterpret_cast<const uint4*>(p.attn + (int64_t)m * p.H + 8 * tid);
       uint32_t pr[CH][4];
       wait_row_words<CH>(p, out_of(p, l, S_QKV) + (int64_t)m * (p.NQKV >> 1), p.NQKV, step_tag(E, l, S_QKV), pr, ws);
+      wait_memory();
       STEP_TRACE(l, 2);
       pr[0][0] = raw.x;
       pr[0][1] = raw.y;
@@ -398,6 +461,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       pairs_to_floats<CH>(pr, v);
       publish_row<CH>(p, l, S_O, m, p.H, p.KSH, v, g, step_tag(E, l, S_O), s_sum, s_max, s_rs);
       STEP_TRACE(l, 3);
+      clear_tile_share<CH>(tile_of(p, l, S_QKV), m, p.KSH, false);
     }
     // ---- GU: h = bf16(h + o); RMSNorm(h; post_attention_layernorm)
     {
@@ -405,12 +469,14 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       load_gain<CH>(ops[S_GU].gamma, nh, g);
       uint32_t pr[CH][4];
       wait_row_words<CH>(p, out_of(p, l, S_O) + (int64_t)m * (p.H >> 1), p.H, step_tag(E, l, S_O), pr, ws);
+      wait_memory();
       STEP_TRACE(l, 4);
       residual_add(hid[0], pr[0], live);
       float v[CH][8];
       pairs_to_floats<CH>(hid, v);
       publish_row<CH>(p, l, S_GU, m, p.H, p.KSH, v, g, step_tag(E, l, S_GU), s_sum, s_max, s_rs);
       STEP_TRACE(l, 5);
+      clear_tile_share<CH>(tile_of(p, l, S_O), m, p.KSH, false);
     }
     // ---- DN: RMSNorm(relu(g)^2 * u; ffn_sub_norm)
     {
@@ -418,20 +484,29 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       load_gain<CF>(ops[S_DN].gamma, nf, g);
       uint32_t pr[CF][4];
       wait_row_words<CF>(p, out_of(p, l, S_GU) + (int64_t)m * (p.F >> 1), p.F, step_tag(E, l, S_GU), pr, ws);
+      wait_memory();
       STEP_TRACE(l, 6);
       float v[CF][8];
       pairs_to_floats<CF>(pr, v);
       publish_row<CF>(p, l, S_DN, m, p.F, p.KSF, v, g, step_tag(E, l, S_DN), s_sum, s_max, s_rs);
       STEP_TRACE(l, 7);
+      clear_tile_share<CH>(tile_of(p, l, S_GU), m, p.KSH, false);
     }
     // ---- h = bf16(h + d)
     {
       if (l + 1 < p.L) load_gain<CH>(sops[(l + 1) * kStepOps + S_QKV].gamma, nh, g_qkv);
       uint32_t pr[CH][4];
       wait_row_words<CH>(p, out_of(p, l, S_DN) + (int64_t)m * (p.H >> 1), p.H, step_tag(E, l, S_DN), pr, ws);
+      wait_memory();
       residual_add(hid[0], pr[0], live);
     }
   }
+  // The last tile back to the sentinel: every launch leaves all tiles so.
+  // Threads with no output words of their own (tid >= H/8) skip the wait
+  // above, so they must not clear before the threads that poll have all of
+  // the row's words (every other clear sits behind publish_row's barriers).
+  lds_barrier();
+  clear_tile_share<CF>(tile_of(p, p.L - 1, S_DN), m, p.KSF, true);
   if (live && tid < nh)
     *reinterpret_cast<uint4*>(p.hidden + (int64_t)m * p.H + 8 * tid) =
         make_uint4(hid[0][0], hid[0][1], hid[0][2], hid[0][3]);
@@ -509,22 +584,63 @@ __device__ __forceinline__ void load_unit_weights(const StepArgs& p, const StepO
   }
 }
 
-// Poll wave: wait for the flags of rows [r0, r0 + n) of (l, j); the row sums
-// they carry go to s_rsum[0 .. n).
-__device__ void wait_flags(const StepArgs& p, int l, int j, int r0, int n, uint32_t want, int* s_rsum, WaitState& ws) {
-  const int lane = threadIdx.x & 63;
+// Poll wave: wait for the flags of rows [r0, r0 + n) of (l, j), lanes 0..31
+// reading word 0 and lanes 32..63 word 1 of row r0 + (lane & 31); the row
+// sums they carry go to s_rsum[0 .. n), a/127 to s_adq[0 .. n).
+__device__ void wait_flags(const StepArgs& p, int l, int j, int r0, int n, uint32_t want, int* s_rsum, float* s_adq,
+                           WaitState& ws) {
+  const int lane = threadIdx.x & 63, r = lane & 31, word = lane >> 5;
+  const bool act = r < n;
   unsigned k = 0;
   uint64_t f = 0;
   while (!ws.dead) {
-    if (lane < n) f = ld_coherent(flag_of(p, l, j, r0 + lane));
-    const bool ok = lane >= n || (uint32_t)(f >> 32) == want;
+    if (act) f = ld_coherent(flag_of(p, l, j, r0 + r) + word);
+    const bool ok = !act || (uint32_t)(f >> 32) == want;
     if (__all(ok)) break;
-    if (should_stop(p, ++k, ws)) break;
+    if (should_stop(p, ++k, ws, WAIT_FLAGS, want)) break;
     __builtin_amdgcn_s_sleep(BTL_STEP_POLL_SLEEP);
   }
-  if (lane < n) s_rsum[lane] = (int32_t)(uint32_t)f;
+  if (act) {
+    if (word == 0)
+      s_rsum[r] = (int32_t)(uint32_t)f;
+    else
+      s_adq[r] = __uint_as_float((uint32_t)f);
+  }
 }
 
+// Running minimum of the 16-bit lanes of the operand dwords read (v_pk_min_i16);
+// a lane at or below kTileSentinelMax16 means a piece still held the sentinel.
+typedef short s16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_min_i16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(s16x2_t, a),
+                                                                __builtin_bit_cast(s16x2_t, b)));
+}
+// Dwords 0 and 2 of a 16-byte operand slot each lie in one 8-byte piece,
+// written (data or sentinel) by one 8-byte store.
+__device__ __forceinline__ uint32_t slot_min(uint32_t mn, const v4i& a) {
+  return pk_min_i16(pk_min_i16(mn, (uint32_t)a.x), (uint32_t)a.z);
+}
+__device__ __forceinline__ bool slot_stale(uint32_t mn) {
+  return (int)(short)(mn & 0xffffu) <= kTileSentinelMax16 || (int)(short)(mn >> 16) <= kTileSentinelMax16;
+}
+// Rare path of an operand read that found the sentinel: polls the two 8-byte
+// pieces of one 16-byte slot (dwords 0 and 2, 4-byte loads that bypass the L1)
+// until neither is the sentinel, or the error word is set, or the wait runs
+// out (which sets it).  The slot is then read again in full.
+__device__ __forceinline__ void wait_tile_piece(const StepArgs& p, __amdgpu_buffer_rsrc_t xa, int off, unsigned& n,
+                                                WaitState& ws, uint32_t want) {
+  while (!ws.dead) {
+    const uint32_t d0 = __builtin_amdgcn_raw_buffer_load_b32(xa, off, 0, 16);
+    const uint32_t d2 = __builtin_amdgcn_raw_buffer_load_b32(xa, off + 8, 0, 16);
+    if (!slot_stale(pk_min_i16(d0, d2))) break;
+    if (++n > p.spin_limit) set_error_word(p, WAIT_TILE, want);
+    if (n > p.spin_limit || ld_coherent(p.error) != 0u) {
+      ws.dead = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(BTL_STEP_POLL_SLEEP);
+  }
+}
 // One BitLinear J of layer l on GEMM workgroup gi: wait for the operand
 // tile's rows, MFMA against the weights held in w, reduce the waves in LDS,
 // epilogue (tagged bf16 pairs), then issue the next BitLinear's weights into wn.
@@ -546,12 +662,12 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
   const uint32_t want = step_tag(E, l, J);
   int32_t* red = lds;                                // reductions
   int32_t* s_rsum = lds + kStepWaves * 2 * 16 * 64;  // [32] row sums from the flags
+  float* s_adq = reinterpret_cast<float*>(s_rsum + 32);  // [32] a/127 from the flags
   constexpr int NR = OpShape<J>::HALF ? 16 : 32;     // rows of the unit
-  if (wv == kStepPollWave) wait_flags(p, l, J, 16 * h, NR, want, s_rsum, ws);
-  lds_barrier();  // the operand rows are out (no wait for loads in flight)
+  if (wv == kStepPollWave) wait_flags(p, l, J, 16 * h, NR, want, s_rsum, s_adq, ws);
+  lds_barrier();  // the rows' flags are in (no wait for loads in flight)
   STEP_TRACE(l, 8 + 2 * J);
   const __amdgpu_buffer_rsrc_t xa = tile_rsrc(tile_of(p, l, J), 32 * op_ks(p, J) * 128);
-  const float* adq = adq_of(p, l, J);
   uint64_t* outw = out_of(p, l, J);
   const int n_out = J == S_QKV ? p.NQKV : J == S_GU ? p.F : p.H;
 
@@ -565,27 +681,51 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     const int er = tid >> 5, ec = tid & 31;
     const int row = 16 * h + er;
     const float sc = op_seg_scale(op, tile0 * 32 + ec);  // LDS reads, early: off the epilogue's path
-    const float ad = ld_coherent(adq + row);
+    const float ad = s_adq[er];
     const int a_lane = 16 * h + (lane & 15) + 32 * ((lane >> 4) & 1);
     const int a_step = lane >> 5;
+    // Operand loads, then the MFMAs as the data arrives, each operand's
+    // 16-bit lanes folded into a running minimum on the way.  A piece that
+    // still held the sentinel had not landed: then (rarely) the wave waits for
+    // its pieces, reads them and its weights again, and redoes the MFMAs.
     v4i a[NSW][2];
+    auto load = [&]() {
 #pragma unroll
-    for (int i = 0; i < NSW; ++i)
-      if (i < cnt)
+      for (int i = 0; i < NSW; ++i)
+        if (i < cnt)
 #pragma unroll
-        for (int pp = 0; pp < 2; ++pp) a[i][pp] = ld_tile(xa, (a_step * 64 + a_lane) * 16, ((wb + i) * 4 + 2 * pp) * 1024);
-    v4i acc[2] = {(v4i){0, 0, 0, 0}, (v4i){0, 0, 0, 0}};
+          for (int pp = 0; pp < 2; ++pp)
+            a[i][pp] = ld_tile(xa, (a_step * 64 + a_lane) * 16, ((wb + i) * 4 + 2 * pp) * 1024);
+    };
+    v4i acc[2];
+    auto mfma = [&](const v4i (&ww)[kStepWSlots]) {
+      acc[0] = acc[1] = (v4i){0, 0, 0, 0};
+      uint32_t mn = 0x7fff7fffu;
 #pragma unroll
-    for (int i = 0; i < NSW; ++i)
-      if (i < cnt)
+      for (int i = 0; i < NSW; ++i)
+        if (i < cnt)
 #pragma unroll
-        for (int pp = 0; pp < 2; ++pp) {
-          const auto s32 = __builtin_amdgcn_permlane32_swap((uint32_t)w[i][2 * pp], (uint32_t)w[i][2 * pp + 1],
-                                                            false, false);
-          const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
-          acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[0]), acc[0], 0, 0, 0);
-          acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[1]), acc[1], 0, 0, 0);
-        }
+          for (int pp = 0; pp < 2; ++pp) {
+            mn = slot_min(mn, a[i][pp]);
+            const auto s32 = __builtin_amdgcn_permlane32_swap((uint32_t)ww[i][2 * pp], (uint32_t)ww[i][2 * pp + 1],
+                                                              false, false);
+            const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
+            acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[0]), acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[1]), acc[1], 0, 0, 0);
+          }
+      return mn;
+    };
+    load();
+    if (__any(slot_stale(mfma(w)))) {
+      unsigned tries = 0;
+      for (int i = 0; i < cnt; ++i)
+        for (int pp = 0; pp < 2; ++pp)
+          wait_tile_piece(p, xa, (a_step * 64 + a_lane) * 16 + ((wb + i) * 4 + 2 * pp) * 1024, tries, ws, want);
+      load();
+      v4i wr[kStepWSlots];
+      load_unit_weights<J, NSW>(p, sops, l, gi, wr);
+      (void)mfma(wr);
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       red[(wv * 8 + q) * 64 + lane] = acc[0][q];
@@ -612,27 +752,47 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
       const int i = acc_row(wv + kStepWaves * rr, lane);
-      ad_r[rr] = ld_coherent(adq + i);
+      ad_r[rr] = s_adq[i];
       rs_r[rr] = s_rsum[i];
     }
+    // Operand loads, MFMAs with the sentinel fold, and the rare re-read, as
+    // in the 16-row body.
     v4i a[NSW][4];
+    auto load = [&]() {
 #pragma unroll
-    for (int i = 0; i < NSW; ++i)
-      if (i < cnt)
+      for (int i = 0; i < NSW; ++i)
+        if (i < cnt)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) a[i][q] = ld_tile(xa, lane * 16, ((wb + i) * 4 + q) * 1024);
+          for (int q = 0; q < 4; ++q) a[i][q] = ld_tile(xa, lane * 16, ((wb + i) * 4 + q) * 1024);
+    };
     v16i acc[TPW];
+    auto mfma = [&](const v4i (&ww)[kStepWSlots]) {
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) acc[t] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+      for (int t = 0; t < TPW; ++t) acc[t] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+      uint32_t mn = 0x7fff7fffu;
 #pragma unroll
-    for (int i = 0; i < NSW; ++i)
-      if (i < cnt)
+      for (int i = 0; i < NSW; ++i)
+        if (i < cnt)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+          for (int q = 0; q < 4; ++q) {
+            mn = slot_min(mn, a[i][q]);
 #pragma unroll
-          for (int t = 0; t < TPW; ++t)
-            acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][q], unpack_b((uint32_t)w[t * NSW + i][q]), acc[t], 0,
-                                                           0, 0);
+            for (int t = 0; t < TPW; ++t)
+              acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][q], unpack_b((uint32_t)ww[t * NSW + i][q]), acc[t],
+                                                             0, 0, 0);
+          }
+      return mn;
+    };
+    load();
+    if (__any(slot_stale(mfma(w)))) {
+      unsigned tries = 0;
+      for (int i = 0; i < cnt; ++i)
+        for (int q = 0; q < 4; ++q) wait_tile_piece(p, xa, lane * 16 + ((wb + i) * 4 + q) * 1024, tries, ws, want);
+      load();
+      v4i wr[kStepWSlots];
+      load_unit_weights<J, NSW>(p, sops, l, gi, wr);
+      (void)mfma(wr);
+    }
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
 #pragma unroll
@@ -652,10 +812,9 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
       }
     }
     lds_barrier();  // LDS free for the next BitLinear
-    // The a/127 loads (long done) are collected here, before the first store:
-    // stores share the in-order vector-memory counter with loads, and with the
-    // stores under lane masks the compiler would otherwise wait for all of
-    // them, coherent write acknowledgements included, before the second row.
+    // Every load of this BitLinear has been consumed; settling the counter
+    // here, before the first store, keeps the compiler from placing a wait
+    // (for the stores' acknowledgements too) between the two rows' stores.
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
@@ -706,7 +865,7 @@ __global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
   // workgroups of the launch.
   __shared__ __attribute__((aligned(16))) int32_t lds[24576];
   constexpr int kTableInts = kStepMaxLayers * kStepOps * (int)sizeof(StepOp) / 4;
-  static_assert(kStepWaves * 2 * 16 * 64 + 32 + kTableInts <= 24576, "LDS layout");
+  static_assert(kStepWaves * 2 * 16 * 64 + 64 + kTableInts <= 24576, "LDS layout");
   StepOp* sops = reinterpret_cast<StepOp*>(lds + (24576 - kTableInts));
   {
     const uint4* src = reinterpret_cast<const uint4*>(p.ops);
@@ -750,14 +909,17 @@ __device__ void floor_row(const StepArgs& p, int m, uint32_t E) {
                             reinterpret_cast<uint32_t(&)[1][4]>(pr), ws);
       }
       __syncthreads();
-      if (threadIdx.x == 0) st_coherent(flag_of(p, l, j, m), (uint64_t)step_tag(E, l, j) << 32);
+      if (threadIdx.x == 0) {
+        st_coherent(flag_of(p, l, j, m), (uint64_t)step_tag(E, l, j) << 32);
+        st_coherent(flag_of(p, l, j, m) + 1, (uint64_t)step_tag(E, l, j) << 32);
+      }
     }
   uint32_t pr[1][4];  // the last down projection's words end the row's step
   wait_row_words<1>(p, out_of(p, p.L - 1, S_DN) + (int64_t)m * (p.H >> 1), p.H, step_tag(E, p.L - 1, S_DN), pr, ws);
 }
 
 template <int J>
-__device__ __forceinline__ void floor_gemm_op(const StepArgs& p, int l, int gi, uint32_t E, int32_t* s_rsum,
+__device__ __forceinline__ void floor_gemm_op(const StepArgs& p, int l, int gi, uint32_t E, int32_t* s_rsum, float* s_adq,
                                               WaitState& ws) {
   if (gi >= op_units<J>(p)) return;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -765,7 +927,7 @@ __device__ __forceinline__ void floor_gemm_op(const StepArgs& p, int l, int gi, 
   unit_of<J>(p, gi, tile0, h);
   const uint32_t want = step_tag(E, l, J);
   constexpr int NR = OpShape<J>::HALF ? 16 : 32;
-  if (wv == kStepPollWave) wait_flags(p, l, J, 16 * h, NR, want, s_rsum, ws);
+  if (wv == kStepPollWave) wait_flags(p, l, J, 16 * h, NR, want, s_rsum, s_adq, ws);
   lds_barrier();
   uint64_t* outw = out_of(p, l, J);
   const int n_out = J == S_QKV ? p.NQKV : J == S_GU ? p.F : p.H;
@@ -785,6 +947,7 @@ __device__ __forceinline__ void floor_gemm_op(const StepArgs& p, int l, int gi, 
 template <int CF>
 __global__ __launch_bounds__(512) void k_decode_step_floor(StepArgs p) {
   __shared__ int32_t s_rsum[32];
+  __shared__ float s_adq[32];
   const int b = blockIdx.x;
   const uint32_t E = p.epoch[b] + 1u;
   if (b < kStepRows) {
@@ -792,10 +955,10 @@ __global__ __launch_bounds__(512) void k_decode_step_floor(StepArgs p) {
   } else {
     WaitState ws{false};
     for (int l = 0; l < p.L; ++l) {
-      floor_gemm_op<S_QKV>(p, l, b - kStepRows, E, s_rsum, ws);
-      floor_gemm_op<S_O>(p, l, b - kStepRows, E, s_rsum, ws);
-      floor_gemm_op<S_GU>(p, l, b - kStepRows, E, s_rsum, ws);
-      floor_gemm_op<S_DN>(p, l, b - kStepRows, E, s_rsum, ws);
+      floor_gemm_op<S_QKV>(p, l, b - kStepRows, E, s_rsum, s_adq, ws);
+      floor_gemm_op<S_O>(p, l, b - kStepRows, E, s_rsum, s_adq, ws);
+      floor_gemm_op<S_GU>(p, l, b - kStepRows, E, s_rsum, s_adq, ws);
+      floor_gemm_op<S_DN>(p, l, b - kStepRows, E, s_rsum, s_adq, ws);
     }
   }
   if (threadIdx.x == 0) p.epoch[b] = E;
@@ -803,7 +966,7 @@ __global__ __launch_bounds__(512) void k_decode_step_floor(StepArgs p) {
 
 // ---------------------------------------------------------------- host ----
 struct StepSizes {
-  int64_t off_xa[kStepOps], off_adq, off_flag, off_out[kStepOps], layer_bytes, total;
+  int64_t off_xa[kStepOps], tiles_end, off_flag, off_out[kStepOps], layer_bytes, total;
 };
 
 static StepSizes step_sizes(int64_t H, int64_t F, int64_t NQKV) {
@@ -816,8 +979,7 @@ static StepSizes step_sizes(int64_t H, int64_t F, int64_t NQKV) {
     z.off_xa[j] = off;
     off += round_up(32 * ksb(Ks[j]) * 128, 4096);
   }
-  z.off_adq = off;
-  off += 4096;
+  z.tiles_end = off;
   z.off_flag = off;
   off += kStepOps * 32 * 128;
   for (int j = 0; j < kStepOps; ++j) {
@@ -925,6 +1087,11 @@ int btl_decode_step_prepare(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64
     (void)hipGetLastError();
     return set_error(BTL_ERR_LAUNCH, "btl_decode_step_prepare: copying the op table failed");
   }
+  // operand tiles start every launch as the sentinel (a launch leaves them so)
+  if (hipMemset((char*)workspace + kStHeader, (int)(kTileSentinel & 0xffu), (size_t)z.tiles_end) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(BTL_ERR_LAUNCH, "btl_decode_step_prepare: resetting the operand tiles failed");
+  }
   return BTL_OK;
 }
 
@@ -964,7 +1131,6 @@ int btl_decode_step(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, fl
     a.off_xa[j] = z.off_xa[j];
     a.off_out[j] = z.off_out[j];
   }
-  a.off_adq = z.off_adq;
   a.off_flag = z.off_flag;
   a.spin_limit = 1u << 18;
   const int grid = step_grid();
@@ -1006,7 +1172,6 @@ int btl_decode_step_floor(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t
     a.off_xa[j] = z.off_xa[j];
     a.off_out[j] = z.off_out[j];
   }
-  a.off_adq = z.off_adq;
   a.off_flag = z.off_flag;
   a.spin_limit = 1u << 18;
   const int grid = step_grid();

@@ -273,11 +273,13 @@ int btl_decode_layer(int64_t M, int64_t H, int64_t Q, int64_t F, int64_t NQKV, c
  *
  * Workspace (256-byte aligned): btl_decode_step_workspace_bytes(...) bytes,
  * zero-filled once, then prepared with btl_decode_step_prepare (which copies
- * the weight table into it, synchronously: not under graph capture) and used
- * only by btl_decode_step calls on one device and one stream.  One workgroup
- * per CU waits on the others: nothing else may hold the GPU's CUs during the
- * launch (a wait that runs out sets the word at btl_decode_step_error_offset
- * and the outputs are invalid). */
+ * the weight table into it and sets its operand tiles to their between-use
+ * state, synchronously: not under graph capture) and used only by
+ * btl_decode_step calls on one device and one stream.  One workgroup per CU
+ * waits on the others: nothing else may hold the GPU's CUs during the launch
+ * (a wait that runs out sets the word at btl_decode_step_error_offset and the
+ * outputs are invalid; the workspace must then be zero-filled and prepared
+ * again before the next btl_decode_step). */
 int64_t btl_decode_step_workspace_bytes(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L);
 int64_t btl_decode_step_error_offset(void);
 int btl_decode_step_prepare(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L,
