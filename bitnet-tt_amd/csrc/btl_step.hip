@@ -689,13 +689,18 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     // still held the sentinel had not landed: then (rarely) the wave waits for
     // its pieces, reads them and its weights again, and redoes the MFMAs.
     v4i a[NSW][2];
+    // Every wave issues NSW superblocks of loads (one past its range reads the
+    // tile's first 16 bytes in every lane, one line), so all waves count the
+    // same loads and each MFMA waits only for its own operands.
     auto load = [&]() {
 #pragma unroll
-      for (int i = 0; i < NSW; ++i)
-        if (i < cnt)
+      for (int i = 0; i < NSW; ++i) {
+        const bool mine = i < cnt;
 #pragma unroll
-          for (int pp = 0; pp < 2; ++pp)
-            a[i][pp] = ld_tile(xa, (a_step * 64 + a_lane) * 16, ((wb + i) * 4 + 2 * pp) * 1024);
+        for (int pp = 0; pp < 2; ++pp)
+          a[i][pp] = ld_tile(xa, mine ? (a_step * 64 + a_lane) * 16 : 0, mine ? ((wb + i) * 4 + 2 * pp) * 1024 : 0);
+        __builtin_amdgcn_sched_barrier(0);  // superblocks in order: the first MFMAs wait for the first loads
+      }
     };
     v4i acc[2];
     auto mfma = [&](const v4i (&ww)[kStepWSlots]) {
@@ -758,12 +763,14 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     // Operand loads, MFMAs with the sentinel fold, and the rare re-read, as
     // in the 16-row body.
     v4i a[NSW][4];
-    auto load = [&]() {
+    auto load = [&]() {  // NSW superblocks in every wave, as in the 16-row body
 #pragma unroll
-      for (int i = 0; i < NSW; ++i)
-        if (i < cnt)
+      for (int i = 0; i < NSW; ++i) {
+        const bool mine = i < cnt;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) a[i][q] = ld_tile(xa, lane * 16, ((wb + i) * 4 + q) * 1024);
+        for (int q = 0; q < 4; ++q) a[i][q] = ld_tile(xa, mine ? lane * 16 : 0, mine ? ((wb + i) * 4 + q) * 1024 : 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     };
     v16i acc[TPW];
     auto mfma = [&](const v4i (&ww)[kStepWSlots]) {
