@@ -231,18 +231,29 @@ __device__ __forceinline__ bool should_stop(const StepArgs& p, unsigned n, WaitS
 #endif
 
 // One poll round: this thread's words, all of them, unconditionally (a chunk
-// past the row's end reads the last chunk, and nothing takes it).  Loads under
-// per-word lane masks would let the register allocator reuse a destination
-// before the round ends, and the wait that reuse needs would split the round
-// into several memory round trips.
+// past the row's end reads the last chunk, and nothing takes it), as 16-byte
+// loads that bypass the L1, two words each.  A word is written by one 8-byte
+// store (two bf16 outputs and their tag), and an aligned 16-byte load is one
+// access to one cache line, so each word it returns is either the old or the
+// new one, never a mix; the words of one load may differ in age, and each is
+// taken only once its own tag shows.  Loads under per-word lane masks would
+// let the register allocator reuse a destination before the round ends, and
+// the wait that reuse needs would split the round into several memory round
+// trips.
 template <int C>
 __device__ __forceinline__ void issue_words(const uint64_t* row, int nch, uint64_t (&d)[C][4]) {
   const int tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(row), (short)0, nch * 32, 0x00020000);
 #pragma unroll
   for (int i = 0; i < C; ++i) {
     const int c = min(tid + kActThreads * i, nch - 1);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) d[i][k] = ld_coherent(row + 4 * c + k);
+    for (int h = 0; h < 2; ++h) {
+      const v4i t = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, c * 32 + h * 16, 0, 16));
+      d[i][2 * h] = (uint64_t)(uint32_t)t.x | ((uint64_t)(uint32_t)t.y << 32);
+      d[i][2 * h + 1] = (uint64_t)(uint32_t)t.z | ((uint64_t)(uint32_t)t.w << 32);
+    }
   }
 }
 // Takes the words of a round (issued for `pend`) that carry the tag.
@@ -838,9 +849,12 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
         o = f2bf(sq * uu);
       }
       const uint32_t pair = o | (xor_partner_u<1>(o) << 16);  // lanes jc, jc+1 share the row (a DPP swap)
-      if ((jc & 1) == 0) st_coherent(outw + (int64_t)i * (n_out >> 1) + (n >> 1), ((uint64_t)want << 32) | pair);
-      if (J == S_QKV && i < p.M) p.qkv_out[(int64_t)i * p.NQKV + n] = (uint16_t)o;
-      if (J == S_GU && i < p.M) p.ffn_h[(int64_t)i * p.F + n] = (uint16_t)o;
+      if ((jc & 1) == 0) {
+        st_coherent(outw + (int64_t)i * (n_out >> 1) + (n >> 1), ((uint64_t)want << 32) | pair);
+        // the caller's copy: the same pair as one 4-byte store
+        if (J == S_QKV && i < p.M) *reinterpret_cast<uint32_t*>(p.qkv_out + (int64_t)i * p.NQKV + n) = pair;
+        if (J == S_GU && i < p.M) *reinterpret_cast<uint32_t*>(p.ffn_h + (int64_t)i * p.F + n) = pair;
+      }
     }
   }
   STEP_TRACE(l, 9 + 2 * J);
@@ -1109,9 +1123,9 @@ int btl_decode_step(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, fl
   int rc = step_check_shape(M, H, F, NQKV, L);
   if (rc) return rc;
   if (!attn || !hidden || !qkv_out || !ffn_h || !workspace) return set_error(BTL_ERR_NULL, "btl_decode_step: null pointer");
-  if (!aligned(attn, 16) || !aligned(hidden, 16) || !aligned(workspace, 256) || !aligned(qkv_out, 2) ||
-      !aligned(ffn_h, 2))
-    return set_error(BTL_ERR_ALIGN, "btl_decode_step: attn/hidden must be 16-byte aligned, workspace 256");
+  if (!aligned(attn, 16) || !aligned(hidden, 16) || !aligned(workspace, 256) || !aligned(qkv_out, 4) ||
+      !aligned(ffn_h, 4))
+    return set_error(BTL_ERR_ALIGN, "btl_decode_step: attn/hidden must be 16-byte aligned, qkv_out/ffn_h 4, workspace 256");
   const StepSizes z = step_sizes(H, F, NQKV);
   if ((int64_t)workspace_bytes < z.total)
     return set_error(BTL_ERR_WORKSPACE, "btl_decode_step: workspace %zu < %lld bytes", workspace_bytes,
