@@ -125,9 +125,13 @@ __device__ __forceinline__ int64_t xa_offset(int m, int k0, int KS) {
 // the rest (xor 8 = half-row mirror of the row mirror, xor 4 = quad reverse of
 // the half-row mirror).  No LDS round trip, so a 64-lane butterfly costs a few
 // ALU cycles per step instead of an LDS latency.
+// Every permutation used here stays inside a row of 16 lanes with all rows and
+// banks enabled, so no lane reads outside the wave and bound_ctrl changes
+// nothing; with it set, the compiler folds the move into the consuming
+// add / max (one v_*_dpp instead of a move and an ALU op).
 template <int C>
 __device__ __forceinline__ uint32_t dpp_mov(uint32_t x) {
-  return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, C, 0xF, 0xF, false);
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, C, 0xF, 0xF, true);
 }
 template <int D>
 __device__ __forceinline__ uint32_t xor_partner_u(uint32_t x) {

@@ -829,7 +829,10 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
         v[t][rr] = sum;
       }
     }
-    lds_barrier();  // LDS free for the next BitLinear
+    // LDS free for the next BitLinear.  The barrier also keeps every wave's
+    // output stores ahead of any wave's loads of the next weights in the CU's
+    // memory pipeline (two reduction areas without it measured 1 % slower).
+    lds_barrier();
     // Every load of this BitLinear has been consumed; settling the counter
     // here, before the first store, keeps the compiler from placing a wait
     // (for the stores' acknowledgements too) between the two rows' stores.
