@@ -103,21 +103,22 @@ struct StepOp {
 static_assert(sizeof(StepOp) == 64, "op table entry");
 constexpr int64_t kStHeader = kStTable + (int64_t)kStepMaxLayers * kStepOps * sizeof(StepOp);
 
-// GEMM unit shapes.  QKV, o_proj and gate||up units cover all 32 rows
-// (v_mfma_i32_32x32x32_i8: each unpacked weight dword feeds one MFMA); down,
-// whose operand tile is 221 KB at K = 6912, runs 16-row halves
-// (v_mfma_i32_16x16x64_i8), so that a unit reads half of it.  Every unit
-// covers all of K and writes bf16 outputs (two per tagged word).
+// GEMM unit shapes.  gate||up units cover all 32 rows (v_mfma_i32_32x32x32_i8:
+// each unpacked weight dword feeds one MFMA) with a gate tile and its up
+// tile.  QKV, o_proj and down run 16-row halves (v_mfma_i32_16x16x64_i8), so
+// that a unit reads half of its operand tile: QKV with two adjacent column
+// tiles per unit (its 120 tiles make 120 units), o_proj and down with one.
+// Every unit covers all of K and writes bf16 outputs (two per tagged word).
 enum { MODE_SCALE = 0, MODE_RELU2 = 1 };
 template <int J>
 struct OpShape;
 template <>
 struct OpShape<S_QKV> {
-  static constexpr int TPW = 1, HALF = 0, MODE = MODE_SCALE;
+  static constexpr int TPW = 2, HALF = 1, MODE = MODE_SCALE;
 };
 template <>
 struct OpShape<S_O> {
-  static constexpr int TPW = 1, HALF = 0, MODE = MODE_SCALE;
+  static constexpr int TPW = 1, HALF = 1, MODE = MODE_SCALE;
 };
 template <>
 struct OpShape<S_GU> {
@@ -472,7 +473,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       pairs_to_floats<CH>(pr, v);
       publish_row<CH>(p, l, S_O, m, p.H, p.KSH, v, g, step_tag(E, l, S_O), s_sum, s_max, s_rs);
       STEP_TRACE(l, 3);
-      clear_tile_share<CH>(tile_of(p, l, S_QKV), m, p.KSH, false);
+      clear_tile_share<CH>(tile_of(p, l, S_QKV), m, p.KSH, true);
     }
     // ---- GU: h = bf16(h + o); RMSNorm(h; post_attention_layernorm)
     {
@@ -487,7 +488,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       pairs_to_floats<CH>(hid, v);
       publish_row<CH>(p, l, S_GU, m, p.H, p.KSH, v, g, step_tag(E, l, S_GU), s_sum, s_max, s_rs);
       STEP_TRACE(l, 5);
-      clear_tile_share<CH>(tile_of(p, l, S_O), m, p.KSH, false);
+      clear_tile_share<CH>(tile_of(p, l, S_O), m, p.KSH, true);
     }
     // ---- DN: RMSNorm(relu(g)^2 * u; ffn_sub_norm)
     {
@@ -531,34 +532,38 @@ __device__ __forceinline__ int op_ks(const StepArgs& p, int j) { return j == S_D
 template <int J>
 __device__ __forceinline__ int op_units(const StepArgs& p) {
   const int NT = op_n(p, J) / 32;
-  return J == S_GU ? NT / 2 : OpShape<J>::HALF ? 2 * NT : NT;
+  return J == S_GU ? NT / 2 : OpShape<J>::HALF ? 2 * NT / OpShape<J>::TPW : NT;
 }
 
 // Unit u of BitLinear J: its first tile (GU: the gate tile; the up tile is
-// F/32 further) and, for 16-row units, its row half h.  The two halves of a
-// tile are 8 workgroups apart, so round-robin dispatch puts them on one XCD
-// and its L2 fetches their weights once.
+// F/32 further) and, for 16-row units, its row half h.  16-row units take
+// groups of TPW adjacent tiles; the two halves of a group are 8 workgroups
+// apart, so round-robin dispatch puts them on one XCD and its L2 fetches
+// their weights once.
 template <int J>
 __device__ __forceinline__ void unit_of(const StepArgs& p, int u, int& tile0, int& h) {
-  const int NT = op_n(p, J) / 32;
+  const int NG = op_n(p, J) / 32 / (OpShape<J>::HALF ? OpShape<J>::TPW : 1);
   h = 0;
   if (!OpShape<J>::HALF) {
     tile0 = u;
     return;
   }
-  const int g8 = NT & ~7;
+  const int g8 = NG & ~7;
+  int g;
   if (u < 2 * g8) {
-    tile0 = ((u >> 4) << 3) | (u & 7);
+    g = ((u >> 4) << 3) | (u & 7);
     h = (u >> 3) & 1;
   } else {
-    const int i = u - 2 * g8, rem = NT - g8;
-    tile0 = g8 + i % rem;
+    const int i = u - 2 * g8, rem = NG - g8;
+    g = g8 + i % rem;
     h = i / rem;
   }
+  tile0 = g * OpShape<J>::TPW;
 }
 template <int J>
 __device__ __forceinline__ int unit_tile(const StepArgs& p, int tile0, int t) {
-  return t == 0 ? tile0 : tile0 + op_n(p, J) / 64;  // GU: up tile F/32 after the gate tile
+  if (J == S_GU) return t == 0 ? tile0 : tile0 + op_n(p, J) / 64;  // the up tile F/32 after the gate tile
+  return tile0 + t;
 }
 
 // This wave's superblocks of [sb0, sb1): waves w and w + 4 share a SIMD, so
@@ -691,7 +696,9 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     // C: lane l, element j is row 4 (l >> 4) + j, column l & 15.
     const int er = tid >> 5, ec = tid & 31;
     const int row = 16 * h + er;
-    const float sc = op_seg_scale(op, tile0 * 32 + ec);  // LDS reads, early: off the epilogue's path
+    float sc[TPW];  // LDS reads, early: off the epilogue's path
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) sc[t] = op_seg_scale(op, unit_tile<J>(p, tile0, t) * 32 + ec);
     const float ad = s_adq[er];
     const int a_lane = 16 * h + (lane & 15) + 32 * ((lane >> 4) & 1);
     const int a_step = lane >> 5;
@@ -713,9 +720,10 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
         __builtin_amdgcn_sched_barrier(0);  // superblocks in order: the first MFMAs wait for the first loads
       }
     };
-    v4i acc[2];
+    v4i acc[TPW][2];
     auto mfma = [&](const v4i (&ww)[kStepWSlots]) {
-      acc[0] = acc[1] = (v4i){0, 0, 0, 0};
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) acc[t][0] = acc[t][1] = (v4i){0, 0, 0, 0};
       uint32_t mn = 0x7fff7fffu;
 #pragma unroll
       for (int i = 0; i < NSW; ++i)
@@ -723,11 +731,14 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
 #pragma unroll
           for (int pp = 0; pp < 2; ++pp) {
             mn = slot_min(mn, a[i][pp]);
-            const auto s32 = __builtin_amdgcn_permlane32_swap((uint32_t)ww[i][2 * pp], (uint32_t)ww[i][2 * pp + 1],
-                                                              false, false);
-            const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
-            acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[0]), acc[0], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[1]), acc[1], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < TPW; ++t) {
+              const auto s32 = __builtin_amdgcn_permlane32_swap((uint32_t)ww[t * NSW + i][2 * pp],
+                                                                (uint32_t)ww[t * NSW + i][2 * pp + 1], false, false);
+              const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
+              acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[0]), acc[t][0], 0, 0, 0);
+              acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[1]), acc[t][1], 0, 0, 0);
+            }
           }
       return mn;
     };
@@ -743,20 +754,32 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
       (void)mfma(wr);
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      red[(wv * 8 + q) * 64 + lane] = acc[0][q];
-      red[(wv * 8 + 4 + q) * 64 + lane] = acc[1][q];
-    }
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        red[((wv * TPW + t) * 8 + q) * 64 + lane] = acc[t][0][q];
+        red[((wv * TPW + t) * 8 + 4 + q) * 64 + lane] = acc[t][1][q];
+      }
     lds_barrier();
     const int reg = 4 * (ec >> 4) + (er & 3), src = 16 * (er >> 2) + (ec & 15);
-    int32_t sum = -s_rsum[er];
+    int32_t sum[TPW];
 #pragma unroll
-    for (int v2 = 0; v2 < kStepWaves; ++v2) sum += red[(v2 * 8 + reg) * 64 + src];
+    for (int t = 0; t < TPW; ++t) {
+      sum[t] = -s_rsum[er];
+#pragma unroll
+      for (int v2 = 0; v2 < kStepWaves; ++v2) sum[t] += red[((v2 * TPW + t) * 8 + reg) * 64 + src];
+    }
     lds_barrier();  // LDS free for the next BitLinear
-    const int n = tile0 * 32 + ec;
-    const uint32_t o = f2bf((float)sum * (sc * ad));
-    const uint32_t pair = o | (xor_partner_u<1>(o) << 16);  // lanes ec, ec+1 share the row (a DPP swap)
-    if ((ec & 1) == 0) st_coherent(outw + (int64_t)row * (n_out >> 1) + (n >> 1), ((uint64_t)want << 32) | pair);
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int n = unit_tile<J>(p, tile0, t) * 32 + ec;
+      const uint32_t o = f2bf((float)sum[t] * (sc[t] * ad));
+      const uint32_t pair = o | (xor_partner_u<1>(o) << 16);  // lanes ec, ec+1 share the row (a DPP swap)
+      if ((ec & 1) == 0) {
+        st_coherent(outw + (int64_t)row * (n_out >> 1) + (n >> 1), ((uint64_t)want << 32) | pair);
+        if (J == S_QKV && row < p.M) *reinterpret_cast<uint32_t*>(p.qkv_out + (int64_t)row * p.NQKV + n) = pair;
+      }
+    }
   } else {
     // ---- all 32 rows on v_mfma_i32_32x32x32_i8 ----
     const int jc = lane & 31;
@@ -956,8 +979,12 @@ __device__ __forceinline__ void floor_gemm_op(const StepArgs& p, int l, int gi, 
   uint64_t* outw = out_of(p, l, J);
   const int n_out = J == S_QKV ? p.NQKV : J == S_GU ? p.F : p.H;
   if constexpr (OpShape<J>::HALF) {
-    const int er = tid >> 5, ec = tid & 31, row = 16 * h + er, n = tile0 * 32 + ec;
-    if ((ec & 1) == 0) st_coherent(outw + (int64_t)row * (n_out >> 1) + (n >> 1), (uint64_t)want << 32);
+    const int er = tid >> 5, ec = tid & 31, row = 16 * h + er;
+#pragma unroll
+    for (int t = 0; t < OpShape<J>::TPW; ++t) {
+      const int n = unit_tile<J>(p, tile0, t) * 32 + ec;
+      if ((ec & 1) == 0) st_coherent(outw + (int64_t)row * (n_out >> 1) + (n >> 1), (uint64_t)want << 32);
+    }
   } else {
     const int jc = lane & 31, n = tile0 * 32 + jc;
 #pragma unroll
