@@ -200,6 +200,7 @@ __device__ __forceinline__ float op_seg_scale(const StepOp& op, int n) {
 // error word is set and waits end early.
 struct WaitState {
   bool dead;
+  bool reread;  // take the operand re-read path every time (set by a test through the workspace)
 };
 // The error word names the first wait that ran out: kind (1 row words, 2 row
 // flags, 3 operand tile) | (layer*4 + BitLinear) << 8 | workgroup << 16.
@@ -743,7 +744,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
       return mn;
     };
     load();
-    if (__any(slot_stale(mfma(w)))) {
+    if (__any(slot_stale(mfma(w))) || ws.reread) {
       unsigned tries = 0;
       for (int i = 0; i < cnt; ++i)
         for (int pp = 0; pp < 2; ++pp)
@@ -825,7 +826,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
       return mn;
     };
     load();
-    if (__any(slot_stale(mfma(w)))) {
+    if (__any(slot_stale(mfma(w))) || ws.reread) {
       unsigned tries = 0;
       for (int i = 0; i < cnt; ++i)
         for (int q = 0; q < 4; ++q) wait_tile_piece(p, xa, lane * 16 + ((wb + i) * 4 + q) * 1024, tries, ws, want);
@@ -892,7 +893,10 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
 // NQ: superblocks per wave of a unit of QKV, O and GU (K = H); NDN: of DN (K = F).
 template <int NQ, int NDN>
 __device__ void step_gemm(const StepArgs& p, const StepOp* sops, int gi, uint32_t E, int32_t* lds) {
-  WaitState ws{false};
+  // Word kStError + 64 of the workspace: bit 0 makes every GEMM unit take the
+  // re-read path of its sentinel check (a test of that rare path; the results
+  // are the same bits).
+  WaitState ws{false, (__builtin_amdgcn_readfirstlane(p.error[16]) & 1u) != 0u};
   v4i wa[kStepWSlots], wb[kStepWSlots];
   load_unit_weights<S_QKV, NQ>(p, sops, 0, gi, wa);
   for (int l = 0; l < p.L; ++l) {

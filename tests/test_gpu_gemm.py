@@ -370,8 +370,9 @@ def test_fused_decode_handshake_clean(orc):
 
 
 @pytest.mark.parametrize("m,k,n,epi", [(32, 2560, 2560, "none"), (17, 6912, 2560, "none"), (24, 2560, 640, "none"),
-                                        (32, 6912, 96, "none"), (32, 2560, 3840, "qkv"), (32, 2560, 13824, "relu2_mul"),
-                                        (19, 2560, 13824, "relu2_mul"), (32, 2560, 1024, "relu2_mul")])
+                                        (32, 6912, 96, "none"), (32, 2560, 3840, "qkv"), (17, 2560, 3840, "qkv"),
+                                        (32, 2560, 13824, "relu2_mul"), (19, 2560, 13824, "relu2_mul"),
+                                        (32, 2560, 1024, "relu2_mul"), (24, 2560, 1024, "relu2_mul")])
 def test_fused_row_halves_bit_exact(orc, m, k, n, epi):
     """Single-launch BitLinear with more than 16 rows.  Two GEMM workgroups
     take each column group, one per 16-row half, in these cases:
@@ -381,11 +382,12 @@ def test_fused_row_halves_bit_exact(orc, m, k, n, epi):
     - gate||up at 1024 (one gate/up pair a group, relu2 epilogue).
     The 2B gate||up shape keeps whole-tile workgroups.  In every case the int8
     rows, int32 accumulators and bf16 outputs equal the oracle's, also for the
-    rows of a half that stops at M."""
+    rows of a half that stops at M.  The two calls take different inputs (a
+    half that read the first call's rows after a timed-out wait would fail),
+    and no bounded wait runs out."""
     from bitnet_tt.ternary_matmul import PackedTernaryWeight, ternary_matmul
 
     print(f"row halves m={m} k={k} n={n} {epi}", flush=True)
-    xb = H.activations(orc, m, k, seed=m + k + 7)
     gb = H.gamma(orc, k, seed=n + 3)
     w = H.ternary(k, n, seed=k + 5)
     if epi == "relu2_mul":
@@ -398,16 +400,18 @@ def test_fused_row_halves_bit_exact(orc, m, k, n, epi):
     pw = PackedTernaryWeight(device_weight(orc, w), k, n, tuple(scales), tuple(ends))
     acc = torch.empty((m, n), dtype=torch.int32, device=H.dev())
     xq = torch.empty((m, k), dtype=torch.int8, device=H.dev())
-    ref = orc.bitlinear(xb, w, scales, ends, gamma_bf16=gb, norm_eps=1e-5, residual_bf16=res)
-    exp = ref["out"] if epi != "relu2_mul" else orc.relu2_mul_bf16(ref["out"][:, : n // 2], ref["out"][:, n // 2:])
     kw = dict(residual=H.to_dev_bf16(res)) if res is not None else {}
     for rep in range(2):
+        xb = H.activations(orc, m, k, seed=m + k + 7 + 1000 * rep)
+        ref = orc.bitlinear(xb, w, scales, ends, gamma_bf16=gb, norm_eps=1e-5, residual_bf16=res)
+        exp = ref["out"] if epi != "relu2_mul" else orc.relu2_mul_bf16(ref["out"][:, : n // 2], ref["out"][:, n // 2:])
         out = ternary_matmul(H.to_dev_bf16(xb), pw, norm_weight=H.to_dev_bf16(gb), norm_epsilon=1e-5,
                              epilogue="relu2_mul" if epi == "relu2_mul" else "none", acc_out=acc, xq_out=xq, **kw)
         torch.cuda.synchronize()
         assert np.array_equal(xq.cpu().numpy(), ref["q"]), f"call {rep}: int8 rows differ"
         assert np.array_equal(acc.cpu().numpy(), ref["acc"]), f"call {rep}: accumulators differ"
         assert np.array_equal(H.bits_of(out), exp), f"call {rep}: outputs differ"
+    N.check_errors(H.dev())  # raises if a bounded wait of these calls ran out
 
 
 def test_fused_workspace_shared_across_shapes(orc):

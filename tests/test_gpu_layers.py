@@ -25,6 +25,7 @@ from bitnet_tt.layers.attention import QKVProjection
 from bitnet_tt.layers.bitlinear import Linear
 from bitnet_tt.layers.ffn import FeedForward
 from bitnet_tt.ternary_matmul import ternary_matmul
+from bitnet_tt import _native as N
 
 pytestmark = pytest.mark.gpu
 
@@ -360,3 +361,28 @@ def test_c4_full_model_persistent_step_exact(orc, c4_model):
         bad = int((got != hiddens[-1]).sum())
         assert bad == 0, f"run {rep}: {bad} of {got.size} hidden values differ after 30 layers"
         assert np.array_equal(H.bits_of(step.qkv_out), ref_qkv), f"run {rep}: last QKV output"
+
+
+def test_c4_persistent_step_reread_path(orc, c4_model):
+    """The rare path of the step's sentinel check (a GEMM unit that found
+    operand bytes not yet landed waits for them, reads its tile and weights
+    again and redoes its MFMAs), forced for every unit through the step
+    workspace's test word: the same bits as the oracle chain."""
+    step, hiddens, ref_qkv = c4_model
+    step.reset_hidden()
+    step.step_persistent()  # prepares this stream's step workspace
+    step.check()
+    key = next(k for k in N._workspaces if k[0] == "step" and k[2] == torch.cuda.current_stream().cuda_stream)
+    ws = N._workspaces[key]
+    off = int(N.lib().btl_decode_step_error_offset()) + 64
+    ws[off:off + 4] = torch.tensor([1, 0, 0, 0], dtype=torch.uint8, device=ws.device)
+    try:
+        step.reset_hidden()
+        step.step_persistent()
+        step.check()
+        got = H.bits_of(step.hidden)
+        assert int((got != hiddens[-1]).sum()) == 0, "hidden differs with every unit on the re-read path"
+        assert np.array_equal(H.bits_of(step.qkv_out), ref_qkv)
+    finally:
+        ws[off:off + 4] = 0
+        torch.cuda.synchronize()
