@@ -324,7 +324,10 @@ def prefill_mfma(torch, N, dev, shapes=PREFILL_SHAPES, pmc_reps=0):
         us_bl = graph_time_us(torch, dev, bitlinear)
         ops = 2.0 * M * K * Nf
         tops = ops / (us * 1e-6) / 1e12
-        out.append({"M": M, "K": K, "N": Nf, "splitk": int(L.btl_choose_splitk(M, K, Nf, 0)),
+        tl = N.gemm_tiling(M, K, Nf)
+        tiling = (f"{tl['rows']}x{32 * tl['col_tiles']}" + (f" wq{tl['k_groups']}" if tl["kind"] == "wide" else "")
+                  + (f" sk{tl['splitk']}" if tl["splitk"] > 1 else ""))
+        out.append({"M": M, "K": K, "N": Nf, "tiling": tiling,
                     "us": round(us, 2), "tops": round(tops, 1), "mfma_i8_util": round(tops / MFMA_I8_PEAK_TOPS, 4),
                     "us_bitlinear": round(us_bl, 2),
                     "mfma_i8_util_bitlinear": round(ops / (us_bl * 1e-6) / 1e12 / MFMA_I8_PEAK_TOPS, 4)})

@@ -77,6 +77,7 @@ EXPORTS = {
     "btl_devlayout_words": ([_I64, _I64], _I64),
     "btl_act_bytes": ([_I64, _I64], _I64),
     "btl_choose_splitk": ([_I64, _I64, _I64, _I], _I),
+    "btl_gemm_tiling": ([_I64, _I64, _I64, _I, _I, _P], _I),
     "btl_gemm_workspace_bytes": ([_I64, _I64, _I64, _I, _I], _I64),
     "btl_fused_workspace_bytes": ([_I64, _I64, _I64, _I, _I], _I64),
     "btl_fused_error_offset": ([], _I64),
@@ -318,3 +319,12 @@ def check_errors(device=None) -> None:
         "was out of range; the outputs of the calls since the last check are invalid, and the workspaces have "
         "been reset"
     )
+
+
+def gemm_tiling(M: int, K: int, N: int, epilogue: int = EPI_SCALE, rowsum_given: bool = True) -> dict:
+    """The tiling btl_gemm_i8t2 runs for a shape (a planning query)."""
+    info = (ctypes.c_int32 * 6)()
+    check(lib().btl_gemm_tiling(M, K, N, epilogue, int(bool(rowsum_given)), info), "btl_gemm_tiling")
+    kind = ("decode", "tiles", "wide")[info[0]]
+    return {"kind": kind, "rows": info[1], "col_tiles": info[2], "splitk": info[3], "k_groups": info[4],
+            "tiles_per_wave": info[5]}

@@ -872,6 +872,315 @@ __global__ __launch_bounds__(256, 2) void k_gemm_prefill(GemmArgs p, int ngm, in
   BTL_TRACE_AT(14);
 }
 
+// ------------------------------------------------- prefill, wide tiles ----
+// Two workgroups per CU (four waves each, one per SIMD) and an output tile
+// sized so that the grid is about two tiles per CU: 64 rows (two row blocks)
+// x CT column tiles, CT = ceil(NT / (2 CUs / row tiles)).  At M = 2048 on 256
+// CUs that is 32 row tiles x 16 column groups (CT = 14, 8, 5 for N = 6912,
+// 3840, 2560), so every CU gets about the same share where 128x256 tiles
+// leave some CUs one tile and others two.  The two workgroups of a CU run
+// independently, so one's barrier and LDS waits overlap the other's MFMAs.
+// Every wave covers both row blocks (each unpacked weight operand feeds two
+// MFMAs); wave w takes column span w / WQ of 4 / WQ and k-step group w % WQ
+// of each superblock:
+//   WQ = 1: span w of 4, all four k-steps;
+//   WQ = 2: span w / 2 of 2, k-steps 2 (w % 2) and 2 (w % 2) + 1;
+//   WQ = 4: all CT tiles, k-step w;
+// whichever gives the smallest per-wave share; spans differ by at most one
+// tile.  k-step partials are added in LDS at the end (integers: any order
+// gives the same sums).
+// Staging as in k_gemm_prefill (global_load_lds, ST rotating stages, one
+// barrier per superblock), with up to 8 stages.  A stage holds the 8
+// activation chunks (chunk rb*4 + k-step) and up to 4*CTW/WQ weight chunks;
+// wave w loads chunks w, w + 4, ...; chunks a tile does not have become
+// 4-byte loads into a pad line, so every wave has the same number of loads in
+// flight and waits on one vmcnt.  (Measured on MI355X: reading the next
+// superblock's operands during the MFMAs, or spreading the refill loads
+// between them, is slower -- more registers, and the other workgroup of the
+// CU already fills those gaps; one workgroup of eight waves per CU is slower
+// too, its barriers stall all four SIMDs at once.)
+// Epilogue per row block: the waves put their raw sums into LDS in MFMA
+// layout ([tile][register][lane]; k-step groups added with LDS atomics);
+// then each thread converts 8 consecutive columns of a row (row sum, weight
+// scale x a_dq, bf16, + residual) and writes them with one 16-byte store,
+// consecutive threads along the row.
+constexpr int kWideLds = 76 * 1024;  // two workgroups a CU
+constexpr int kWideMaxStages = 8;
+constexpr int kWideGroupRows = 8;  // XCD order: groups of 8 row tiles, column groups inner
+constexpr int kWideResWords = 16 * 64 + 8;  // epilogue words per column tile (padded)
+
+template <int CTW, int WQ>
+struct WideShape {
+  static constexpr int qw = 4 / WQ;                        // k-steps per superblock per wave
+  static constexpr int ctmax = CTW * 4 / WQ;               // column tiles a tile may have
+  static constexpr int pw = 2 + (ctmax + 3) / 4;           // loads per wave per stage
+  static constexpr int stage_bytes = (8 + ctmax) * 1024 + 256;  // + the pad line
+  static constexpr int st = kWideLds / stage_bytes < kWideMaxStages ? kWideLds / stage_bytes : kWideMaxStages;
+  static constexpr int kpt = (32 * 4 * ctmax + 255) / 256;  // epilogue chunks per thread and row block
+  static_assert((st - 1) * pw < 64, "vmcnt immediate");
+  static_assert(st >= 3, "pipeline depth");
+  // column tiles whose epilogue sums fit in the stage buffers
+  static constexpr int ctfit = st * stage_bytes / (kWideResWords * 4) < ctmax ? st * stage_bytes / (kWideResWords * 4)
+                                                                             : ctmax;
+};
+
+// Wave wv's loads of superblock ks: chunk wv + 4i of the stage; loads
+// i < nreal are real, the rest pad loads.
+template <int PW>
+__device__ __forceinline__ void wide_issue(int8_t* stage, int8_t* pad, const int8_t* const* src, const int* step,
+                                           int nreal, int ks, int wv) {
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    if (i < nreal)
+      __builtin_amdgcn_global_load_lds(src[i] + (int64_t)ks * step[i], stage + (wv + 4 * i) * 1024, 16, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds(src[0] + (int64_t)ks * step[0], pad, 4, 0, 0);
+  }
+}
+
+template <int QW>
+__device__ __forceinline__ void wide_read_b(const int8_t* p, uint32_t (&d)[QW]) {
+  if constexpr (QW == 4) {
+    const v4i v = *reinterpret_cast<const v4i*>(p);
+    d[0] = (uint32_t)v.x, d[1] = (uint32_t)v.y, d[2] = (uint32_t)v.z, d[3] = (uint32_t)v.w;
+  } else if constexpr (QW == 2) {
+    typedef int v2i __attribute__((ext_vector_type(2)));
+    const v2i v = *reinterpret_cast<const v2i*>(p);
+    d[0] = (uint32_t)v.x, d[1] = (uint32_t)v.y;
+  } else {
+    d[0] = *reinterpret_cast<const uint32_t*>(p);
+  }
+}
+
+// Operands of one superblock for a wave with NC column tiles: the
+// activation k-steps of its group (both row blocks) and its weight dwords.
+template <int NC, int QW>
+struct WideOps {
+  v4i a[QW][2];
+  uint32_t bw[NC > 0 ? NC : 1][QW];
+};
+
+template <int NC, int QW>
+__device__ __forceinline__ void wide_read_ops(const int8_t* buf, int qg, int slot0, int lane, WideOps<NC, QW>& o) {
+  if constexpr (NC > 0) {
+#pragma unroll
+    for (int q = 0; q < QW; ++q) {
+      o.a[q][0] = *reinterpret_cast<const v4i*>(buf + (qg * QW + q) * 1024 + lane * 16);
+      o.a[q][1] = *reinterpret_cast<const v4i*>(buf + (4 + qg * QW + q) * 1024 + lane * 16);
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) wide_read_b<QW>(buf + slot0 + c * 1024 + lane * 16 + qg * QW * 4, o.bw[c]);
+  }
+}
+
+template <int NC, int CTW, int QW>
+__device__ __forceinline__ void wide_mfma(v16i (&acc)[2][CTW], const WideOps<NC, QW>& o) {
+  if constexpr (NC > 0) {
+#pragma unroll
+    for (int q = 0; q < QW; ++q) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const v4i b = unpack_b(o.bw[c][q]);
+        acc[0][c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[q][0], b, acc[0][c], 0, 0, 0);
+        acc[1][c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[q][1], b, acc[1][c], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// The superblock loop of a wave with NC column tiles (NC <= CTW), its first
+// tile at LDS offset slot0 of a stage; the first ST superblocks are issued.
+template <int NC, int CTW, int WQ>
+__device__ __forceinline__ void wide_loop(v16i (&acc)[2][CTW], int8_t* lds, int8_t* pad, const int8_t* const* src,
+                                          const int* step, int nreal, int KS, int wv, int qg, int slot0, int lane) {
+  using S = WideShape<CTW, WQ>;
+  constexpr int ST = S::st, SB = S::stage_bytes, PW = S::pw, QW = S::qw;
+  for (int ks = 0; ks < KS; ++ks) {
+    pf_wait<PW, ST>(min(ks == 0 ? ST - 1 : ST - 2, KS - 1 - ks));
+    // every wave's loads of ks have landed and every wave is done reading
+    // stage (ks - 1) % ST, which is refilled with superblock ks - 1 + ST
+    lds_barrier();
+    if (ks < 2) BTL_TRACE_AT(1 + ks);
+    if (ks == KS / 2) BTL_TRACE_AT(3);
+    if (ks >= 1 && ks - 1 + ST < KS) wide_issue<PW>(lds + ((ks - 1) % ST) * SB, pad, src, step, nreal, ks - 1 + ST, wv);
+    WideOps<NC, QW> o;
+    wide_read_ops<NC, QW>(lds + (ks % ST) * SB, qg, slot0, lane, o);
+    wide_mfma<NC, CTW, QW>(acc, o);
+  }
+}
+
+// The loop unrolled over the wave's range size nct (0 <= nct <= CTW).
+template <int N, int CTW, int WQ>
+__device__ __forceinline__ void wide_dispatch(int nct, v16i (&acc)[2][CTW], int8_t* lds, int8_t* pad,
+                                              const int8_t* const* src, const int* step, int nreal, int KS, int wv,
+                                              int qg, int slot0, int lane) {
+  if constexpr (N == 0) {
+    wide_loop<0, CTW, WQ>(acc, lds, pad, src, step, nreal, KS, wv, qg, slot0, lane);
+  } else {
+    if (nct == N)
+      wide_loop<N, CTW, WQ>(acc, lds, pad, src, step, nreal, KS, wv, qg, slot0, lane);
+    else
+      wide_dispatch<N - 1, CTW, WQ>(nct, acc, lds, pad, src, step, nreal, KS, wv, qg, slot0, lane);
+  }
+}
+
+// Scale epilogue with the row sums given (p.rowsum).  CT <= WideShape::ctfit.
+template <int CTW, int WQ>
+__global__ __launch_bounds__(256, 2) void k_gemm_wide(GemmArgs p, int ngm, int ngn, int CT) {
+  using S = WideShape<CTW, WQ>;
+  constexpr int ST = S::st, SB = S::stage_bytes, PW = S::pw, KPT = S::kpt;
+  __shared__ __attribute__((aligned(16))) int8_t lds[ST * SB + 64 * 8 + S::ctmax * 4];
+  float* s_adq = reinterpret_cast<float*>(lds + ST * SB);
+  int32_t* s_rs = reinterpret_cast<int32_t*>(lds + ST * SB + 64 * 4);
+  float* s_sw = reinterpret_cast<float*>(lds + ST * SB + 64 * 8);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // SIMD s = wv % 4 takes k-step group qg of column span [lo, hi); its two
+  // waves take the two halves of the span.
+  const int qg = wv % WQ, part = wv / WQ, nparts = 4 / WQ;
+  const int ntiles = ngm * ngn;
+  const int per = (ntiles + kPfXcds - 1) / kPfXcds;
+  const int t = (int)(blockIdx.x % kPfXcds) * per + (int)(blockIdx.x / kPfXcds);
+  if (t >= ntiles) return;
+  const int grp = t / (kWideGroupRows * ngn);
+  const int rows_in = min(kWideGroupRows, ngm - grp * kWideGroupRows);
+  const int rt = t - grp * kWideGroupRows * ngn;
+  const int gm = grp * kWideGroupRows + rt % rows_in;
+  const int gn = rt / rows_in;
+  const int KS = p.KS;
+
+  // Sources: i = 0, 1 the activation chunk of row block i, k-step wv; i >= 2
+  // weight tile wv + 4 (i - 2) of the tile (clamped into the matrix).
+  const int8_t* src[PW];
+  int step[PW];
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    if (i < 2) {
+      const int mb = min(gm * 2 + i, p.Mb - 1);
+      src[i] = p.xa + ((((int64_t)mb * KS) * 4 + wv) * 64 + lane) * 16;
+      step[i] = 4096;
+    } else {
+      const int tile = min(gn * CT + wv + 4 * (i - 2), p.NT - 1);
+      src[i] = reinterpret_cast<const int8_t*>(p.wdev) + (((int64_t)tile * KS) * 64 + lane) * 16;
+      step[i] = 1024;
+    }
+  }
+  const int nreal = 2 + (CT > wv ? (CT - wv + 3) / 4 : 0);
+  int8_t* const pad = lds + SB - 256;  // pad line of stage 0 (never read)
+
+  // This wave's column tiles [c0, c0 + nct)
+  const int c0 = part * CT / nparts, nct = (part + 1) * CT / nparts - c0;
+
+  v16i acc[2][CTW];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int c = 0; c < CTW; ++c) acc[x][c] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+
+  const int row_mine = gm * 64 + (tid & 63);
+  const float adq_mine = p.a_dq[min(row_mine, p.Mb * 32 - 1)];
+  const int32_t rs_mine = p.rowsum[min(row_mine, p.M - 1)];
+#pragma unroll
+  for (int k = 0; k < ST; ++k)
+    if (k < KS) wide_issue<PW>(lds + k * SB, pad, src, step, nreal, k, wv);
+  BTL_TRACE_AT(0);
+#ifdef BTL_TRACE
+  if (tid == 0 && blockIdx.x < (unsigned)kTraceBlocks) g_trace[blockIdx.x][15][0] = __builtin_amdgcn_s_memtime();
+#endif
+  wide_dispatch<CTW, CTW, WQ>(nct, acc, lds, pad, src, step, nreal, KS, wv, qg, (8 + c0) * 1024, lane);
+  BTL_TRACE_AT(13);
+#ifdef BTL_TRACE
+  if (tid == 0 && blockIdx.x < (unsigned)kTraceBlocks) g_trace[blockIdx.x][15][13] = __builtin_amdgcn_s_memtime();
+#endif
+
+  if (tid < 64) {
+    s_adq[tid] = adq_mine;
+    s_rs[tid] = rs_mine;
+  }
+  if (tid < CT) s_sw[tid] = seg_scale_of(p, min(gn * CT + tid, p.NT - 1) * 32);
+  __syncthreads();  // every wave is done with the stage buffers
+  int32_t* const R = reinterpret_cast<int32_t*>(lds);
+  const int nch = CT * 4;  // 16-byte output chunks per row
+  const float inv_nch = 1.0f / (float)nch;
+  const int n_cols = p.NT * 32;
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    // chunk k = tid + 256 j: row il = k / nch (exact in float: k < 2^13,
+    // nch <= 256), column chunk cc = k - il * nch
+    int il_[KPT], cc_[KPT];
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int k = tid + 256 * j;
+      il_[j] = (int)(((float)k + 0.5f) * inv_nch);
+      cc_[j] = k - il_[j] * nch;
+    }
+    uint4 res[KPT];
+    if (p.residual) {
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const int i = min(gm * 64 + x * 32 + il_[j], p.M - 1);
+        const int col = min(gn * CT * 32 + cc_[j] * 8, n_cols - 8);
+        res[j] = il_[j] < 32 ? *reinterpret_cast<const uint4*>(p.residual + (int64_t)i * p.n_out + col)
+                             : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+    if (x) __syncthreads();  // the previous row block's sums have been read
+    if (qg == 0) {
+#pragma unroll
+      for (int c = 0; c < CTW; ++c)
+        if (c < nct)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) R[(c0 + c) * kWideResWords + r * 64 + lane] = acc[x][c][r];
+    }
+    if (WQ > 1) {
+      __syncthreads();
+      if (qg != 0) {
+#pragma unroll
+        for (int c = 0; c < CTW; ++c)
+          if (c < nct)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) atomicAdd(&R[(c0 + c) * kWideResWords + r * 64 + lane], acc[x][c][r]);
+      }
+    }
+    __syncthreads();
+    if (x == 0) BTL_TRACE_AT(11);
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int il = il_[j], cc = cc_[j], ct = cc >> 2, jq = cc & 3;
+      if (il >= 32) break;
+      const int i = gm * 64 + x * 32 + il;
+      const int col = (gn * CT + ct) * 32 + jq * 8;
+      if (i >= p.M || col >= n_cols) continue;
+      // row il of the block: lane half (il >> 2) & 1, register 4 (il >> 3) + (il & 3)
+      const int32_t* s = R + ct * kWideResWords + (((il >> 3) << 2) | (il & 3)) * 64 + ((il >> 2) & 1) * 32 + jq * 8;
+      const v4i v0 = *reinterpret_cast<const v4i*>(s);
+      const v4i v1 = *reinterpret_cast<const v4i*>(s + 4);
+      const int32_t rs = s_rs[x * 32 + il];
+      const float f = s_sw[ct] * s_adq[x * 32 + il];
+      const int32_t e[8] = {v0.x - rs, v0.y - rs, v0.z - rs, v0.w - rs, v1.x - rs, v1.y - rs, v1.z - rs, v1.w - rs};
+      uint32_t o[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) o[h] = f2bf_pair((float)e[2 * h] * f, (float)e[2 * h + 1] * f);
+      if (p.acc_out) {
+        int32_t* const ao = p.acc_out + (int64_t)i * p.N + col;
+        *reinterpret_cast<v4i*>(ao) = (v4i){e[0], e[1], e[2], e[3]};
+        *reinterpret_cast<v4i*>(ao + 4) = (v4i){e[4], e[5], e[6], e[7]};
+      }
+      if (p.residual) {
+        const uint32_t rw[4] = {res[j].x, res[j].y, res[j].z, res[j].w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const uint32_t lo = f2bf(bf2f((uint16_t)(rw[h] & 0xffffu)) + bf2f((uint16_t)(o[h] & 0xffffu)));
+          const uint32_t hi = f2bf(bf2f((uint16_t)(rw[h] >> 16)) + bf2f((uint16_t)(o[h] >> 16)));
+          o[h] = lo | (hi << 16);
+        }
+      }
+      *reinterpret_cast<uint4*>(p.out + (int64_t)i * p.n_out + col) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+  BTL_TRACE_AT(14);
+}
+
 // ------------------------------------------------------------- planning --
 // Waves per standalone decode workgroup: 8 (two per SIMD) unless
 // BTL_DECODE_WAVES=4.  The fused kernel always runs 8.
@@ -1146,6 +1455,86 @@ static GemmArgs gemm_args(const int8_t* xa, const float* a_dq, const int32_t* ro
   return a;
 }
 
+// Wide-tile plan (k_gemm_wide): 64-row tiles and CT column tiles, about two
+// tiles per CU; WQ the split (1, 2 or 4 k-step groups) whose busiest wave has
+// the fewest MFMAs (ties: the smaller WQ, fewer partial sums), CTW the
+// largest wave range rounded up to an instantiated size (2, 3, 5; WQ = 1:
+// 2, 3, 4).  Used for the scale epilogue with the row sums given, from M = 256,
+// while the ranges fit (N <= 8192 at M = 2048); BTL_PREFILL_WIDE=0 turns it
+// off (the 128x256 / 64x256 kernel then runs).
+struct WidePlan {
+  int ngm, ngn, ct, ctw, wq;
+};
+// k-step x column-tile MFMA pairs per superblock of the busiest wave, and the
+// largest wave range, for CT tiles split the k_gemm_wide way.
+static int wide_simd_load(int ct, int wq, int* ctw) {
+  const int parts = 4 / wq, span = (ct + parts - 1) / parts;
+  *ctw = span;
+  return span * (4 / wq);
+}
+template <int WQ>
+static int wide_ctfit_wq(int ctw) {
+  return ctw <= 2 ? WideShape<2, WQ>::ctfit
+                  : (ctw == 3 ? WideShape<3, WQ>::ctfit : WideShape<WQ == 1 ? 4 : 5, WQ>::ctfit);
+}
+static int wide_ctfit(int wq, int ctw) {
+  return wq == 4 ? wide_ctfit_wq<4>(ctw) : (wq == 2 ? wide_ctfit_wq<2>(ctw) : wide_ctfit_wq<1>(ctw));
+}
+static bool wide_plan(int64_t M, int64_t K, int64_t N, int epilogue, bool prs, WidePlan* w) {
+  const char* e = getenv("BTL_PREFILL_WIDE");
+  if (e && e[0] == '0') return false;
+  if (epilogue != BTL_EPI_SCALE || !prs || M < 256) return false;
+  const int Mb = (int)mblocks(M), NT = (int)(N / 32);
+  const int cus = device_cus();
+  w->ngm = (Mb + 1) / 2;
+  if (w->ngm > 2 * cus) return false;
+  const int ngn_t = 2 * cus / w->ngm;
+  w->ct = (NT + ngn_t - 1) / ngn_t;
+  if (w->ct > 40) return false;
+  w->ngn = (NT + w->ct - 1) / w->ct;
+  // A grid well short of two tiles per CU with a long K runs faster as the
+  // split-K 64-row tiles (measured on MI355X at M = 512, K = 6912, N = 2560:
+  // 320 wide tiles 23.0-24.5 us, 64x256 tiles split in 3 22.0 us).
+  if (w->ngm * w->ngn * 2 < 3 * cus && ksb(K) > 32) return false;
+  int best = -1;
+  for (int wq = 1; wq <= 4; wq *= 2) {
+    int need;
+    const int load = wide_simd_load(w->ct, wq, &need);
+    // instantiated: CTW 2..5 (WQ = 1: 2..4; five tiles a wave with four
+    // k-steps of operands held twice would spill)
+    if (need > (wq == 1 ? 4 : 5) || w->ct > wide_ctfit(wq, need < 2 ? 2 : (need == 4 && wq != 1 ? 5 : need)))
+      continue;
+    if (best < 0 || load < best) {
+      best = load;
+      w->wq = wq;
+      w->ctw = need < 2 ? 2 : (need == 4 && wq != 1 ? 5 : need);
+    }
+  }
+  return best >= 0;
+}
+
+template <int WQ>
+static void launch_wide_wq(int ctw, dim3 grid, hipStream_t s, const GemmArgs& a, int ngm, int ngn, int ct) {
+  switch (ctw) {
+    case 2: hipLaunchKernelGGL((k_gemm_wide<2, WQ>), grid, dim3(256), 0, s, a, ngm, ngn, ct); break;
+    case 3: hipLaunchKernelGGL((k_gemm_wide<3, WQ>), grid, dim3(256), 0, s, a, ngm, ngn, ct); break;
+    default:  // 4 (WQ = 1) or 5; the plan never takes four tiles with WQ = 2 or 4
+      hipLaunchKernelGGL((k_gemm_wide<WQ == 1 ? 4 : 5, WQ>), grid, dim3(256), 0, s, a, ngm, ngn, ct);
+      break;
+  }
+}
+
+static void launch_wide(const WidePlan& w, hipStream_t s, const GemmArgs& a) {
+  const int per = (w.ngm * w.ngn + kPfXcds - 1) / kPfXcds;
+  const dim3 grid((unsigned)(per * kPfXcds));
+  if (w.wq == 4)
+    launch_wide_wq<4>(w.ctw, grid, s, a, w.ngm, w.ngn, w.ct);
+  else if (w.wq == 2)
+    launch_wide_wq<2>(w.ctw, grid, s, a, w.ngm, w.ngn, w.ct);
+  else
+    launch_wide_wq<1>(w.ctw, grid, s, a, w.ngm, w.ngn, w.ct);
+}
+
 template <int EPI>
 static void launch_prefill_epi(bool prs, int rb, bool sk, dim3 grid, hipStream_t s, const GemmArgs& a, int ngm,
                                int ngn) {
@@ -1165,6 +1554,12 @@ static void launch_prefill_epi(bool prs, int rb, bool sk, dim3 grid, hipStream_t
 
 static int launch_gemm(const GemmArgs& a, int epilogue, const GemmPlan& pl, hipStream_t s) {
   if (pl.prefill) {
+    WidePlan w;
+    const int64_t K = (int64_t)a.KS * 128;
+    if (wide_plan(a.M, K, a.N, epilogue, a.rowsum != nullptr, &w) && aligned(a.acc_out, 16)) {
+      launch_wide(w, s, a);
+      return check_launch("ternary gemm (prefill, wide tiles)");
+    }
     const PfGrid g = pf_grid(a.M, (int64_t)a.KS * 128, a.N, epilogue);
     const int ngm = g.ngm, ngn = g.ngn, rb = g.rb;
     // split-K runs with the given row sums (partials are raw sums; the row sum
@@ -1376,6 +1771,24 @@ static int bitlinear_fused_impl(const uint16_t* x, int64_t M, int64_t K, int64_t
 using namespace btl;
 
 extern "C" {
+
+int btl_gemm_tiling(int64_t M, int64_t K, int64_t N, int epilogue, int rowsum_given, int32_t* info) {
+  if (!info) return set_error(BTL_ERR_NULL, "btl_gemm_tiling: info is NULL");
+  if (M <= 0 || K <= 0 || N <= 0 || N % 32 || K % 32)
+    return set_error(BTL_ERR_SHAPE, "btl_gemm_tiling: M=%lld K=%lld N=%lld", (long long)M, (long long)K, (long long)N);
+  for (int i = 0; i < 6; ++i) info[i] = 0;
+  WidePlan w;
+  if (M <= 32) {
+    const GemmPlan pl = plan_gemm(M, K, N, epilogue, 0);
+    info[0] = 0, info[1] = 32, info[2] = pl.tpw, info[3] = pl.splitk;
+  } else if (wide_plan(M, K, N, epilogue, rowsum_given != 0, &w)) {
+    info[0] = 2, info[1] = 64, info[2] = w.ct, info[3] = 1, info[4] = w.wq, info[5] = w.ctw;
+  } else {
+    const PfGrid g = pf_grid(M, K, N, epilogue);
+    info[0] = 1, info[1] = g.rb * 32, info[2] = kPfCT, info[3] = rowsum_given ? g.splitk : 1;
+  }
+  return BTL_OK;
+}
 
 int btl_choose_splitk(int64_t M, int64_t K, int64_t N, int epilogue) {
   if (M <= 0 || K <= 0 || N <= 0 || N % 32) return 0;

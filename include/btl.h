@@ -75,6 +75,13 @@ int64_t btl_packed_dram_bytes(int64_t in_features, int64_t out_features);
 int64_t btl_devlayout_words(int64_t K, int64_t N);
 int64_t btl_act_bytes(int64_t M, int64_t K);
 int btl_choose_splitk(int64_t M, int64_t K, int64_t N, int epilogue);
+/* The tiling btl_gemm_i8t2 runs for a shape (no counterpart in the reference:
+ * a planning query for benchmarks and tests).  rowsum_given: the caller
+ * passes the row sums (the prefill BitLinear does).  info[6] = {kind (0
+ * decode, 1 prefill 128x256 / 64x256 tiles, 2 prefill wide tiles), rows per
+ * tile, column tiles of 32 per tile (kind 1: slots; relu2 pairs gate and up),
+ * split-K factor, k-step groups (kind 2), column tiles per wave (kind 2)}.  */
+int btl_gemm_tiling(int64_t M, int64_t K, int64_t N, int epilogue, int rowsum_given, int32_t* info);
 int64_t btl_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int epilogue, int splitk);
 int64_t btl_fused_workspace_bytes(int64_t M, int64_t K, int64_t N, int epilogue, int splitk);
 

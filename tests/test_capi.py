@@ -67,6 +67,24 @@ def test_split_k_plans(L):
     assert L.btl_choose_splitk(32, 256, 64, 0) == 1
 
 
+def test_gemm_tiling_query(L):
+    t = N.gemm_tiling
+    # 2048 x 2560 -> N on 256 CUs: 64-row tiles, 16 column groups (two tiles a CU)
+    assert t(2048, 2560, 6912) == {"kind": "wide", "rows": 64, "col_tiles": 14, "splitk": 1, "k_groups": 1,
+                                   "tiles_per_wave": 4}
+    assert t(2048, 2560, 2560) == {"kind": "wide", "rows": 64, "col_tiles": 5, "splitk": 1, "k_groups": 4,
+                                   "tiles_per_wave": 5}
+    assert t(512, 2560, 3840)["col_tiles"] == 2
+    # without row sums, for relu2 and below 256 rows: the 128x256 / 64x256 tiles
+    assert t(2048, 2560, 6912, rowsum_given=False)["kind"] == "tiles"
+    assert t(2048, 2560, 13824, N.EPI_RELU2_MUL)["kind"] == "tiles"
+    assert t(100, 1536, 160)["kind"] == "tiles" and t(100, 1536, 160)["splitk"] > 1
+    assert t(32, 2560, 3840) == {"kind": "decode", "rows": 32, "col_tiles": 1, "splitk": 2, "k_groups": 0,
+                                 "tiles_per_wave": 0}
+    with pytest.raises(RuntimeError):
+        t(64, 100, 64)
+
+
 FAKE = 0x100000  # never dereferenced: every call below is rejected first
 
 

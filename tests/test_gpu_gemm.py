@@ -272,6 +272,49 @@ def test_prefill_full_size_properties(orc, m, k, n, epi, rowsum):
     assert np.array_equal(out[rows], exp_rows)
 
 
+# Wide-tile prefill (64-row x CT-column tiles, about two per CU; with the row
+# sums given, scale epilogue, M >= 256).  The planner's choice on 256 CUs is
+# listed per shape as (CT, tiles per wave CTW, k-step groups WQ); together
+# they run every instantiated (CTW, WQ) pair, a ragged last row tile
+# (M % 64 != 0), a ragged last column group (NT % CT != 0), K not a multiple
+# of 128 and fewer superblocks than pipeline stages.
+WIDE_SHAPES = [  # m, k, n, (CT, CTW, WQ)
+    (300, 640, 2560, (1, 2, 4)),    # 5 superblocks, last row tile 44 rows
+    (512, 384, 3840, (2, 2, 2)),    # 3 superblocks
+    (1024, 2560, 2560, (3, 3, 4)),  # last column group 2 tiles
+    (512, 992, 6912, (4, 2, 1)),    # last superblock 96 deep
+    (2048, 2560, 2560, (5, 5, 4)),
+    (2048, 512, 3072, (6, 3, 2)),
+    (1000, 512, 6912, (7, 2, 1)),   # last row tile 40 rows, last column group 6 tiles
+    (2048, 256, 5120, (10, 5, 2)),
+    (2048, 256, 6144, (12, 3, 1)),
+    (2000, 1056, 6880, (14, 4, 1)),  # last column group 5 tiles, last row tile 16 rows
+]
+
+
+@pytest.mark.parametrize("m,k,n,plan", WIDE_SHAPES)
+def test_prefill_wide_tiles(orc, m, k, n, plan):
+    """Sampled rows exact (accumulators and bf16 with a residual and three
+    weight-scale segments), every row and column checksum exact."""
+    t = N.gemm_tiling(m, k, n)
+    assert (t["kind"], t["col_tiles"], t["tiles_per_wave"], t["k_groups"]) == ("wide", *plan), t
+    print(f"prefill wide m={m} k={k} n={n} tiling={t}", flush=True)
+    rng = np.random.default_rng(m * 5 + k + n)
+    q = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
+    w = H.ternary(k, n, seed=k * 3 + n)
+    ends = [n // 4 - n // 4 % 32, n // 2 - n // 2 % 32, n]
+    scales = [0.013, 0.029, 0.021]
+    res = orc.f32_to_bf16(rng.standard_normal((m, n)).astype(np.float32))
+    acc, out, a_dq, _ = run_gemm(orc, q, w, scales, ends, residual_bits=res, rowsum=True)
+    rows = np.unique(np.concatenate([[0, m - 1], rng.choice(m, 22, replace=False)]))
+    ref_rows = orc.gemm_i8t(np.ascontiguousarray(q[rows]), w)
+    assert np.array_equal(acc[rows], ref_rows)
+    q64, w64 = q.astype(np.int64), w.astype(np.int64)
+    assert np.array_equal(acc.astype(np.int64).sum(1), q64 @ w64.sum(1))
+    assert np.array_equal(acc.astype(np.int64).sum(0), q64.sum(0) @ w64)
+    assert np.array_equal(out[rows], expected_out(orc, ref_rows, a_dq[rows], scales, ends, 0, res[rows]))
+
+
 @pytest.mark.parametrize("m", [512, 2048])
 def test_prefill_gate_up_relu2_through_ternary_matmul(orc, m):
     """Prefill gate||up as the layer runs it: ternary_matmul (RMSNorm +
