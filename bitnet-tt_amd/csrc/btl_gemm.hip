@@ -1048,6 +1048,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_wide(GemmArgs p, int ngm, int n
   const int gm = grp * kWideGroupRows + rt % rows_in;
   const int gn = rt / rows_in;
   const int KS = p.KS;
+  const int CTg = min(CT, p.NT - gn * CT);  // this tile's column tiles (the last group may have fewer)
 
   // Sources: i = 0, 1 the activation chunk of row block i, k-step wv; i >= 2
   // weight tile wv + 4 (i - 2) of the tile (clamped into the matrix).
@@ -1065,11 +1066,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_wide(GemmArgs p, int ngm, int n
       step[i] = 1024;
     }
   }
-  const int nreal = 2 + (CT > wv ? (CT - wv + 3) / 4 : 0);
+  const int nreal = 2 + (CTg > wv ? (CTg - wv + 3) / 4 : 0);
   int8_t* const pad = lds + SB - 256;  // pad line of stage 0 (never read)
 
   // This wave's column tiles [c0, c0 + nct)
-  const int c0 = part * CT / nparts, nct = (part + 1) * CT / nparts - c0;
+  const int c0 = part * CTg / nparts, nct = (part + 1) * CTg / nparts - c0;
 
   v16i acc[2][CTW];
 #pragma unroll
@@ -1097,10 +1098,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_wide(GemmArgs p, int ngm, int n
     s_adq[tid] = adq_mine;
     s_rs[tid] = rs_mine;
   }
-  if (tid < CT) s_sw[tid] = seg_scale_of(p, min(gn * CT + tid, p.NT - 1) * 32);
+  if (tid < CTg) s_sw[tid] = seg_scale_of(p, (gn * CT + tid) * 32);
   __syncthreads();  // every wave is done with the stage buffers
   int32_t* const R = reinterpret_cast<int32_t*>(lds);
-  const int nch = CT * 4;  // 16-byte output chunks per row
+  const int nch = CTg * 4;  // 16-byte output chunks per row
   const float inv_nch = 1.0f / (float)nch;
   const int n_cols = p.NT * 32;
 #pragma unroll
