@@ -1,6 +1,7 @@
-// Standalone activation prologue kernel: one workgroup (256 threads) per
-// token row, running the row computation of btl_act_row.h (RMSNorm, absmax
-// int8 quantisation, blocked operand layout).  The fused decode kernel in
+// Standalone activation prologue kernels: one wave per token row for the
+// quantising prologue of large batches of rows up to 8192 long, else one
+// workgroup of 512 threads per row running the row computation of
+// btl_act_row.h (RMSNorm, absmax int8 quantisation, blocked operand layout).  The fused decode kernel in
 // btl_gemm.hip runs the same row computation inside the GEMM launch.
 #include "btl_act_row.h"
 
@@ -11,8 +12,149 @@ __global__ __launch_bounds__(kActThreads) void k_act_rows(ActArgs p) {
   act_row<NORM, QUANT, false, CPT>(p, blockIdx.x, threadIdx.x);
 }
 
+// The quantising prologue with one wave per row, four rows a workgroup:
+// every row of a prefill batch in flight at once, no barrier, no LDS (the
+// 512-thread row above spends most of its time in two block reductions and
+// runs a few hundred rows at a time).  The wave plays the eight waves of
+// act_row in turn: lane l holds the chunks of threads l, l + 64, ..., l + 448
+// of that row, so the sum of squares runs the same per-thread order, the same
+// 64-lane butterfly per (virtual) wave and the same fixed combination of the
+// eight wave sums -- bit for bit the statistic act_row computes.  The maximum
+// and the row sum do not depend on the order.  Rows past M and columns past K
+// are written as zeros, as act_row writes them.
+constexpr int kActRowWaves = 4;
+template <bool NORM, int CPT>
+__global__ __launch_bounds__(64 * kActRowWaves) void k_act_rows_wave(ActArgs p) {
+  constexpr int NV = kActWaves;  // the 512-thread row's waves
+  const int lane = threadIdx.x & 63;
+  // Workgroup b runs on XCD b % 8; XCD x takes a contiguous range of rows, so
+  // the 32 rows of a row block, whose quantised bytes interleave in 16-byte
+  // pieces, meet in one L2 instead of leaving partial lines in eight.
+  const int per = (gridDim.x + 7) / 8;
+  const int v = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (v >= (int)gridDim.x) return;
+  const int m = v * kActRowWaves + (threadIdx.x >> 6);
+  const int nch = p.K >> 3, nchp = p.KS * 16;
+  if (p.zero_words && m == 0)
+    for (int i = lane; i < p.n_zero_words; i += 64) p.zero_words[i] = 0u;
+  if (m >= p.M) {  // padding row of the last 32-row block
+    for (int c = lane; c < nchp; c += 64) store8<false>(p.xa + xa_offset(m, 8 * c, p.KS), 0u, 0u);
+    if (lane == 0) {
+      p.a_dq[m] = 0.0f;
+      if (p.rowsum) p.rowsum[m] = 0;
+    }
+    return;
+  }
+  const uint16_t* xr = p.x + (int64_t)m * p.ldx;
+  // chunk of (virtual wave w, i): c = 64 w + lane + 512 i
+  uint4 y[CPT][NV], graw[CPT][NV];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i)
+#pragma unroll
+    for (int w = 0; w < NV; ++w) {
+      const int c = 64 * w + lane + kActThreads * i;
+      y[i][w] = c < nch ? *reinterpret_cast<const uint4*>(xr + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
+      graw[i][w] = make_uint4(0u, 0u, 0u, 0u);
+      if (NORM && p.gamma && c < nch) graw[i][w] = *reinterpret_cast<const uint4*>(p.gamma + 8 * c);
+    }
+  if (NORM) {
+    float ws[NV];
+#pragma unroll
+    for (int w = 0; w < NV; ++w) {
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const uint32_t w4[4] = {y[i][w].x, y[i][w].y, y[i][w].z, y[i][w].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {  // elements 2j, 2j+1 in order; zero chunks add zeros
+          const float a = bf_lo(w4[j]), b = bf_hi(w4[j]);
+          s = s + a * a;
+          s = s + b * b;
+        }
+      }
+      ws[w] = wave_xor_sum(s);
+    }
+    const float r = 1.0f / sqrtf(sum8_fixed(ws) / (float)p.K + p.norm_eps);
+    // y = bf16(gamma * bf16(x * r)) (bf16(x * r) without gamma), kept as bf16 pairs
+#pragma unroll
+    for (int i = 0; i < CPT; ++i)
+#pragma unroll
+      for (int w = 0; w < NV; ++w) {
+        uint32_t w4[4] = {y[i][w].x, y[i][w].y, y[i][w].z, y[i][w].w};
+        const uint32_t g4[4] = {graw[i][w].x, graw[i][w].y, graw[i][w].z, graw[i][w].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t t = f2bf_pair(bf_lo(w4[j]) * r, bf_hi(w4[j]) * r);
+          w4[j] = p.gamma ? f2bf_pair(bf_lo(g4[j]) * bf_lo(t), bf_hi(g4[j]) * bf_hi(t)) : t;
+        }
+        y[i][w] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+      }
+  }
+  // a = max(max|y|, act_eps), as act_row takes it (fmaxf within the lane,
+  // then the bit patterns across lanes)
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i)
+#pragma unroll
+    for (int w = 0; w < NV; ++w) {
+      const uint32_t w4[4] = {y[i][w].x, y[i][w].y, y[i][w].z, y[i][w].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) amax = fmaxf(fmaxf(amax, fabsf(bf_lo(w4[j]))), fabsf(bf_hi(w4[j])));
+    }
+  uint32_t u = __float_as_uint(amax);
+  u = max(u, xor_partner_u<32>(u));
+  u = max(u, xor_partner_u<16>(u));
+  u = max(u, xor_partner_u<8>(u));
+  u = max(u, xor_partner_u<4>(u));
+  u = max(u, xor_partner_u<2>(u));
+  u = max(u, xor_partner_u<1>(u));
+  const float amx = __uint_as_float(u);
+  const float a = amx > p.act_eps ? amx : p.act_eps;
+  const float scale = 127.0f / a;
+  if (lane == 0) {
+    p.a_dq[m] = a / 127.0f;
+    if (p.act_scale) p.act_scale[m] = scale;
+  }
+  int rs = 0;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i)
+#pragma unroll
+    for (int w = 0; w < NV; ++w) {
+      const int c = 64 * w + lane + kActThreads * i;
+      if (c < nch) {
+        const uint32_t w4[4] = {y[i][w].x, y[i][w].y, y[i][w].z, y[i][w].w};
+        const float v[8] = {bf_lo(w4[0]), bf_hi(w4[0]), bf_lo(w4[1]), bf_hi(w4[1]),
+                            bf_lo(w4[2]), bf_hi(w4[2]), bf_lo(w4[3]), bf_hi(w4[3])};
+        uint32_t lo, hi;
+        quant8(v, scale, lo, hi, rs);
+        store_chunk<false>(p.xa, m, c, p.KS, lo, hi);
+        if (p.xq_rm) *reinterpret_cast<uint2*>(p.xq_rm + (int64_t)m * p.K + 8 * c) = make_uint2(lo, hi);
+        if (p.y_rm) *reinterpret_cast<uint4*>(p.y_rm + (int64_t)m * p.K + 8 * c) = y[i][w];
+      }
+    }
+  for (int c = nch + lane; c < nchp; c += 64) store8<false>(p.xa + xa_offset(m, 8 * c, p.KS), 0u, 0u);
+  if (!p.rowsum) return;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) rs += __shfl_xor(rs, off, 64);
+  if (lane == 0) p.rowsum[m] = rs;
+}
+
 template <bool NORM, bool QUANT>
 static void launch_rows(unsigned rows, hipStream_t s, const ActArgs& p) {
+  // rows is a multiple of 32 (whole row blocks) when quantising.  One wave
+  // per row from 1024 rows (measured on MI355X, M = 2048: K = 2560 10.6 ->
+  // 9.5 us, K = 6912 17.9 -> 14.3 us); at 512 rows the 512-thread row is as
+  // fast (K = 2560) or faster (K = 6912: 7.7 against 9.2 us): a wave per row
+  // then leaves two waves per CU to hide the load latency.
+  if (QUANT && act_cpt(p.K) <= 2 && rows >= 1024) {
+    const unsigned wgs = rows / kActRowWaves;
+    const dim3 grid(wgs), block(64 * kActRowWaves);
+    if (act_cpt(p.K) == 1)
+      hipLaunchKernelGGL((k_act_rows_wave<NORM, 1>), grid, block, 0, s, p);
+    else
+      hipLaunchKernelGGL((k_act_rows_wave<NORM, 2>), grid, block, 0, s, p);
+    return;
+  }
   switch (act_cpt(p.K)) {
     case 1: hipLaunchKernelGGL((k_act_rows<NORM, QUANT, 1>), dim3(rows), dim3(kActThreads), 0, s, p); break;
     case 2: hipLaunchKernelGGL((k_act_rows<NORM, QUANT, 2>), dim3(rows), dim3(kActThreads), 0, s, p); break;

@@ -33,7 +33,10 @@ def run_quant(m, k, xb, gb=None, eps=1e-5):
                 scale=scale.cpu().numpy(), xq=xq.cpu().numpy(), y=H.bits_of(y))
 
 
-@pytest.mark.parametrize("m,k", [(1, 32), (5, 256), (32, 2560), (33, 2560), (70, 640), (32, 6912), (3, 16384)])
+# From 1024 rows (K <= 8192) the prologue runs one wave per row: (1000, 2560)
+# and (1100, 6912) take that kernel, with padding rows in the last row block.
+@pytest.mark.parametrize("m,k", [(1, 32), (5, 256), (32, 2560), (33, 2560), (70, 640), (32, 6912), (3, 16384),
+                                 (1000, 2560), (1100, 6912)])
 @pytest.mark.parametrize("norm", [False, True])
 def test_quant_absmax_bit_exact(orc, m, k, norm):
     print(f"quant m={m} k={k} norm={norm}", flush=True)
