@@ -315,6 +315,26 @@ def test_prefill_wide_tiles(orc, m, k, n, plan):
     assert np.array_equal(out[rows], expected_out(orc, ref_rows, a_dq[rows], scales, ends, 0, res[rows]))
 
 
+@pytest.mark.parametrize("m,k,n", [(2048, 2560, 3072), (1000, 512, 6912), (512, 1024, 2560)])
+def test_prefill_tilings_agree(orc, m, k, n, monkeypatch):
+    """The wide tiles and the 128x256 / 64x256 tiles (BTL_PREFILL_WIDE=0,
+    read at every call) give the same accumulators and the same bf16 outputs,
+    residual and three weight-scale segments included."""
+    rng = np.random.default_rng(m + 11 * n)
+    q = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
+    w = H.ternary(k, n, seed=n + 3)
+    ends = [n // 4 - n // 4 % 32, n // 2 - n // 2 % 32, n]
+    scales = [0.013, 0.029, 0.021]
+    res = orc.f32_to_bf16(rng.standard_normal((m, n)).astype(np.float32))
+    assert N.gemm_tiling(m, k, n)["kind"] == "wide"
+    acc_w, out_w, _, _ = run_gemm(orc, q, w, scales, ends, residual_bits=res, rowsum=True)
+    monkeypatch.setenv("BTL_PREFILL_WIDE", "0")
+    assert N.gemm_tiling(m, k, n)["kind"] == "tiles"
+    acc_t, out_t, _, _ = run_gemm(orc, q, w, scales, ends, residual_bits=res, rowsum=True)
+    assert np.array_equal(acc_w, acc_t)
+    assert np.array_equal(out_w, out_t)
+
+
 @pytest.mark.parametrize("m", [512, 2048])
 def test_prefill_gate_up_relu2_through_ternary_matmul(orc, m):
     """Prefill gate||up as the layer runs it: ternary_matmul (RMSNorm +
