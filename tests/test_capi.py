@@ -34,7 +34,7 @@ def test_library_loads_and_exports_every_declaration(L):
         assert hasattr(L, name), f"{name} declared in include/btl.h but not exported"
         assert name in N.EXPORTS, f"{name} has no ctypes signature"
     assert set(N.EXPORTS) == set(names)
-    assert L.btl_version() == 100
+    assert L.btl_version() == 101
     assert L.btl_fused_error_offset() % 4 == 0 and 0 < L.btl_fused_error_offset() < 8192
 
 
