@@ -1,5 +1,5 @@
-// Standalone activation prologue kernels: one wave per token row for the
-// quantising prologue of large batches of rows up to 8192 long, else one
+// Standalone activation prologue kernels: one or two waves per token row for
+// the quantising prologue of batches of rows up to 8192 long, else one
 // workgroup of 512 threads per row running the row computation of
 // btl_act_row.h (RMSNorm, absmax int8 quantisation, blocked operand layout).  The fused decode kernel in
 // btl_gemm.hip runs the same row computation inside the GEMM launch.
@@ -12,59 +12,68 @@ __global__ __launch_bounds__(kActThreads) void k_act_rows(ActArgs p) {
   act_row<NORM, QUANT, false, CPT>(p, blockIdx.x, threadIdx.x);
 }
 
-// The quantising prologue with one wave per row, four rows a workgroup:
-// every row of a prefill batch in flight at once, no barrier, no LDS (the
-// 512-thread row above spends most of its time in two block reductions and
-// runs a few hundred rows at a time).  The wave plays the eight waves of
+// The quantising prologue with one wave per row (four rows a workgroup) or
+// two (two rows): every row of a prefill batch in flight at once, with no
+// barrier (one wave) or a barrier between two waves (the 512-thread row above
+// spends most of its time in two block reductions over eight waves and runs a
+// few hundred rows at a time).  The wave plays the eight waves of
 // act_row in turn: lane l holds the chunks of threads l, l + 64, ..., l + 448
 // of that row, so the sum of squares runs the same per-thread order, the same
 // 64-lane butterfly per (virtual) wave and the same fixed combination of the
 // eight wave sums -- bit for bit the statistic act_row computes.  The maximum
 // and the row sum do not depend on the order.  Rows past M and columns past K
 // are written as zeros, as act_row writes them.
-constexpr int kActRowWaves = 4;
-template <bool NORM, int CPT>
+constexpr int kActRowWaves = 4;  // waves a workgroup
+// WPR waves per row (1 or 2): wave h of a row takes the virtual waves
+// h * 8 / WPR .. and the two meet in LDS for the three row statistics.
+template <bool NORM, int CPT, int WPR>
 __global__ __launch_bounds__(64 * kActRowWaves) void k_act_rows_wave(ActArgs p) {
   constexpr int NV = kActWaves;  // the 512-thread row's waves
-  const int lane = threadIdx.x & 63;
+  constexpr int NL = NV / WPR;   // of them on this wave
+  constexpr int RPW = kActRowWaves / WPR;
+  __shared__ float s_ws[RPW][NV];
+  __shared__ uint32_t s_mx[RPW][WPR];
+  __shared__ int s_rsum[RPW][WPR];
+  const int lane = threadIdx.x & 63, wi = threadIdx.x >> 6, r = wi / WPR, h = wi % WPR;
   // Workgroup b runs on XCD b % 8; XCD x takes a contiguous range of rows, so
   // the 32 rows of a row block, whose quantised bytes interleave in 16-byte
   // pieces, meet in one L2 instead of leaving partial lines in eight.
   const int per = (gridDim.x + 7) / 8;
   const int v = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
   if (v >= (int)gridDim.x) return;
-  const int m = v * kActRowWaves + (threadIdx.x >> 6);
+  const int m = v * RPW + r;
   const int nch = p.K >> 3, nchp = p.KS * 16;
-  if (p.zero_words && m == 0)
+  const bool pad = m >= p.M;  // padding row of the last 32-row block
+  if (p.zero_words && m == 0 && h == 0)
     for (int i = lane; i < p.n_zero_words; i += 64) p.zero_words[i] = 0u;
-  if (m >= p.M) {  // padding row of the last 32-row block
-    for (int c = lane; c < nchp; c += 64) store8<false>(p.xa + xa_offset(m, 8 * c, p.KS), 0u, 0u);
-    if (lane == 0) {
+  if (pad) {
+    for (int c = h * 64 + lane; c < nchp; c += 64 * WPR) store8<false>(p.xa + xa_offset(m, 8 * c, p.KS), 0u, 0u);
+    if (lane == 0 && h == 0) {
       p.a_dq[m] = 0.0f;
       if (p.rowsum) p.rowsum[m] = 0;
     }
-    return;
+    if (WPR == 1) return;  // with two waves a row it still takes part in the barriers
   }
   const uint16_t* xr = p.x + (int64_t)m * p.ldx;
-  // chunk of (virtual wave w, i): c = 64 w + lane + 512 i
-  uint4 y[CPT][NV], graw[CPT][NV];
+  // chunk of (virtual wave w = h * NL + l, i): c = 64 w + lane + 512 i
+  uint4 y[CPT][NL], graw[CPT][NL];
 #pragma unroll
   for (int i = 0; i < CPT; ++i)
 #pragma unroll
-    for (int w = 0; w < NV; ++w) {
-      const int c = 64 * w + lane + kActThreads * i;
-      y[i][w] = c < nch ? *reinterpret_cast<const uint4*>(xr + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
-      graw[i][w] = make_uint4(0u, 0u, 0u, 0u);
-      if (NORM && p.gamma && c < nch) graw[i][w] = *reinterpret_cast<const uint4*>(p.gamma + 8 * c);
+    for (int l = 0; l < NL; ++l) {
+      const int c = 64 * (h * NL + l) + lane + kActThreads * i;
+      y[i][l] = !pad && c < nch ? *reinterpret_cast<const uint4*>(xr + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
+      graw[i][l] = make_uint4(0u, 0u, 0u, 0u);
+      if (NORM && p.gamma && !pad && c < nch) graw[i][l] = *reinterpret_cast<const uint4*>(p.gamma + 8 * c);
     }
   if (NORM) {
-    float ws[NV];
+    float ws[NL];
 #pragma unroll
-    for (int w = 0; w < NV; ++w) {
+    for (int l = 0; l < NL; ++l) {
       float s = 0.0f;
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
-        const uint32_t w4[4] = {y[i][w].x, y[i][w].y, y[i][w].z, y[i][w].w};
+        const uint32_t w4[4] = {y[i][l].x, y[i][l].y, y[i][l].z, y[i][l].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {  // elements 2j, 2j+1 in order; zero chunks add zeros
           const float a = bf_lo(w4[j]), b = bf_hi(w4[j]);
@@ -72,22 +81,32 @@ __global__ __launch_bounds__(64 * kActRowWaves) void k_act_rows_wave(ActArgs p) 
           s = s + b * b;
         }
       }
-      ws[w] = wave_xor_sum(s);
+      ws[l] = wave_xor_sum(s);
     }
-    const float r = 1.0f / sqrtf(sum8_fixed(ws) / (float)p.K + p.norm_eps);
+    float total;
+    if constexpr (WPR == 1) {
+      total = sum8_fixed(ws);
+    } else {
+      if (lane == 0)
+#pragma unroll
+        for (int l = 0; l < NL; ++l) s_ws[r][h * NL + l] = ws[l];
+      __syncthreads();
+      total = sum8_fixed(s_ws[r]);
+    }
+    const float rr = 1.0f / sqrtf(total / (float)p.K + p.norm_eps);
     // y = bf16(gamma * bf16(x * r)) (bf16(x * r) without gamma), kept as bf16 pairs
 #pragma unroll
     for (int i = 0; i < CPT; ++i)
 #pragma unroll
-      for (int w = 0; w < NV; ++w) {
-        uint32_t w4[4] = {y[i][w].x, y[i][w].y, y[i][w].z, y[i][w].w};
-        const uint32_t g4[4] = {graw[i][w].x, graw[i][w].y, graw[i][w].z, graw[i][w].w};
+      for (int l = 0; l < NL; ++l) {
+        uint32_t w4[4] = {y[i][l].x, y[i][l].y, y[i][l].z, y[i][l].w};
+        const uint32_t g4[4] = {graw[i][l].x, graw[i][l].y, graw[i][l].z, graw[i][l].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint32_t t = f2bf_pair(bf_lo(w4[j]) * r, bf_hi(w4[j]) * r);
+          const uint32_t t = f2bf_pair(bf_lo(w4[j]) * rr, bf_hi(w4[j]) * rr);
           w4[j] = p.gamma ? f2bf_pair(bf_lo(g4[j]) * bf_lo(t), bf_hi(g4[j]) * bf_hi(t)) : t;
         }
-        y[i][w] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        y[i][l] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
       }
   }
   // a = max(max|y|, act_eps), as act_row takes it (fmaxf within the lane,
@@ -96,8 +115,8 @@ __global__ __launch_bounds__(64 * kActRowWaves) void k_act_rows_wave(ActArgs p) 
 #pragma unroll
   for (int i = 0; i < CPT; ++i)
 #pragma unroll
-    for (int w = 0; w < NV; ++w) {
-      const uint32_t w4[4] = {y[i][w].x, y[i][w].y, y[i][w].z, y[i][w].w};
+    for (int l = 0; l < NL; ++l) {
+      const uint32_t w4[4] = {y[i][l].x, y[i][l].y, y[i][l].z, y[i][l].w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) amax = fmaxf(fmaxf(amax, fabsf(bf_lo(w4[j]))), fabsf(bf_hi(w4[j])));
     }
@@ -108,51 +127,71 @@ __global__ __launch_bounds__(64 * kActRowWaves) void k_act_rows_wave(ActArgs p) 
   u = max(u, xor_partner_u<4>(u));
   u = max(u, xor_partner_u<2>(u));
   u = max(u, xor_partner_u<1>(u));
+  if constexpr (WPR == 2) {
+    if (lane == 0) s_mx[r][h] = u;
+    __syncthreads();
+    u = max(s_mx[r][0], s_mx[r][1]);
+  }
   const float amx = __uint_as_float(u);
   const float a = amx > p.act_eps ? amx : p.act_eps;
   const float scale = 127.0f / a;
-  if (lane == 0) {
+  if (lane == 0 && h == 0 && !pad) {
     p.a_dq[m] = a / 127.0f;
     if (p.act_scale) p.act_scale[m] = scale;
   }
   int rs = 0;
+  if (!pad) {
 #pragma unroll
-  for (int i = 0; i < CPT; ++i)
+    for (int i = 0; i < CPT; ++i)
 #pragma unroll
-    for (int w = 0; w < NV; ++w) {
-      const int c = 64 * w + lane + kActThreads * i;
-      if (c < nch) {
-        const uint32_t w4[4] = {y[i][w].x, y[i][w].y, y[i][w].z, y[i][w].w};
-        const float v[8] = {bf_lo(w4[0]), bf_hi(w4[0]), bf_lo(w4[1]), bf_hi(w4[1]),
-                            bf_lo(w4[2]), bf_hi(w4[2]), bf_lo(w4[3]), bf_hi(w4[3])};
-        uint32_t lo, hi;
-        quant8(v, scale, lo, hi, rs);
-        store_chunk<false>(p.xa, m, c, p.KS, lo, hi);
-        if (p.xq_rm) *reinterpret_cast<uint2*>(p.xq_rm + (int64_t)m * p.K + 8 * c) = make_uint2(lo, hi);
-        if (p.y_rm) *reinterpret_cast<uint4*>(p.y_rm + (int64_t)m * p.K + 8 * c) = y[i][w];
+      for (int l = 0; l < NL; ++l) {
+        const int c = 64 * (h * NL + l) + lane + kActThreads * i;
+        if (c < nch) {
+          const uint32_t w4[4] = {y[i][l].x, y[i][l].y, y[i][l].z, y[i][l].w};
+          const float vv[8] = {bf_lo(w4[0]), bf_hi(w4[0]), bf_lo(w4[1]), bf_hi(w4[1]),
+                               bf_lo(w4[2]), bf_hi(w4[2]), bf_lo(w4[3]), bf_hi(w4[3])};
+          uint32_t lo, hi;
+          quant8(vv, scale, lo, hi, rs);
+          store_chunk<false>(p.xa, m, c, p.KS, lo, hi);
+          if (p.xq_rm) *reinterpret_cast<uint2*>(p.xq_rm + (int64_t)m * p.K + 8 * c) = make_uint2(lo, hi);
+          if (p.y_rm) *reinterpret_cast<uint4*>(p.y_rm + (int64_t)m * p.K + 8 * c) = y[i][l];
+        }
       }
-    }
-  for (int c = nch + lane; c < nchp; c += 64) store8<false>(p.xa + xa_offset(m, 8 * c, p.KS), 0u, 0u);
+    for (int c = nch + h * 64 + lane; c < nchp; c += 64 * WPR) store8<false>(p.xa + xa_offset(m, 8 * c, p.KS), 0u, 0u);
+  }
   if (!p.rowsum) return;
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) rs += __shfl_xor(rs, off, 64);
-  if (lane == 0) p.rowsum[m] = rs;
+  if constexpr (WPR == 2) {
+    if (lane == 0) s_rsum[r][h] = rs;
+    __syncthreads();
+    rs = s_rsum[r][0] + s_rsum[r][1];
+  }
+  if (lane == 0 && h == 0 && !pad) p.rowsum[m] = rs;
 }
 
 template <bool NORM, bool QUANT>
 static void launch_rows(unsigned rows, hipStream_t s, const ActArgs& p) {
   // rows is a multiple of 32 (whole row blocks) when quantising.  One wave
-  // per row from 1024 rows (measured on MI355X, M = 2048: K = 2560 10.6 ->
-  // 9.5 us, K = 6912 17.9 -> 14.3 us); at 512 rows the 512-thread row is as
-  // fast (K = 2560) or faster (K = 6912: 7.7 against 9.2 us): a wave per row
-  // then leaves two waves per CU to hide the load latency.
+  // per row from 1024 rows, two from 256, the 512-thread row below that
+  // (measured on MI355X, graph-timed: M = 2048, K = 2560 / 6912: 512-thread
+  // rows 10.6 / 17.9 us in a BitLinear sequence, one wave 9.5 / 14.3 us;
+  // M = 512: 512-thread rows 5.05 / 7.26 us, two waves 4.5 / 6.1 us, one wave
+  // 6.0 / 9.2 us; M = 100: 512-thread rows 3.6 us, two waves 4.3 us).
   if (QUANT && act_cpt(p.K) <= 2 && rows >= 1024) {
-    const unsigned wgs = rows / kActRowWaves;
-    const dim3 grid(wgs), block(64 * kActRowWaves);
+    const dim3 grid(rows / kActRowWaves), block(64 * kActRowWaves);
     if (act_cpt(p.K) == 1)
-      hipLaunchKernelGGL((k_act_rows_wave<NORM, 1>), grid, block, 0, s, p);
+      hipLaunchKernelGGL((k_act_rows_wave<NORM, 1, 1>), grid, block, 0, s, p);
     else
-      hipLaunchKernelGGL((k_act_rows_wave<NORM, 2>), grid, block, 0, s, p);
+      hipLaunchKernelGGL((k_act_rows_wave<NORM, 2, 1>), grid, block, 0, s, p);
+    return;
+  }
+  if (QUANT && act_cpt(p.K) <= 2 && rows >= 256) {
+    const dim3 grid(rows / (kActRowWaves / 2)), block(64 * kActRowWaves);
+    if (act_cpt(p.K) == 1)
+      hipLaunchKernelGGL((k_act_rows_wave<NORM, 1, 2>), grid, block, 0, s, p);
+    else
+      hipLaunchKernelGGL((k_act_rows_wave<NORM, 2, 2>), grid, block, 0, s, p);
     return;
   }
   switch (act_cpt(p.K)) {

@@ -33,10 +33,12 @@ def run_quant(m, k, xb, gb=None, eps=1e-5):
                 scale=scale.cpu().numpy(), xq=xq.cpu().numpy(), y=H.bits_of(y))
 
 
-# From 1024 rows (K <= 8192) the prologue runs one wave per row: (1000, 2560)
-# and (1100, 6912) take that kernel, with padding rows in the last row block.
+# For K <= 8192 the prologue runs two waves per row from 256 rows and one wave
+# per row from 1024: (300, 2560) and (500, 6912) take the first kernel,
+# (1000, 2560) and (1100, 6912) the second, with padding rows in the last row
+# block.
 @pytest.mark.parametrize("m,k", [(1, 32), (5, 256), (32, 2560), (33, 2560), (70, 640), (32, 6912), (3, 16384),
-                                 (1000, 2560), (1100, 6912)])
+                                 (300, 2560), (500, 6912), (1000, 2560), (1100, 6912)])
 @pytest.mark.parametrize("norm", [False, True])
 def test_quant_absmax_bit_exact(orc, m, k, norm):
     print(f"quant m={m} k={k} norm={norm}", flush=True)

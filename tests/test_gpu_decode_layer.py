@@ -130,4 +130,4 @@ def test_capture_without_warm_up_is_refused():
         with torch.cuda.graph(g, stream=s):
             step.decode_layer(0, step.hidden, step.attn_out, step.qkv_out, step.ffn_h)
     torch.cuda.synchronize()
-    assert N.lib().btl_version() == 100
+    assert N.lib().btl_version() == 101
