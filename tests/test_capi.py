@@ -85,6 +85,28 @@ def test_gemm_tiling_query(L):
         t(64, 100, 64)
 
 
+def test_gemm_tiling_invariants():
+    """Over a sweep of prefill shapes: a wide plan's wave ranges cover its
+    column tiles (spans of CT / (4 / WQ) tiles, at most CTW each), CTW is an
+    instantiated size, and shapes the wide tiles do not take fall back to
+    the 128x256 / 64x256 tiles."""
+    for m in (256, 300, 512, 777, 1024, 2048, 4096, 8192):
+        for n in (32, 96, 640, 2560, 3072, 3840, 5120, 6912, 8192, 13824):
+            for k in (256, 2560, 6912):
+                t = N.gemm_tiling(m, k, n)
+                if t["kind"] == "tiles":
+                    assert t["rows"] in (64, 128)
+                    continue
+                assert t["kind"] == "wide" and t["rows"] == 64 and t["splitk"] == 1
+                ct, wq, ctw = t["col_tiles"], t["k_groups"], t["tiles_per_wave"]
+                assert wq in (1, 2, 4) and ctw in ((2, 3, 4) if wq == 1 else (2, 3, 5)), t
+                parts = 4 // wq
+                assert 1 <= ct and -(-ct // parts) <= ctw, t
+                # about two tiles per CU on 256 CUs, at least one
+                tiles = -(-m // 64) * -(-(n // 32) // ct)
+                assert tiles <= 2 * 256, t
+
+
 FAKE = 0x100000  # never dereferenced: every call below is rejected first
 
 
