@@ -75,16 +75,18 @@ enum { S_QKV = 0, S_O = 1, S_GU = 2, S_DN = 3, kStepOps = 4 };
 // Operand tiles between uses.  Row m writes its slice of tile j for (l, j)
 // (8-byte coherent stores, no acknowledgement wait).  Right after publishing
 // (l, j + 1), when it has all of its outputs of (l, j), it clears a share of
-// tile j to the sentinel in whole lines: any 1/32 of a tile whose units all
-// cover the 32 rows (every unit has then read the whole tile), 1/16 of its
-// half's lines of a tile of 16-row units.  Every row stage starts with a wait
-// for all of the row's earlier memory operations (microseconds old by then,
-// so it costs nothing), so a clear is performed before the row publishes
-// anything later, and every row's next flag of tile j causally follows the
-// publications of every row (through the 32-row units in between).  A unit
-// that has seen the flags of (l + 1, j) therefore reads, for every 8-byte
-// piece, either the sentinel or the new bytes, never bytes of (l, j); seeing
-// the sentinel it waits for the piece and reads again.  Tiles start
+// tile j to the sentinel in whole lines: 1/16 of the lines that hold its
+// 16-row half's bytes (every unit of that half, 16-row or 32-row, has then
+// read them).  Every row stage starts with a wait for all of the row's
+// earlier memory operations (microseconds old by then, so it costs nothing),
+// so a clear is performed before the row publishes anything later, and the
+// next flag of tile j of every row of the same half causally follows it
+// (through that half's units of the BitLinears in between, which wait for
+// this row's flags).  A row of the other half may run ahead, but it never
+// writes lines of this half.  A unit that has seen the flags of (l + 1, j)
+// therefore reads, for every 8-byte piece, either the sentinel or the new
+// bytes, never bytes of (l, j); seeing the sentinel it waits for the piece
+// and reads again.  Tiles start
 // (btl_decode_step_prepare) and end (the last row stage clears the last tile)
 // every launch as the sentinel.
 constexpr int64_t kStEpoch = 0;          // [kStepMaxGrid] u32
@@ -382,29 +384,29 @@ __device__ void publish_row(const StepArgs& p, int l, int j, int m, int K, int K
 }
 
 // Row m's share of a tile back to the sentinel, in whole 128-byte lines (a
-// wave's store instruction writes four full lines).  When every unit of the
-// tile covers all 32 rows, any row that has all of its outputs knows that the
-// whole tile has been read, and the tile is split into 32 contiguous shares.
-// A tile of 16-row units (half) is split among the 16 rows of each half, over
-// the lines that hold only that half's operand bytes: in each 1 KiB k-step
-// block, lines 0, 1, 4, 5 (rows 0-15) and 2, 3, 6, 7 (rows 16-31).  Row m's
-// share is KS lines (KS * 16 8-byte pieces; CP pieces per thread cover it).
+// wave's store instruction writes four full lines).  The share lies in lines
+// that hold operand bytes of row m's 16-row half only: in each 1 KiB k-step
+// block, lines 0, 1, 4, 5 hold rows 0-15 and lines 2, 3, 6, 7 rows 16-31
+// (lane l of a block holds row l & 31).  The 16 rows of a half split their
+// half's 16 KS lines into shares of KS lines (16 KS 8-byte pieces each), so
+// the 32 shares cover the tile once.  Every clear being by half is what
+// orders it before the tile's next write: the next write of those lines is
+// by rows of the same half, and each of them publishes it only after
+// receiving outputs of units of that half which waited for row m's flag of a
+// later BitLinear (or, for gate||up, of units that waited for every row).
+__host__ __device__ __forceinline__ int64_t clear_piece_offset(int m, int KS, int pc) {
+  const int li = (m & 15) * KS + (pc >> 4), sub = li & 3;
+  return (int64_t)(li >> 2) * 1024 + ((sub & 1) + ((sub >> 1) << 2) + 2 * (m >> 4)) * 128 + (pc & 15) * 8;
+}
 template <int CP>
-__device__ __forceinline__ void clear_tile_share(int8_t* xa, int m, int KS, bool half) {
+__device__ __forceinline__ void clear_tile_share(int8_t* xa, int m, int KS) {
   const int tid = threadIdx.x, npieces = KS * 16;
 #pragma unroll
   for (int i = 0; i < CP; ++i) {
     const int pc = tid + kActThreads * i;
-    if (pc < npieces) {
-      int64_t off;
-      if (!half) {
-        off = (int64_t)m * KS * 128 + pc * 8;
-      } else {
-        const int li = (m & 15) * KS + (pc >> 4), sub = li & 3;
-        off = (int64_t)(li >> 2) * 1024 + ((sub & 1) + ((sub >> 1) << 2) + 2 * (m >> 4)) * 128 + (pc & 15) * 8;
-      }
-      st_coherent(reinterpret_cast<uint64_t*>(xa + off), ((uint64_t)kTileSentinel << 32) | kTileSentinel);
-    }
+    if (pc < npieces)
+      st_coherent(reinterpret_cast<uint64_t*>(xa + clear_piece_offset(m, KS, pc)),
+                  ((uint64_t)kTileSentinel << 32) | kTileSentinel);
   }
 }
 
@@ -453,7 +455,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       STEP_TRACE(l, 0);
       publish_row<CH>(p, l, S_QKV, m, p.H, p.KSH, v, g_qkv, step_tag(E, l, S_QKV), s_sum, s_max, s_rs);
       STEP_TRACE(l, 1);
-      if (l > 0) clear_tile_share<CF>(tile_of(p, l - 1, S_DN), m, p.KSF, true);
+      if (l > 0) clear_tile_share<CF>(tile_of(p, l - 1, S_DN), m, p.KSF);
     }
     // ---- O: the user's QKV row, then RMSNorm(attn; attn_sub_norm)
     {
@@ -474,7 +476,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       pairs_to_floats<CH>(pr, v);
       publish_row<CH>(p, l, S_O, m, p.H, p.KSH, v, g, step_tag(E, l, S_O), s_sum, s_max, s_rs);
       STEP_TRACE(l, 3);
-      clear_tile_share<CH>(tile_of(p, l, S_QKV), m, p.KSH, true);
+      clear_tile_share<CH>(tile_of(p, l, S_QKV), m, p.KSH);
     }
     // ---- GU: h = bf16(h + o); RMSNorm(h; post_attention_layernorm)
     {
@@ -489,7 +491,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       pairs_to_floats<CH>(hid, v);
       publish_row<CH>(p, l, S_GU, m, p.H, p.KSH, v, g, step_tag(E, l, S_GU), s_sum, s_max, s_rs);
       STEP_TRACE(l, 5);
-      clear_tile_share<CH>(tile_of(p, l, S_O), m, p.KSH, true);
+      clear_tile_share<CH>(tile_of(p, l, S_O), m, p.KSH);
     }
     // ---- DN: RMSNorm(relu(g)^2 * u; ffn_sub_norm)
     {
@@ -503,7 +505,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       pairs_to_floats<CF>(pr, v);
       publish_row<CF>(p, l, S_DN, m, p.F, p.KSF, v, g, step_tag(E, l, S_DN), s_sum, s_max, s_rs);
       STEP_TRACE(l, 7);
-      clear_tile_share<CH>(tile_of(p, l, S_GU), m, p.KSH, false);
+      clear_tile_share<CH>(tile_of(p, l, S_GU), m, p.KSH);
     }
     // ---- h = bf16(h + d)
     {
@@ -519,7 +521,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
   // above, so they must not clear before the threads that poll have all of
   // the row's words (every other clear sits behind publish_row's barriers).
   lds_barrier();
-  clear_tile_share<CF>(tile_of(p, p.L - 1, S_DN), m, p.KSF, true);
+  clear_tile_share<CF>(tile_of(p, p.L - 1, S_DN), m, p.KSF);
   if (live && tid < nh)
     *reinterpret_cast<uint4*>(p.hidden + (int64_t)m * p.H + 8 * tid) =
         make_uint4(hid[0][0], hid[0][1], hid[0][2], hid[0][3]);
@@ -1088,6 +1090,16 @@ int64_t btl_decode_step_workspace_bytes(int64_t M, int64_t H, int64_t F, int64_t
 }
 
 int64_t btl_decode_step_error_offset(void) { return kStError; }
+
+int btl_decode_step_clear_share(int m, int64_t KS, int64_t* offsets, int64_t n) {
+  clear_error();
+  if (!offsets) return set_error(BTL_ERR_NULL, "btl_decode_step_clear_share: null offsets");
+  if (m < 0 || m >= kStepRows || KS < 1 || KS > 128 || n < 0)
+    return set_error(BTL_ERR_ARG, "btl_decode_step_clear_share: m=%d (0..31), KS=%lld (1..128), n=%lld", m,
+                     (long long)KS, (long long)n);
+  for (int64_t pc = 0; pc < n && pc < 16 * KS; ++pc) offsets[pc] = clear_piece_offset(m, (int)KS, (int)pc);
+  return BTL_OK;
+}
 
 int btl_decode_step_prepare(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L,
                             const btl_layer_weight_t* weights, void* workspace, size_t workspace_bytes) {

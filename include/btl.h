@@ -308,6 +308,14 @@ int btl_decode_step(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, fl
 int btl_decode_step_floor(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, void* workspace,
                           size_t workspace_bytes, btl_stream_t stream);
 
+/* Test hook with no counterpart in the reference: the byte offsets (from an
+ * operand tile's base) of the 16*KS 8-byte pieces that row m (0..31) of
+ * btl_decode_step writes back to the between-use sentinel after a tile's
+ * readers are done, for a tile of KS 128-column superblocks (1..128): the
+ * same function the kernel calls.  Writes min(n, 16*KS) offsets; returns
+ * BTL_OK or BTL_ERR_ARG / BTL_ERR_NULL.  Host only (no device call). */
+int btl_decode_step_clear_share(int m, int64_t KS, int64_t* offsets, int64_t n);
+
 /* ---- LM head (final norm is btl_rmsnorm) ------------------------------
  * Replaces the head matmul of src/bitnet_tt/inference/generator_batch32.py:
  * 768-811 (ttnn.matmul of the normed hidden state with the head weight that

@@ -256,6 +256,55 @@ def test_decode_step_sizes_and_argument_checks(L):
     assert L.btl_decode_step_prepare(0, 2560, 6912, 3840, 1, table, _p(FAKE), 1 << 28) == 2
 
 
+def _clear_share(L, m, KS):
+    out = (ctypes.c_int64 * (16 * KS))()
+    assert L.btl_decode_step_clear_share(m, KS, out, 16 * KS) == 0
+    return list(out)
+
+
+@pytest.mark.parametrize("KS", [1, 3, 20, 54])
+def test_decode_step_tile_clear_shares(L, KS):
+    """The persistent step's between-use clears of an operand tile (the
+    function the kernel calls).  Operand layout of a tile: in each 1 KiB
+    k-step block, lane l's 16 bytes (offset 16 l) belong to row l & 31, so a
+    128-byte line holds rows of one 8-row group.  Each row's share must lie in
+    whole lines of its own 16-row half (a row of the other half may already be
+    writing the tile's next use), be 8-byte aligned, and the 32 shares must
+    cover the tile's 32*KS*128 bytes exactly once."""
+    tile_bytes = 32 * KS * 128
+    seen = {}
+    for m in range(32):
+        offs = _clear_share(L, m, KS)
+        lines = {o // 128 for o in offs}
+        assert len(lines) == KS  # whole lines: 16 pieces of 8 bytes each
+        for o in offs:
+            assert o % 8 == 0 and 0 <= o < tile_bytes
+            assert o not in seen, f"piece {o} cleared by rows {seen[o]} and {m}"
+            seen[o] = m
+        for ln in lines:
+            rows = {(lane & 31) for lane in range((ln * 128 % 1024) // 16, (ln * 128 % 1024) // 16 + 8)}
+            assert {r >> 4 for r in rows} == {m >> 4}, f"row {m} clears line {ln} holding rows {sorted(rows)}"
+    assert len(seen) == tile_bytes // 8
+    # argument checks
+    out = (ctypes.c_int64 * 4)()
+    assert L.btl_decode_step_clear_share(32, KS, out, 4) == 5
+    assert L.btl_decode_step_clear_share(0, 0, out, 4) == 5
+    assert L.btl_decode_step_clear_share(0, KS, None, 4) == 1
+
+
+def test_decode_step_tile_clear_planted_mistake_is_caught(L):
+    """The coverage check above fails for a share map that splits the tile
+    into 32 contiguous ranges (lines shared by both halves)."""
+    KS = 20
+    bad = {m: [m * KS * 128 + 8 * pc for pc in range(16 * KS)] for m in range(32)}
+    crossing = 0
+    for m, offs in bad.items():
+        for ln in {o // 128 for o in offs}:
+            rows = {(lane & 31) for lane in range((ln * 128 % 1024) // 16, (ln * 128 % 1024) // 16 + 8)}
+            crossing += {r >> 4 for r in rows} != {m >> 4}
+    assert crossing > 0
+
+
 def test_lm_head_sizes_and_argument_checks(L):
     # 16 vocab rows x 32 k per KiB, K padded to the supported multiple of 256
     assert L.btl_lm_head_weight_bytes(128256, 2560) == 128256 * 2560 * 2
