@@ -791,17 +791,12 @@ def main():
         f"{value:.0f} GB/s")
     del graph
 
-    # the same step as 120 per-BitLinear launches and as 31 per-layer launches
+    # the same step as 120 per-BitLinear launches
     graph_c = capture(step.step_per_call)
     us_per_call, _ = timed(graph_c, args.steps)
     step.check()
     del graph_c
-    graph_l = capture(step.step_layers)
-    us_layers, _ = timed(graph_l, args.steps)
-    step.check()
-    del graph_l
-    log(f"[bench] per-BitLinear launches: {us_per_call:.1f} us per step; per-layer launches: "
-        f"{us_layers:.1f} us per step")
+    log(f"[bench] per-BitLinear launches: {us_per_call:.1f} us per step")
     # the latency floor of the persistent step's launch structure: the same
     # waits and hand-off stores with no arithmetic and no weight traffic
     graph_f = capture(step.step_floor)
@@ -810,16 +805,15 @@ def main():
     del graph_f
     log(f"[bench] hand-off floor of the persistent step (waits and hand-off stores only): {us_floor:.1f} us per step")
 
-    # the three launch structures compute the same bits from the same input
+    # the two launch structures compute the same bits from the same input
     outs = {}
-    for name, fn in (("persistent", step.step_persistent), ("per_call", step.step_per_call),
-                     ("layers", step.step_layers)):
+    for name, fn in (("persistent", step.step_persistent), ("per_call", step.step_per_call)):
         step.reset_hidden()
         fn()
         step.check()
         outs[name] = step.hidden.clone()
     same_bits = all(torch.equal(outs["persistent"].view(torch.int16), o.view(torch.int16)) for o in outs.values())
-    log(f"[bench] persistent / per-call / per-layer hidden bits equal: {same_bits}")
+    log(f"[bench] persistent / per-call hidden bits equal: {same_bits}")
     if not same_bits:
         raise SystemExit("launch structures disagree")
 
@@ -908,7 +902,6 @@ def main():
             "step_roofline_frac": round(value / HBM_PEAK_GBS, 4),
             "us_per_step_event": round(us_event, 1),
             "us_per_step_per_bitlinear_launches": round(us_per_call, 1),
-            "us_per_step_layer_launches": round(us_layers, 1),
             "us_per_step_handoff_floor": round(us_floor, 1),
             "launch_structures_bits_equal": same_bits,
             "us_per_bitlinear_launch": kernel_us,

@@ -40,7 +40,7 @@ _SZ = ctypes.c_size_t
 
 
 class LayerWeight(ctypes.Structure):
-    """btl_layer_weight_t: one BitLinear of a btl_decode_layer launch."""
+    """btl_layer_weight_t: one BitLinear of a btl_decode_step launch."""
 
     _fields_ = [
         ("wdev", ctypes.c_void_p),
@@ -107,8 +107,6 @@ EXPORTS = {
     "btl_decode_step_floor": ([_I64, _I64, _I64, _I64, _I64, _P, _SZ, _P], _I),
     "btl_decode_step_clear_share": ([_I, _I64, _P, _I64], _I),
     "btl_gemm_i8t2_dot4": ([_P, _P, _I64, _I64, _I64, _P, _P, _P], _I),
-    "btl_decode_layer_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64], _I64),
-    "btl_decode_layer_error_offset": ([], _I64),
     "btl_lm_head_weight_bytes": ([_I64, _I64], _I64),
     "btl_lm_head_workspace_bytes": ([], _I64),
     "btl_lm_head_repack": ([_P, _I64, _I64, _P, _P], _I),
@@ -116,10 +114,6 @@ EXPORTS = {
     "btl_decode_attention_workspace_bytes": ([_I64, _I64, _I64, _I64], _I64),
     "btl_decode_attention_error_offset": ([_I64, _I64], _I64),
     "btl_decode_attention": ([_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I, _F, _P, _P, _P, _P, _SZ, _P], _I),
-    "btl_decode_layer": (
-        [_I64, _I64, _I64, _I64, _I64, _LWP, _LWP, _LWP, _LWP, _F, _P, _P, _P, _P, _P, _SZ, _P],
-        _I,
-    ),
 }
 
 
@@ -251,7 +245,7 @@ def workspace(device, nbytes: int, kind: str = "bitlinear", error_offset: int | 
     """Zero-filled device workspace of at least nbytes for the current stream.
 
     kind separates workspaces whose layouts differ ("bitlinear" for
-    btl_bitlinear_fused / btl_gemm_i8t2, "layer" for btl_decode_layer).  A
+    btl_bitlinear_fused / btl_gemm_i8t2, "step" for btl_decode_step).  A
     workspace that grows is replaced by a fresh zero-filled one; the old one
     is released in stream order, after the calls that used it.
     ``error_offset`` registers the byte offset of a sticky error word inside
@@ -279,7 +273,7 @@ def check_errors(device=None) -> None:
     """Raise RuntimeError if any kernel on ``device`` set its sticky error word.
 
     The kernels that hand data between workgroups of one launch (the fused
-    decode BitLinear, the decode layer, decode attention) never hang: a wait
+    decode BitLinear, the decode step, decode attention) never hang: a wait
     that exceeds its spin limit sets a sticky error word in the call's
     workspace and the kernel finishes with invalid outputs.  This reads every
     registered error word of the device's workspaces (all streams) after a

@@ -11,21 +11,17 @@ generator_batch32.py:713-761) issues four ternary-matmul launches:
 Here the remaining norms and residual adds ride along with the BitLinears:
 attn_sub_norm and post_attention_layernorm become RMSNorm prologues, relu^2*up
 the gate||up epilogue, ffn_sub_norm the down prologue, and both residual adds
-epilogues.  Three launch structures compute the same bits:
+epilogues.  Two launch structures compute the same bits:
 
 * ``step_persistent``: the whole step's BitLinears as one ``btl_decode_step``
   launch (one workgroup per CU; 32 row workgroups run the elementwise stages
   of the token rows, the others one GEMM unit of each BitLinear, with weights
-  loaded one BitLinear ahead).  The fastest on MI355X (0.81 ms for the 2B
+  loaded one BitLinear ahead).  The fastest on MI355X (0.70 ms for the 2B
   model's 30 layers); it needs the attention width equal to hidden and the
   shape limits of include/btl.h.
 * ``step_per_call`` (the default ``step``, which takes any shape the fused
   op takes): one ``btl_bitlinear_fused`` launch per BitLinear (120 per
-  30-layer step, 1.0 ms);
-* ``step_layers``: layer 0's QKV as one such launch, then one
-  ``btl_decode_layer`` launch per layer covering o_proj, gate||up, down and
-  the next layer's QKV -- the BitLinear work between two attentions (31
-  launches per step, 1.26 ms).
+  30-layer step, 1.0 ms).
 
 ``step`` takes the attention output as an input buffer (the BitLinear
 portion alone).  After ``alloc_attention`` the step can also run whole:
@@ -234,7 +230,6 @@ class BitLinearDecodeStep:
         while len(self.layers) <= layer_idx:
             self.layers.append(None)
         self.layers[layer_idx] = lw
-        self._lw = None  # layer structs of the persistent launches are rebuilt
         self._st = None
 
     # -- buffers -----------------------------------------------------------
@@ -329,70 +324,11 @@ class BitLinearDecodeStep:
             self.layer(i, self.hidden, self.attn_out, self.qkv_out, self.ffn_h)
         return self.hidden
 
-    # -- persistent layer launches ------------------------------------------
-    def _layer_structs(self):
-        """btl_layer_weight_t of every BitLinear (kept alive with the step)."""
-        if getattr(self, "_lw", None) is None:
-            lw = []
-            for w in self.layers:
-                lw.append((N.layer_weight(w.o_proj, w.attn_sub_norm),
-                           N.layer_weight(w.gate_up, w.post_attention_layernorm),
-                           N.layer_weight(w.down, w.ffn_sub_norm),
-                           N.layer_weight(w.qkv, w.input_layernorm)))
-            self._lw = lw
-        return self._lw
-
-    def decode_layer(self, i: int, hidden, attn_out, qkv_out, ffn_h):
-        """Layer i's o_proj, gate||up and down plus layer i+1's QKV (when
-        there is one) as one btl_decode_layer launch, in place on hidden."""
-        import ctypes
-
-        import torch
-
-        c = self.config
-        lw = self._layer_structs()
-        B = hidden.shape[0]
-        H, F, qd = c.hidden_size, c.intermediate_size, c.num_attention_heads * c.head_dim
-        nxt = lw[i + 1][3] if i + 1 < len(lw) else None
-        for t, name in ((hidden, "hidden"), (attn_out, "attn_out"), (qkv_out, "qkv_out"), (ffn_h, "ffn_h")):
-            N.require_cuda(t, name)
-        L = N.lib()
-        nbytes = int(L.btl_decode_layer_workspace_bytes(B, H, qd, F, c.qkv_dim))
-        if torch.cuda.is_current_stream_capturing() and not N.has_workspace(hidden.device, nbytes, "layer"):
-            # a workspace made inside a capture would be re-zeroed by every
-            # replay, resetting the launch counters the kernel's flags rely on
-            raise RuntimeError("run one eager decode step on this stream before capturing it in a graph")
-        ws = N.workspace(hidden.device, nbytes, kind="layer", error_offset=int(L.btl_decode_layer_error_offset()))
-        N.check(
-            L.btl_decode_layer(B, H, qd, F, c.qkv_dim, ctypes.byref(lw[i][0]), ctypes.byref(lw[i][1]),
-                               ctypes.byref(lw[i][2]), ctypes.byref(nxt) if nxt is not None else None,
-                               float(self.eps), N.ptr(attn_out), N.ptr(hidden), N.ptr(ffn_h), N.ptr(qkv_out),
-                               N.ptr(ws), ws.numel(), N.stream_of(hidden.device)),
-            "btl_decode_layer",
-        )
-
-    def layer_error_word(self) -> int:
-        """Error word of this stream's decode-layer workspace (0: no bounded
-        wait ran out)."""
-        import torch
-
-        L = N.lib()
-        ws = N.workspace(self.device, 0, kind="layer")
-        off = int(L.btl_decode_layer_error_offset())
-        return int(ws[off:off + 4].view(torch.int32).item())
-
     def check(self) -> None:
         """Raise RuntimeError if a bounded wait in any launch of this
-        device's steps (fused BitLinears, decode layers, decode attention)
+        device's steps (fused BitLinears, the persistent step, decode attention)
         ran out since the last check; synchronises the device."""
         N.check_errors(self.device)
-
-    def step_layers(self):
-        w0 = self.layers[0]
-        ternary_matmul_into(self.hidden, w0.qkv, self.qkv_out, norm_weight=w0.input_layernorm, norm_epsilon=self.eps)
-        for i in range(len(self.layers)):
-            self.decode_layer(i, self.hidden, self.attn_out, self.qkv_out, self.ffn_h)
-        return self.hidden
 
     # -- one launch for the whole step ----------------------------------------
     def _step_table(self):

@@ -216,7 +216,7 @@ using namespace btl;
 extern "C" {
 
 const char* btl_last_error(void) { return g_err; }
-int btl_version(void) { return 101; }
+int btl_version(void) { return 200; }
 
 int64_t btl_packed_tile_count(int64_t in_f, int64_t out_f) {
   if (in_f <= 0 || out_f <= 0) return 0;

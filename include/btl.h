@@ -215,9 +215,9 @@ int btl_bitlinear_fused_noalloc(const uint16_t* x, int64_t M, int64_t K, int64_t
                                 uint16_t* out, int32_t* acc_out, int8_t* xq_debug, uint32_t* error_word, int splitk,
                                 btl_stream_t stream);
 
-/* ---- persistent decode layer ------------------------------------------ */
+/* ---- persistent decode step ------------------------------------------- */
 
-/* One BitLinear weight of a decode layer: device layout (btl_repack), its
+/* One BitLinear weight of the decode step: device layout (btl_repack), its
  * per-segment scales with exclusive column ends (host values), and the
  * RMSNorm gain applied to the BitLinear's input (bf16, device). */
 typedef struct {
@@ -227,37 +227,6 @@ typedef struct {
   int nseg;
   const uint16_t* gamma;
 } btl_layer_weight_t;
-
-/* Workspace of btl_decode_layer (256-byte aligned): zero-filled once before
- * first use, then used only by btl_decode_layer calls on one device and one
- * stream (it holds per-workgroup launch counters). */
-int64_t btl_decode_layer_workspace_bytes(int64_t M, int64_t H, int64_t Q, int64_t F, int64_t NQKV);
-/* Byte offset of the word that is non-zero when a bounded wait inside a
- * btl_decode_layer launch ran out (that call's outputs are then invalid). */
-int64_t btl_decode_layer_error_offset(void);
-
-/* Every BitLinear of a decode layer from o_proj to the next layer's QKV, as
- * one launch (the body of src/bitnet_tt/inference/generator_batch32.py:
- * 739-761 followed by :718-727 of the next layer; attention runs between two
- * such launches):
- *   hidden += o_proj(RMSNorm(attn; o_proj->gamma))               (residual)
- *   ffn_h   = relu(g)^2 * u, g||u = gate_up(RMSNorm(hidden; gate_up->gamma))
- *   hidden += down(RMSNorm(ffn_h; down->gamma))                   (residual)
- *   qkv_out = next_qkv(RMSNorm(hidden; next_qkv->gamma))  if next_qkv != NULL
- * Each BitLinear is the same arithmetic as btl_bitlinear_fused (bit-identical
- * results).  M <= 32 rows; attn [M,Q], hidden [M,H] (in/out), ffn_h [M,F],
- * qkv_out [M,NQKV] bf16.  gate_up has two segments split at F.  The launch
- * uses one workgroup per CU and waits between its phases; nothing else may
- * share the GPU's compute units while it runs (a wait that runs out sets the
- * word at btl_decode_layer_error_offset(); zero-fill the workspace before
- * reusing it then). */
-int btl_decode_layer(int64_t M, int64_t H, int64_t Q, int64_t F, int64_t NQKV, const btl_layer_weight_t* o_proj,
-                     const btl_layer_weight_t* gate_up, const btl_layer_weight_t* down,
-                     const btl_layer_weight_t* next_qkv, float eps, const uint16_t* attn, uint16_t* hidden,
-                     uint16_t* ffn_h, uint16_t* qkv_out, void* workspace, size_t workspace_bytes,
-                     btl_stream_t stream);
-
-/* ---- persistent decode step ------------------------------------------- */
 
 /* The BitLinear portion of a whole decode step as one launch: for every
  * layer l, QKV (RMSNorm(hidden; input_layernorm), output to qkv_out), o_proj
