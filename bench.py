@@ -563,6 +563,12 @@ def cpu_baseline(step, torch, gpu_hidden, reps=20, warmup=3):
     med = times[len(times) // 2]
     nbytes = step.algorithmic_bytes()["step"]
     equal = float((h.view(torch.int16) == gpu_hidden.view(torch.int16)).float().mean().item())
+    # the GPU's hidden state against this reference-order chain: normwise
+    # relative error, largest element error over the largest magnitude, PCC
+    g64, r64 = gpu_hidden.float().cpu().double(), h.float().double()
+    d = g64 - r64
+    agree = {"rel_fro": float(d.norm() / r64.norm()), "max_rel": float(d.abs().max() / r64.abs().max()),
+             "pcc": float(np.corrcoef(g64.numpy().ravel(), r64.numpy().ravel())[0, 1])}
     return {
         "value": round(nbytes / med / 1e9, 3),
         "unit": "GB/s",
@@ -579,6 +585,7 @@ def cpu_baseline(step, torch, gpu_hidden, reps=20, warmup=3):
         "torch": torch.__version__,
         "numpy": np.__version__,
         "hidden_bits_equal_to_gpu": round(equal, 6),
+        "hidden_vs_gpu": {k: round(v, 7) for k, v in agree.items()},
     }
 
 
@@ -876,7 +883,8 @@ def main():
         log("[bench] CPU baseline (reference CPU path: numpy absmax + torch fp32 GEMM) ...")
         cpu = cpu_baseline(step, torch, gpu_hidden, reps=args.cpu_reps)
         log(f"[bench] CPU: {cpu['ms_per_step']} ms per step on {cpu['cores']} threads ({cpu['cpu_model']}); "
-            f"{cpu['value']} GB/s; hidden bits equal to the GPU's: {cpu['hidden_bits_equal_to_gpu']}")
+            f"{cpu['value']} GB/s; hidden bits equal to the GPU's: {cpu['hidden_bits_equal_to_gpu']}; "
+            f"against the GPU's: {cpu['hidden_vs_gpu']}")
 
     line = {
         "metric": "ternary GEMM HBM GB/s (% roofline) at M=32; BitLinear ms per batch-32 decode step",

@@ -139,3 +139,68 @@ def write_hf_snapshot(path, cfg, seed, packed=False, embed=True):
                    "intermediate_size": cfg.intermediate_size, "vocab_size": cfg.vocab_size,
                    "rms_norm_eps": cfg.rms_norm_eps, "rope_theta": cfg.rope_theta}, f)
     return expect
+
+
+def reference_order_chain(orc, step, hidden_bits, attn_bits, layers=None):
+    """The decode step's BitLinear chain in the reference's own CPU order: per
+    BitLinear the RMSNorm as HF BitNetRMSNorm computes it in torch (fp32
+    mean of squares, rsqrt, bf16 normalised value times the bf16 gain), numpy
+    absmax quantisation (src/bitnet_tt/utils/quantization.py:60-91), a torch
+    fp32 GEMM of the integer operands (exact), the scale to bf16, relu^2*up
+    and the residual adds in bf16.  Weights are read back from the device.
+    Returns (hidden bits after the chain, the last layer's qkv bits)."""
+    import torch
+
+    from bitnet_tt.utils.quantization import activation_quant_absmax
+
+    bf = torch.bfloat16
+    eps = step.eps
+    F = step.config.intermediate_size
+
+    def tb(bits):
+        return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(bf)
+
+    def wm(pw):
+        dev_words = pw.data.cpu().numpy().view(np.uint32)
+        w = orc.devlayout_decode(dev_words, pw.in_features, pw.out_features)
+        srow = torch.empty(pw.out_features, dtype=torch.float32)
+        lo = 0
+        for sc, end in zip(pw.segment_scales, pw.segment_ends):
+            srow[lo:end] = float(sc)
+            lo = end
+        return torch.from_numpy(w.astype(np.float32)), srow
+
+    def rmsnorm(x, g):
+        x32 = x.float()
+        var = x32.pow(2).mean(-1, keepdim=True)
+        return g * (x32 * torch.rsqrt(var + eps)).to(bf)
+
+    def bitlinear(x, g, w_s):
+        w, srow = w_s
+        y = rmsnorm(x, g).float().numpy()
+        q, scale = activation_quant_absmax(y)
+        acc = torch.from_numpy(q.astype(np.float32)) @ w
+        return (acc * (srow * torch.from_numpy((1.0 / scale).astype(np.float32)))).to(bf)
+
+    h, attn, qkv = tb(hidden_bits).clone(), tb(attn_bits), None
+    for lw in step.layers[: layers if layers is not None else len(step.layers)]:
+        gl = lambda t: tb(bits_of(t))  # noqa: E731
+        qkv = bitlinear(h, gl(lw.input_layernorm), wm(lw.qkv))
+        h = (h.float() + bitlinear(attn, gl(lw.attn_sub_norm), wm(lw.o_proj)).float()).to(bf)
+        gu = bitlinear(h, gl(lw.post_attention_layernorm), wm(lw.gate_up))
+        g_, u_ = gu[:, :F].float(), gu[:, F:].float()
+        r = (torch.relu(g_).pow(2).to(bf).float() * u_).to(bf)
+        h = (h.float() + bitlinear(r, gl(lw.ffn_sub_norm), wm(lw.down)).float()).to(bf)
+    return h.view(torch.int16).numpy().view(np.uint16), qkv.view(torch.int16).numpy().view(np.uint16)
+
+
+def chain_agreement(orc, got_bits, ref_bits):
+    """Normwise relative error, max-element error over the largest reference
+    magnitude, Pearson correlation and the fraction of equal bf16 values."""
+    g = orc.bf16_to_f32(got_bits).astype(np.float64)
+    r = orc.bf16_to_f32(ref_bits).astype(np.float64)
+    d = g - r
+    return {"rel_fro": float(np.linalg.norm(d) / np.linalg.norm(r)),
+            "max_rel": float(np.abs(d).max() / np.abs(r).max()),
+            "pcc": float(np.corrcoef(g.ravel(), r.ravel())[0, 1]),
+            "bits_equal": float((np.asarray(got_bits) == np.asarray(ref_bits)).mean())}

@@ -2,8 +2,11 @@
 
 int32 accumulators are compared bit for bit with the oracle; bf16 outputs too
 (the epilogue's rounding is specified exactly).  Decode shapes run every
-split-K factor; prefill shapes at full size are checked on sampled rows plus
-row- and column-checksums against the oracle."""
+split-K factor; prefill shapes at full size are compared in every row, with
+the reference accumulators from a host fp32 matmul of the integer operands
+(exact: every partial sum is an integer below 2^24) that is itself checked
+against the oracle's integer GEMM on sampled rows, plus row and column
+checksums in int64."""
 
 import numpy as np
 import pytest
@@ -54,6 +57,21 @@ def run_gemm(orc, q, w_kn, scales, ends=None, epi=0, splitk=0, residual_bits=Non
     torch.cuda.synchronize()
     counters_clean = ws_bytes == 0 or not ws[: 4 * 2048].cpu().numpy()[: 4 * ((n // 32) or 1)].any()
     return acc.cpu().numpy(), H.bits_of(out), a_dq[:m], counters_clean
+
+
+def full_acc_ref(orc, q, w, check_rows=8, seed=0):
+    """Reference int32 accumulators of q [m,k] int8 x w [k,n] ternary for
+    every row: a host torch fp32 matmul of the integer-valued operands.  The
+    sums are exact (|acc| <= 128 k < 2^24 for k <= 131072, so every partial
+    sum is an integer that fp32 holds), and sampled rows are checked against
+    the oracle's integer GEMM."""
+    m, k = q.shape
+    assert 128 * k < (1 << 24)
+    ref = (torch.from_numpy(q.astype(np.float32)) @ torch.from_numpy(w.astype(np.float32))).numpy()
+    ref = ref.astype(np.int32)
+    rows = np.unique(np.concatenate([[0, m - 1], np.random.default_rng(seed).choice(m, check_rows)]))
+    assert np.array_equal(ref[rows], orc.gemm_i8t(np.ascontiguousarray(q[rows]), w)), "host fp32 reference"
+    return ref
 
 
 def expected_out(orc, acc, a_dq, scales, ends, epi, residual_bits=None):
@@ -251,8 +269,8 @@ PREFILL_SHAPES = [
 
 @pytest.mark.parametrize("m,k,n,epi,rowsum", PREFILL_SHAPES)
 def test_prefill_full_size_properties(orc, m, k, n, epi, rowsum):
-    """Full prefill shapes: 16 sampled rows exact (accumulators and bf16),
-    every row checksum and every column checksum exact."""
+    """Full prefill shapes: every accumulator and every bf16 output exact,
+    and every row and column checksum in int64."""
     print(f"prefill full m={m} k={k} n={n} epi={epi} rowsum={rowsum} splitk={N.lib().btl_choose_splitk(m, k, n, epi)}",
           flush=True)
     rng = np.random.default_rng(m + n + k)
@@ -262,14 +280,15 @@ def test_prefill_full_size_properties(orc, m, k, n, epi, rowsum):
     ends = [n] if epi == 0 else [n // 2, n]
     acc, out, a_dq, clean = run_gemm(orc, q, w, scales, ends, epi=epi, rowsum=rowsum)
     assert clean, "split-K arrival counters not back at zero"
-    rows = np.sort(rng.choice(m, 16, replace=False))
-    ref_rows = orc.gemm_i8t(np.ascontiguousarray(q[rows]), w)
-    assert np.array_equal(acc[rows], ref_rows)
+    ref = full_acc_ref(orc, q, w, seed=m + n)
+    bad = np.argwhere(acc != ref)
+    assert bad.size == 0, f"{len(bad)} accumulators differ, first at {bad[0].tolist()}"
     q64, w64 = q.astype(np.int64), w.astype(np.int64)
     assert np.array_equal(acc.astype(np.int64).sum(1), q64 @ w64.sum(1))
     assert np.array_equal(acc.astype(np.int64).sum(0), q64.sum(0) @ w64)
-    exp_rows = expected_out(orc, ref_rows, a_dq[rows], scales, ends, epi)
-    assert np.array_equal(out[rows], exp_rows)
+    exp = expected_out(orc, ref, a_dq, scales, ends, epi)
+    bad = np.argwhere(out != exp)
+    assert bad.size == 0, f"{len(bad)} bf16 outputs differ, first at {bad[0].tolist()}"
 
 
 # Wide-tile prefill (64-row x CT-column tiles, about two per CU; with the row
@@ -294,7 +313,7 @@ WIDE_SHAPES = [  # m, k, n, (CT, CTW, WQ)
 
 @pytest.mark.parametrize("m,k,n,plan", WIDE_SHAPES)
 def test_prefill_wide_tiles(orc, m, k, n, plan):
-    """Sampled rows exact (accumulators and bf16 with a residual and three
+    """Every accumulator and every bf16 output exact (a residual and three
     weight-scale segments), every row and column checksum exact."""
     t = N.gemm_tiling(m, k, n)
     assert (t["kind"], t["col_tiles"], t["tiles_per_wave"], t["k_groups"]) == ("wide", *plan), t
@@ -306,13 +325,12 @@ def test_prefill_wide_tiles(orc, m, k, n, plan):
     scales = [0.013, 0.029, 0.021]
     res = orc.f32_to_bf16(rng.standard_normal((m, n)).astype(np.float32))
     acc, out, a_dq, _ = run_gemm(orc, q, w, scales, ends, residual_bits=res, rowsum=True)
-    rows = np.unique(np.concatenate([[0, m - 1], rng.choice(m, 22, replace=False)]))
-    ref_rows = orc.gemm_i8t(np.ascontiguousarray(q[rows]), w)
-    assert np.array_equal(acc[rows], ref_rows)
+    ref = full_acc_ref(orc, q, w, seed=m + k)
+    assert np.array_equal(acc, ref)
     q64, w64 = q.astype(np.int64), w.astype(np.int64)
     assert np.array_equal(acc.astype(np.int64).sum(1), q64 @ w64.sum(1))
     assert np.array_equal(acc.astype(np.int64).sum(0), q64.sum(0) @ w64)
-    assert np.array_equal(out[rows], expected_out(orc, ref_rows, a_dq[rows], scales, ends, 0, res[rows]))
+    assert np.array_equal(out, expected_out(orc, ref, a_dq, scales, ends, 0, res))
 
 
 @pytest.mark.parametrize("m,k,n", [(2048, 2560, 3072), (1000, 512, 6912), (512, 1024, 2560)])
@@ -340,10 +358,9 @@ def test_prefill_gate_up_relu2_through_ternary_matmul(orc, m):
     """Prefill gate||up as the layer runs it: ternary_matmul (RMSNorm +
     absmax activation kernel, then the prefill GEMM with its row sums) on
     x ~ N(0, 1) with 1 % outlier channels and gate/up weights absmean-quantised
-    from seeded N(0, 0.02) latents.  The quantised activations are compared
-    with the oracle for every row, every row and column checksum of the
-    accumulators exactly, and 64 sampled rows of accumulators and relu^2*up
-    outputs bit for bit."""
+    from seeded N(0, 0.02) latents.  The quantised activations, every
+    accumulator and every relu^2*up output are compared with the oracle bit
+    for bit (64 rows through the oracle's whole BitLinear chain as well)."""
     from bitnet_tt.ternary_matmul import PackedTernaryWeight, ternary_matmul
 
     k, f = 2560, 6912
@@ -360,7 +377,7 @@ def test_prefill_gate_up_relu2_through_ternary_matmul(orc, m):
                          epilogue="relu2_mul", acc_out=acc, xq_out=xq)
     torch.cuda.synchronize()
     y = orc.rmsnorm_bf16(xb, gb, 1e-5)
-    q_ref, _, _, _ = orc.act_quant_absmax(orc.bf16_to_f32(y))
+    q_ref, _, a_dq_ref, _ = orc.act_quant_absmax(orc.bf16_to_f32(y))
     q_got = xq.cpu().numpy()
     assert np.array_equal(q_got, q_ref), "quantised activations differ"
     a = acc.cpu().numpy().astype(np.int64)
@@ -371,6 +388,10 @@ def test_prefill_gate_up_relu2_through_ternary_matmul(orc, m):
     ref = orc.gate_up_relu2(np.ascontiguousarray(xb[rows]), w, float(gs), float(us), gamma_bf16=gb, norm_eps=1e-5)
     assert np.array_equal(a[rows], ref["acc"]), "sampled accumulators"
     assert np.array_equal(H.bits_of(out)[rows], ref["h"]), "sampled relu^2*up outputs"
+    full = full_acc_ref(orc, q_ref, w, seed=m)
+    assert np.array_equal(a, full), "accumulators"
+    exp = expected_out(orc, full, a_dq_ref, [float(gs), float(us)], [f, 2 * f], 1)
+    assert np.array_equal(H.bits_of(out), exp), "relu^2*up outputs"
 
 
 @pytest.mark.parametrize("m", [32, 100])
