@@ -72,6 +72,7 @@ _LWP = ctypes.POINTER(LayerWeight)
 EXPORTS = {
     "btl_last_error": ([], ctypes.c_char_p),
     "btl_version": ([], _I),
+    "btl_check_coresident": ([_I64, _I64, _I64], _I),
     "btl_packed_tile_count": ([_I64, _I64], _I64),
     "btl_packed_dram_bytes": ([_I64, _I64], _I64),
     "btl_devlayout_words": ([_I64, _I64], _I64),

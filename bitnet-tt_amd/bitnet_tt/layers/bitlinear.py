@@ -69,7 +69,7 @@ class Linear:
     _WEIGHT_DTYPE_MAP = {"packed_ternary": "int32 (2-bit codes, GEMM device layout)"}
 
     def __init__(self, in_features: int, out_features: int, device=None, compute_fidelity: str = "hifi2",
-                 weight_dtype: str = "packed_ternary") -> None:
+                 weight_dtype: str = "packed_ternary", check_errors: bool | None = None) -> None:
         if weight_dtype not in self._WEIGHT_DTYPE_MAP:
             raise ValueError(
                 f"weight_dtype {weight_dtype!r} is a Tensix storage format; this backend stores 'packed_ternary'"
@@ -83,6 +83,10 @@ class Linear:
         self._weight_dtype_name = weight_dtype
         self._use_packed_ternary = True
         self.epilogue = "none"
+        # True: every call synchronises and raises RuntimeError at the call if
+        # a bounded wait of its launch ran out (None: the library-wide mode,
+        # bitnet_tt.ternary_matmul.set_check_after_call)
+        self.check_errors = check_errors
 
     def _check_shape(self, out_f: int, in_f: int) -> None:
         if (out_f, in_f) != (self.out_features, self.in_features):
@@ -150,9 +154,9 @@ class Linear:
             raise RuntimeError("Weights not loaded. Call load_weights() first.")
         if out is None:
             return ternary_matmul(x, self.weight, norm_weight=norm_weight, norm_epsilon=norm_epsilon,
-                                  epilogue=self.epilogue, residual=residual)
+                                  epilogue=self.epilogue, residual=residual, check_errors=self.check_errors)
         return ternary_matmul_into(x, self.weight, out, norm_weight=norm_weight, norm_epsilon=norm_epsilon,
-                                   epilogue=self.epilogue, residual=residual)
+                                   epilogue=self.epilogue, residual=residual, check_errors=self.check_errors)
 
     def check(self) -> None:
         """Raise RuntimeError if a bounded wait of a launch on this layer's

@@ -18,11 +18,29 @@ backend: inputs must live on a ROCm device and libbtl.so must be built.
 
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass, field
 
 from . import _native as N
 
 EPILOGUES = {"none": N.EPI_SCALE, "scale": N.EPI_SCALE, "relu2_mul": N.EPI_RELU2_MUL}
+
+# Check-after-call mode: every call synchronises its device and raises
+# RuntimeError at the call when a bounded wait of a fused decode launch ran
+# out, as the reference's op raises at its call (bitlinear.py:329-330).  Off by
+# default (a synchronisation per call; not allowed inside a graph capture);
+# on with set_check_after_call(True) or BTL_CHECK_AFTER_CALL=1, or per call.
+_check_after_call = os.environ.get("BTL_CHECK_AFTER_CALL", "0") not in ("", "0")
+
+
+def set_check_after_call(enabled: bool) -> None:
+    """Turn the check-after-call mode on or off for every later call."""
+    global _check_after_call
+    _check_after_call = bool(enabled)
+
+
+def check_after_call_enabled() -> bool:
+    return _check_after_call
 
 
 @dataclass
@@ -68,6 +86,7 @@ def ternary_matmul(
     splitk: int = 0,
     acc_out=None,
     xq_out=None,
+    check_errors: bool | None = None,
 ):
     """``y = epilogue(quant(norm(a)) @ W)`` in bf16.
 
@@ -86,6 +105,9 @@ def ternary_matmul(
         exact accumulators and the quantised activations (parity checks).
     compute_kernel_config: accepted for signature compatibility; the gfx950
         path has a single (exact) accumulation mode.
+    check_errors: True synchronises after the launch and raises RuntimeError
+        if a bounded wait of a fused decode launch ran out (None: the mode set
+        by :func:`set_check_after_call`).
     """
     import torch
 
@@ -113,6 +135,7 @@ def ternary_matmul(
     ternary_matmul_into(
         x, w, out, norm_weight=norm_weight, norm_epsilon=norm_epsilon, weight_scale=weight_scale,
         epilogue=epilogue, residual=residual, splitk=splitk, acc_out=acc_out, xq_out=xq_out,
+        check_errors=check_errors,
     )
     return out
 
@@ -139,6 +162,7 @@ def ternary_matmul_into(
     splitk: int = 0,
     acc_out=None,
     xq_out=None,
+    check_errors: bool | None = None,
 ):
     """Same as :func:`ternary_matmul` writing into ``out`` (no allocation once
     the per-stream workspace exists, so the call can be captured in a graph).
@@ -194,4 +218,6 @@ def ternary_matmul_into(
         ),
         "btl_bitlinear_fused",
     )
+    if _check_after_call if check_errors is None else check_errors:
+        N.check_errors(dev)
     return out

@@ -42,6 +42,15 @@ int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3
 void clear_error();
 int check_launch(const char* what);
 
+// Co-residency of a grid whose workgroups wait on each other: BTL_OK when
+// `grid` workgroups fit at once (per_cu x cus), else BTL_ERR_LAUNCH with a
+// message.  check_coresident_launch queries the kernel's occupancy and the
+// CUs the stream may use.
+int coresident_check(const char* who, int64_t grid, int64_t per_cu, int64_t cus);
+int stream_cus(hipStream_t s);
+int kernel_per_cu(const void* kernel, int threads);
+int check_coresident_launch(const char* who, const void* kernel, int threads, int64_t grid, hipStream_t s);
+
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 // ---- layout quantities ----------------------------------------------------

@@ -1360,19 +1360,22 @@ static void launch_decode_nsb(int nsb, dim3 grid, hipStream_t s, const GemmArgs&
   }
 }
 
+// The fused kernel's workgroups wait on each other: the instance launches
+// only if the device (the stream's CUs) holds the whole grid at once.
 template <int TPW, int EPI, bool NORM, int CPT, bool HALF>
-static void launch_fused_nsb(int nsb, dim3 grid, hipStream_t s, const GemmArgs& g, const ActArgs& a,
-                             const FusedSync& fs) {
-  const dim3 block(512);
+static int launch_fused_nsb(int nsb, dim3 grid, hipStream_t s, const GemmArgs& g, const ActArgs& a,
+                            const FusedSync& fs) {
+  void (*k)(GemmArgs, ActArgs, FusedSync);
   switch (nsb) {
-    case 2: hipLaunchKernelGGL((k_bitlinear_decode<TPW, 2, EPI, NORM, CPT, HALF>), grid, block, 0, s, g, a, fs); break;
-    case 4: hipLaunchKernelGGL((k_bitlinear_decode<TPW, 4, EPI, NORM, CPT, HALF>), grid, block, 0, s, g, a, fs); break;
-    case 6: hipLaunchKernelGGL((k_bitlinear_decode<TPW, 6, EPI, NORM, CPT, HALF>), grid, block, 0, s, g, a, fs); break;
-    default:
-      hipLaunchKernelGGL((k_bitlinear_decode<TPW, TPW == 2 ? 6 : 8, EPI, NORM, CPT, HALF>), grid, block, 0, s, g, a,
-                         fs);
-      break;
+    case 2: k = k_bitlinear_decode<TPW, 2, EPI, NORM, CPT, HALF>; break;
+    case 4: k = k_bitlinear_decode<TPW, 4, EPI, NORM, CPT, HALF>; break;
+    case 6: k = k_bitlinear_decode<TPW, 6, EPI, NORM, CPT, HALF>; break;
+    default: k = k_bitlinear_decode<TPW, TPW == 2 ? 6 : 8, EPI, NORM, CPT, HALF>; break;
   }
+  const int rc = check_coresident_launch("fused decode BitLinear", reinterpret_cast<const void*>(k), 512, grid.x, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(k, grid, dim3(512), 0, s, g, a, fs);
+  return BTL_OK;
 }
 
 // Superblocks per pass: the slice's share per wave, bucketed.  Two waves per
@@ -1603,35 +1606,25 @@ static int launch_gemm(const GemmArgs& a, int epilogue, const GemmPlan& pl, hipS
 }
 
 template <bool NORM, int CPT>
-static void launch_fused_epi(int epilogue, const GemmPlan& pl, int nsb, dim3 grid, hipStream_t s, const GemmArgs& g,
-                             const ActArgs& a, const FusedSync& fs) {
+static int launch_fused_epi(int epilogue, const GemmPlan& pl, int nsb, dim3 grid, hipStream_t s, const GemmArgs& g,
+                            const ActArgs& a, const FusedSync& fs) {
   if (pl.mh == 2) {
-    if (epilogue == BTL_EPI_RELU2_MUL) {
-      launch_fused_nsb<2, EPI_RELU2, NORM, CPT, true>(nsb, grid, s, g, a, fs);
-    } else if (pl.tpw == 2) {
-      launch_fused_nsb<2, EPI_SCALE, NORM, CPT, true>(nsb, grid, s, g, a, fs);
-    } else {
-      launch_fused_nsb<1, EPI_SCALE, NORM, CPT, true>(nsb, grid, s, g, a, fs);
-    }
-  } else if (epilogue == BTL_EPI_RELU2_MUL) {
-    launch_fused_nsb<2, EPI_RELU2, NORM, CPT, false>(nsb, grid, s, g, a, fs);
-  } else if (pl.tpw == 2) {
-    launch_fused_nsb<2, EPI_SCALE, NORM, CPT, false>(nsb, grid, s, g, a, fs);
-  } else {
-    launch_fused_nsb<1, EPI_SCALE, NORM, CPT, false>(nsb, grid, s, g, a, fs);
+    if (epilogue == BTL_EPI_RELU2_MUL) return launch_fused_nsb<2, EPI_RELU2, NORM, CPT, true>(nsb, grid, s, g, a, fs);
+    if (pl.tpw == 2) return launch_fused_nsb<2, EPI_SCALE, NORM, CPT, true>(nsb, grid, s, g, a, fs);
+    return launch_fused_nsb<1, EPI_SCALE, NORM, CPT, true>(nsb, grid, s, g, a, fs);
   }
+  if (epilogue == BTL_EPI_RELU2_MUL) return launch_fused_nsb<2, EPI_RELU2, NORM, CPT, false>(nsb, grid, s, g, a, fs);
+  if (pl.tpw == 2) return launch_fused_nsb<2, EPI_SCALE, NORM, CPT, false>(nsb, grid, s, g, a, fs);
+  return launch_fused_nsb<1, EPI_SCALE, NORM, CPT, false>(nsb, grid, s, g, a, fs);
 }
 
 // Rows of 1, 2 or 4 chunks of 8 per thread (K <= 4096, 8192, 16384).
 template <bool NORM>
-static void launch_fused(int cpt, int epilogue, const GemmPlan& pl, int nsb, dim3 grid, hipStream_t s,
-                         const GemmArgs& g, const ActArgs& a, const FusedSync& fs) {
-  if (cpt <= 1)
-    launch_fused_epi<NORM, 1>(epilogue, pl, nsb, grid, s, g, a, fs);
-  else if (cpt <= 2)
-    launch_fused_epi<NORM, 2>(epilogue, pl, nsb, grid, s, g, a, fs);
-  else
-    launch_fused_epi<NORM, 4>(epilogue, pl, nsb, grid, s, g, a, fs);
+static int launch_fused(int cpt, int epilogue, const GemmPlan& pl, int nsb, dim3 grid, hipStream_t s,
+                        const GemmArgs& g, const ActArgs& a, const FusedSync& fs) {
+  if (cpt <= 1) return launch_fused_epi<NORM, 1>(epilogue, pl, nsb, grid, s, g, a, fs);
+  if (cpt <= 2) return launch_fused_epi<NORM, 2>(epilogue, pl, nsb, grid, s, g, a, fs);
+  return launch_fused_epi<NORM, 4>(epilogue, pl, nsb, grid, s, g, a, fs);
 }
 
 
@@ -1748,11 +1741,13 @@ static int bitlinear_fused_impl(const uint16_t* x, int64_t M, int64_t K, int64_t
     const int nsb = decode_nsb(pf, ksb(K), epilogue);
     const dim3 grid((unsigned)(kFusedActBlocks + fs.ngemm));
     const int cpt = act_cpt(K);
-    if (gamma)
-      launch_fused<true>(cpt, epilogue, pf, nsb, grid, s, g, a, fs);
-    else
-      launch_fused<false>(cpt, epilogue, pf, nsb, grid, s, g, a, fs);
-    return check_launch("fused decode BitLinear");
+    const int rc = gamma ? launch_fused<true>(cpt, epilogue, pf, nsb, grid, s, g, a, fs)
+                         : launch_fused<false>(cpt, epilogue, pf, nsb, grid, s, g, a, fs);
+    if (rc == BTL_OK) return check_launch("fused decode BitLinear");
+    // Not co-resident on this stream's CUs: the two-launch path below (the
+    // activation kernel, then the GEMM) computes the same bits without any
+    // wait between workgroups.
+    clear_error();
   }
 
   const GemmPlan pl = plan_gemm(M, K, N, epilogue, splitk);

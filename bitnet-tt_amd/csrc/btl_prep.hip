@@ -10,6 +10,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "btl_common.h"
 
 namespace btl {
@@ -29,6 +31,72 @@ int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(BTL_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
   return BTL_OK;
+}
+
+// ------------------------------------------------------- co-residency --
+// Kernels whose workgroups wait on each other (the fused decode BitLinear,
+// the persistent step) need the whole grid resident at once.  The capacity
+// is the kernel's occupancy (workgroups per CU at its block size, from its
+// registers and LDS) times the CUs the stream may use (its CU mask, when the
+// runtime reports one, else the device's CU count).  Occupancy per kernel
+// and block size is cached (fixed by the compiled code object).
+int coresident_check(const char* who, int64_t grid, int64_t per_cu, int64_t cus) {
+  if (per_cu <= 0 || cus <= 0)
+    return set_error(BTL_ERR_LAUNCH, "%s: the device holds no workgroup of this kernel (%lld per CU, %lld CUs)", who,
+                     (long long)per_cu, (long long)cus);
+  if (grid > per_cu * cus)
+    return set_error(BTL_ERR_LAUNCH,
+                     "%s: %lld workgroups that wait on each other, but only %lld fit at once (%lld per CU x %lld CUs)",
+                     who, (long long)grid, (long long)(per_cu * cus), (long long)per_cu, (long long)cus);
+  return BTL_OK;
+}
+
+int stream_cus(hipStream_t s) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  uint32_t mask[32];  // up to 1024 CUs
+  const uint32_t words = (uint32_t)((cus + 31) / 32);
+  if (words <= 32 && hipExtStreamGetCUMask(s, words, mask) == hipSuccess) {
+    int n = 0;
+    for (uint32_t i = 0; i < words; ++i) n += __builtin_popcount(mask[i]);
+    if (n > 0 && n < cus) cus = n;
+  } else {
+    (void)hipGetLastError();
+  }
+  return cus;
+}
+
+int kernel_per_cu(const void* kernel, int threads) {
+  struct Entry {
+    const void* k;
+    int dev, threads, per_cu;
+  };
+  static Entry cache[128];
+  static int used = 0;
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  for (int i = 0; i < used; ++i)
+    if (cache[i].k == kernel && cache[i].dev == dev && cache[i].threads == threads) return cache[i].per_cu;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (used < 128) cache[used++] = Entry{kernel, dev, threads, n};
+  return n;
+}
+
+int check_coresident_launch(const char* who, const void* kernel, int threads, int64_t grid, hipStream_t s) {
+  return coresident_check(who, grid, kernel_per_cu(kernel, threads), stream_cus(s));
 }
 
 // ------------------------------------------------- numpy-order abs-sum --
@@ -217,6 +285,11 @@ extern "C" {
 
 const char* btl_last_error(void) { return g_err; }
 int btl_version(void) { return 200; }
+
+int btl_check_coresident(int64_t grid, int64_t per_cu, int64_t cus) {
+  clear_error();
+  return coresident_check("btl_check_coresident", grid, per_cu, cus);
+}
 
 int64_t btl_packed_tile_count(int64_t in_f, int64_t out_f) {
   if (in_f <= 0 || out_f <= 0) return 0;

@@ -1055,6 +1055,16 @@ static int step_grid() {
   return cus;
 }
 
+// The step's instance for F (the down projection's row chunks per thread).
+static const void* step_kernel(int64_t F, bool floor) {
+  const int cf = act_cpt(F);
+  if (floor) return cf == 1 ? reinterpret_cast<const void*>(k_decode_step_floor<1>)
+                            : reinterpret_cast<const void*>(k_decode_step_floor<2>);
+  if (cf == 1) return reinterpret_cast<const void*>(k_decode_step<1, 3, 7>);
+  if (cf == 2) return reinterpret_cast<const void*>(k_decode_step<2, 3, 7>);
+  return nullptr;
+}
+
 static int step_check_shape(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L) {
   if (M <= 0 || M > 32) return set_error(BTL_ERR_SHAPE, "btl_decode_step: M=%lld (1..32 decode rows)", (long long)M);
   if (L <= 0 || L > kStepMaxLayers)
@@ -1107,6 +1117,9 @@ int btl_decode_step_prepare(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64
   int rc = step_check_shape(M, H, F, NQKV, L);
   if (rc) return rc;
   if (!weights || !workspace) return set_error(BTL_ERR_NULL, "btl_decode_step_prepare: null pointer");
+  // every workgroup of the launch waits on others: the device must hold the grid at once
+  rc = check_coresident_launch("btl_decode_step_prepare", step_kernel(F, false), 512, step_grid(), nullptr);
+  if (rc) return rc;
   if (!aligned(workspace, 256)) return set_error(BTL_ERR_ALIGN, "btl_decode_step_prepare: workspace must be 256-byte aligned");
   const StepSizes z = step_sizes(H, F, NQKV);
   if ((int64_t)workspace_bytes < z.total)
@@ -1203,6 +1216,8 @@ int btl_decode_step(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, fl
   const int grid = step_grid();
   const int cf = act_cpt(F);
   hipStream_t s = (hipStream_t)stream;
+  rc = check_coresident_launch("btl_decode_step", step_kernel(F, false), 512, grid, s);
+  if (rc) return rc;
   if (cf == 1)
     hipLaunchKernelGGL((k_decode_step<1, 3, 7>), dim3(grid), dim3(512), 0, s, a);
   else if (cf == 2)
@@ -1243,6 +1258,8 @@ int btl_decode_step_floor(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t
   a.spin_limit = 1u << 18;
   const int grid = step_grid();
   hipStream_t s = (hipStream_t)stream;
+  rc = check_coresident_launch("btl_decode_step_floor", step_kernel(F, true), 512, grid, s);
+  if (rc) return rc;
   if (act_cpt(F) == 1)
     hipLaunchKernelGGL((k_decode_step_floor<1>), dim3(grid), dim3(512), 0, s, a);
   else

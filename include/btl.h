@@ -55,6 +55,19 @@ enum {
 #define BTL_MAX_SEGMENTS 4
 #define BTL_MAX_K 16384
 
+/* Co-residency rule of the kernels whose workgroups wait on each other
+ * (btl_bitlinear_fused's one-launch decode path, btl_decode_step and its
+ * floor): `grid` workgroups must fit on the device at once, per_cu (the
+ * kernel's occupancy at its block size) x cus (the CUs the stream may use:
+ * its CU mask, else all).  Returns BTL_OK, or BTL_ERR_LAUNCH with a message.
+ * The library applies it with the queried values before every such launch:
+ * the fused entry point then takes its two-launch path (same bits), the step
+ * refuses (btl_decode_step_prepare and btl_decode_step return the error).
+ * No counterpart in the reference (its op surfaces failures as RuntimeError,
+ * src/bitnet_tt/layers/bitlinear.py:329-330); exported so that the rule can
+ * be checked without a device. */
+int btl_check_coresident(int64_t grid, int64_t per_cu, int64_t cus);
+
 /* Last error message of the calling thread ("" if none). */
 const char* btl_last_error(void);
 /* ABI version (major*100 + minor). */

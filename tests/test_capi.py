@@ -7,6 +7,8 @@ every argument-check case is rejected before the library touches HIP.
 import ctypes
 import os
 import re
+import subprocess
+import sys
 
 import pytest
 
@@ -217,6 +219,42 @@ def test_decode_step_sizes_and_argument_checks(L):
     assert step(H=3200) == 2  # 25 superblocks of K = H exceed three register slots
     table = (N.LayerWeight * 4)()
     assert L.btl_decode_step_prepare(0, 2560, 6912, 3840, 1, table, _p(FAKE), 1 << 28) == 2
+
+
+def test_coresidency_rule(L):
+    """The rule the fused one-launch decode path and the persistent step apply
+    before launching (their workgroups wait on each other): the grid must fit
+    on the stream's CUs at once, occupancy x CUs.  A refusal is an error with a
+    message, never a launch that would wait for workgroups that cannot run."""
+    assert L.btl_check_coresident(256, 1, 256) == 0
+    assert L.btl_check_coresident(280, 2, 256) == 0
+    assert L.btl_check_coresident(257, 1, 256) == 6
+    msg = N.last_error()
+    assert "257 workgroups" in msg and "only 256 fit" in msg
+    assert L.btl_check_coresident(256, 1, 64) == 6  # a stream masked to 64 CUs
+    assert L.btl_check_coresident(10, 0, 256) == 6  # the kernel fits no workgroup at all
+    assert "no workgroup" in N.last_error()
+
+
+def test_check_after_call_mode():
+    """The opt-in check-after-call mode: off by default, switched by
+    set_check_after_call or BTL_CHECK_AFTER_CALL, and carried per layer."""
+    from bitnet_tt import ternary_matmul as T
+    from bitnet_tt.layers.bitlinear import Linear
+
+    assert T.check_after_call_enabled() is False
+    T.set_check_after_call(True)
+    try:
+        assert T.check_after_call_enabled() is True
+    finally:
+        T.set_check_after_call(False)
+    code = "from bitnet_tt import ternary_matmul as T; print(T.check_after_call_enabled())"
+    env = dict(os.environ, BTL_CHECK_AFTER_CALL="1",
+               PYTHONPATH=os.pathsep.join([os.path.join(REPO, "bitnet-tt_amd"), REPO]))
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+    assert r.stdout.strip() == "True", r.stderr
+    assert Linear(64, 64, check_errors=True).check_errors is True
+    assert Linear(64, 64).check_errors is None
 
 
 def _clear_share(L, m, KS):

@@ -262,15 +262,15 @@ def test_c4_full_model_per_call_chain_exact(orc, c4_model):
 # numpy quantiser).  The GPU follows a fixed fp32 order for the RMS statistic
 # (bit-exact with the oracle above); the reference order differs from it in the
 # last bit of 1/rms now and then, which flips ~1e-5 of the normalised bf16
-# values and ~2e-7 of the int8 codes per BitLinear.  A flipped code moves one
-# output by one ternary weight times its scale, and through the residual stream
-# the difference spreads over 30 layers; on the CPU with the same shapes the
-# oracle chain and the reference-order chain end 0.6 % apart normwise (1.1 %
-# in the largest element, PCC 0.99998).  Bounds: each single BitLinear output
-# within 1e-2 of the largest reference magnitude (the per-BitLinear bar), and
-# after the whole chain normwise within 1e-2, the largest element within 5e-2
-# of the largest reference magnitude, PCC >= 0.9999.
-CHAIN_REL_FRO, CHAIN_MAX_REL, CHAIN_PCC, ONE_BITLINEAR_MAX_REL = 1e-2, 5e-2, 0.9999, 1e-2
+# values and ~1.6e-7 of the int8 codes per BitLinear: ~2.3 flipped codes in the
+# 14 M codes of a 30-layer batch-32 step.  One flipped code moves a whole output
+# row by one quantisation step, and the chain carries that on: on the CPU, a
+# single flipped code in layer 0 ends the 30-layer chain 2.2 % apart normwise,
+# 4.0 % in the largest element (relative to the largest magnitude), PCC 0.99975.
+# Bounds: each single BitLinear within 1e-2 of the largest reference magnitude
+# (the per-BitLinear bar); the 30-layer chain within what a few early flipped
+# codes give: normwise 5e-2, largest element 1e-1, PCC >= 0.999.
+CHAIN_REL_FRO, CHAIN_MAX_REL, CHAIN_PCC, ONE_BITLINEAR_MAX_REL = 5e-2, 1e-1, 0.999, 1e-2
 
 
 def test_c4_persistent_step_against_reference_order_chain(orc, c4_model):
