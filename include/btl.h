@@ -93,7 +93,10 @@ int btl_choose_splitk(int64_t M, int64_t K, int64_t N, int epilogue);
  * passes the row sums (the prefill BitLinear does).  info[6] = {kind (0
  * decode, 1 prefill 128x256 / 64x256 tiles, 2 prefill wide tiles), rows per
  * tile, column tiles of 32 per tile (kind 1: slots; relu2 pairs gate and up),
- * split-K factor, k-step groups (kind 2), column tiles per wave (kind 2)}.  */
+ * split-K factor, k-step groups (kind 2), column tiles per wave (kind 2)}.
+ * The answer describes a call whose acc_out is NULL or 16-byte aligned: the
+ * wide tiles store accumulators 16 bytes at a time, so a call with an acc_out
+ * aligned to 4 bytes only runs the kind-1 tiles instead. */
 int btl_gemm_tiling(int64_t M, int64_t K, int64_t N, int epilogue, int rowsum_given, int32_t* info);
 int64_t btl_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int epilogue, int splitk);
 int64_t btl_fused_workspace_bytes(int64_t M, int64_t K, int64_t N, int epilogue, int splitk);
@@ -213,15 +216,16 @@ int btl_bitlinear_fused(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, co
  * (each GPU the library runs on keeps its copy until the process ends); it
  * calls no allocating routine.  Shapes whose workspace
  * (btl_fused_workspace_bytes) exceeds that size are rejected with
- * BTL_ERR_WORKSPACE; every decode shape (M <= 32, K <= 16384) without a
- * split-K request fits.  error_word: optional device uint32 the caller owns;
+ * BTL_ERR_WORKSPACE; every decode shape (M <= 32, K <= 16384, N <= 16384,
+ * either epilogue) without a split-K request fits (the largest needs
+ * 2,630,656 bytes).  error_word: optional device uint32 the caller owns;
  * a bounded wait that runs out stores a non-zero value there (the call's
  * outputs are then invalid; the library never clears it).  Every call on a
  * device shares that device's scratch and leaves it ready for the next call;
  * calls that overlap on one device (concurrent streams or threads) race on
  * it and must be serialised by the caller.  The first call on a device
  * clears the scratch with a kernel on `stream`. */
-#define BTL_NOALLOC_SCRATCH_BYTES (2 << 20)
+#define BTL_NOALLOC_SCRATCH_BYTES (3 << 20)
 int btl_bitlinear_fused_noalloc(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const uint16_t* gamma,
                                 float norm_eps, const uint32_t* wdev, int64_t N, const float* seg_scale,
                                 const int64_t* seg_end, int nseg, int epilogue, const uint16_t* residual,

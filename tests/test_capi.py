@@ -257,6 +257,24 @@ def test_check_after_call_mode():
     assert Linear(64, 64).check_errors is None
 
 
+def test_noalloc_scratch_holds_every_decode_shape(L):
+    """The header's promise for btl_bitlinear_fused_noalloc: every decode shape
+    (M <= 32, K and N multiples of 32 up to 16384, either epilogue, no split-K
+    request) has a workspace within BTL_NOALLOC_SCRATCH_BYTES."""
+    text = open(HEADER).read()
+    limit = eval(re.search(r"#define BTL_NOALLOC_SCRATCH_BYTES \((\d+ << \d+)\)", text).group(1))
+    worst = 0
+    for epi, step in ((0, 32), (1, 64)):
+        for k in range(32, 16385, 32):
+            for n in range(step, 16385, step):
+                worst = max(worst, L.btl_fused_workspace_bytes(32, k, n, epi, 0))
+    assert 0 < worst <= limit, (worst, limit)
+    # M below 32 uses the same 32-row blocks
+    assert L.btl_fused_workspace_bytes(1, 16288, 8192, 0, 0) <= limit
+    # a prefill shape does not fit, and is refused by the entry point (GPU test)
+    assert L.btl_fused_workspace_bytes(2048, 6912, 2560, 0, 0) > limit
+
+
 def _clear_share(L, m, KS):
     out = (ctypes.c_int64 * (16 * KS))()
     assert L.btl_decode_step_clear_share(m, KS, out, 16 * KS) == 0

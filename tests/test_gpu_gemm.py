@@ -549,3 +549,89 @@ def test_check_raises_on_sticky_error_word(orc):
     out = ternary_matmul(H.to_dev_bf16(xb), pw)
     check()
     assert np.array_equal(H.bits_of(out), ref["out"])
+
+
+def test_check_after_call_raises_at_the_call(orc):
+    """Check-after-call mode: a call whose launch finds the error word set (as
+    a bounded wait that ran out sets it; here set from the host) raises
+    RuntimeError at that call, as the reference's op raises at its call; the
+    workspace is reset and the next call returns the oracle's bits."""
+    from bitnet_tt.layers.bitlinear import Linear
+    from bitnet_tt.ternary_matmul import PackedTernaryWeight, ternary_matmul
+
+    m, k, n = 32, 512, 256
+    xb = H.activations(orc, m, k, seed=15)
+    w = H.ternary(k, n, seed=16)
+    pw = PackedTernaryWeight(device_weight(orc, w), k, n, (0.02,), (n,))
+    ref = orc.bitlinear(xb, w, [0.02])
+    out = ternary_matmul(H.to_dev_bf16(xb), pw, check_errors=True)
+    assert np.array_equal(H.bits_of(out), ref["out"])
+    key = next(key for key in N._workspaces if key[0] == "bitlinear" and key[1] == str(H.dev()))
+    ws = N._workspaces[key]
+    off = int(N.lib().btl_fused_error_offset())
+    ws[off:off + 4].view(torch.int32).fill_(1)
+    with pytest.raises(RuntimeError, match="bounded wait ran out"):
+        ternary_matmul(H.to_dev_bf16(xb), pw, check_errors=True)
+    out = ternary_matmul(H.to_dev_bf16(xb), pw, check_errors=True)
+    assert np.array_equal(H.bits_of(out), ref["out"])
+    lin = Linear(k, n, H.dev(), check_errors=True)
+    lin.load_pretransposed_weight(w.astype(np.float32), scale=0.02)
+    ws[off:off + 4].view(torch.int32).fill_(1)
+    with pytest.raises(RuntimeError, match="bounded wait ran out"):
+        lin(H.to_dev_bf16(xb))
+    assert np.array_equal(H.bits_of(lin(H.to_dev_bf16(xb))), ref["out"])
+
+
+def _hip():
+    import ctypes
+
+    for name in ("libamdhip64.so", "libamdhip64.so.7", "libamdhip64.so.6"):
+        try:
+            return ctypes.CDLL(name)
+        except OSError:
+            continue
+    pytest.skip("libamdhip64 not found")
+
+
+def test_cu_masked_stream_coresidency(orc):
+    """A stream limited to 32 CUs (hipExtStreamCreateWithCUMask): the
+    persistent step (one workgroup per CU of the device, all waiting on each
+    other) is refused with RuntimeError before anything is launched, and the
+    fused decode BitLinear, whose one-launch grid does not fit there, takes
+    its two-launch path and returns the oracle's bits."""
+    import ctypes
+
+    from bitnet_tt.config import BitNetMiniConfig
+    from bitnet_tt.decode import BitLinearDecodeStep
+    from bitnet_tt.ternary_matmul import PackedTernaryWeight, ternary_matmul
+
+    hip = _hip()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    words = (cus + 31) // 32
+    mask = (ctypes.c_uint32 * words)(*([0xFFFFFFFF] + [0] * (words - 1)))
+    raw = ctypes.c_void_p()
+    assert hip.hipExtStreamCreateWithCUMask(ctypes.byref(raw), ctypes.c_uint32(words), mask) == 0
+    try:
+        back = (ctypes.c_uint32 * words)()
+        assert hip.hipExtStreamGetCUMask(raw, ctypes.c_uint32(words), back) == 0
+        if sum(bin(v).count("1") for v in back) != 32:
+            pytest.skip("the runtime does not report the stream's CU mask")
+        s = torch.cuda.ExternalStream(raw.value)
+        m, k, f = 32, 2560, 6912
+        xb = H.activations(orc, m, k, seed=21)
+        gq, uq = H.ternary(f, k, seed=22), H.ternary(f, k, seed=23)
+        w = np.ascontiguousarray(np.concatenate([gq, uq]).T)
+        pw = PackedTernaryWeight(device_weight(orc, w), k, 2 * f, (0.02, 0.03), (f, 2 * f))
+        ref = orc.gate_up_relu2(xb, w, 0.02, 0.03)
+        step = BitLinearDecodeStep.random_init(BitNetMiniConfig(num_layers=1), H.dev(), seed=24).alloc_buffers(seed=25)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            out = ternary_matmul(H.to_dev_bf16(xb), pw, epilogue="relu2_mul", check_errors=True)
+            s.synchronize()
+            assert np.array_equal(H.bits_of(out), ref["h"])
+            with pytest.raises(RuntimeError, match="fit at once"):
+                step.step_persistent()
+        s.synchronize()
+    finally:
+        torch.cuda.synchronize()
+        hip.hipStreamDestroy(raw)
