@@ -20,6 +20,12 @@ OUT = os.path.join(_PKG, "_lib", "libbtl.so")
 # Measurement build: the same sources with -DBTL_TRACE (phase timestamps of the
 # persistent decode step, read by bench.py --step-trace).  Not loaded otherwise.
 OUT_TRACE = os.path.join(_PKG, "_lib", "libbtl_trace.so")
+# Host-sanitizer build: the host code (argument checks, planning, layouts)
+# instrumented with AddressSanitizer and UBSan; device code as in the product
+# build.  Loaded only by tests/host_asan.sh (BTL_LIBRARY) on the CPU.
+OUT_ASAN = os.path.join(_PKG, "_lib", "libbtl_hostasan.so")
+ASAN_FLAGS = ["-Xarch_host", "-fsanitize=address,undefined", "-Xarch_host", "-fno-sanitize-recover=undefined",
+              "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_host", "-g"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -46,16 +52,17 @@ def hipcc() -> str:
     return "hipcc"
 
 
-def build_native(verbose: bool = False, trace: bool = False) -> str:
+def build_native(verbose: bool = False, trace: bool = False, asan: bool = False) -> str:
     """Compile libbtl.so (trace=True: the -DBTL_TRACE measurement build,
-    libbtl_trace.so)."""
+    libbtl_trace.so; asan=True: the host-sanitizer build, libbtl_hostasan.so)."""
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    out = OUT_TRACE if trace else OUT
+    out = OUT_TRACE if trace else OUT_ASAN if asan else OUT
     os.makedirs(os.path.dirname(out), exist_ok=True)
     tmp = out + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, *(["-DBTL_TRACE"] if trace else []), f"-I{INCLUDE}", "-o", tmp, *sources]
+    extra = (["-DBTL_TRACE"] if trace else []) + (ASAN_FLAGS if asan else [])
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, f"-I{INCLUDE}", "-o", tmp, *sources]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     errs = "\n".join(ln for ln in proc.stderr.splitlines() if noise not in ln)
@@ -70,4 +77,4 @@ def build_native(verbose: bool = False, trace: bool = False) -> str:
 if __name__ == "__main__":
     import sys
 
-    print(build_native(verbose=True, trace="--trace" in sys.argv[1:]))
+    print(build_native(verbose=True, trace="--trace" in sys.argv[1:], asan="--asan" in sys.argv[1:]))

@@ -14,7 +14,9 @@ import os
 import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "_lib", "libbtl.so")
+# BTL_LIBRARY names another build of the same library (the host-sanitizer
+# build of tests/host_asan.sh); the default is the in-tree product build.
+LIB_PATH = os.environ.get("BTL_LIBRARY") or os.path.join(_HERE, "_lib", "libbtl.so")
 
 # Status codes and epilogue modes (include/btl.h).
 BTL_OK = 0

@@ -33,7 +33,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# BTL_ORACLE_LIBRARY names another build of the oracle (the host-sanitizer
+# build of tests/host_asan.sh).
+_LIB_PATH = os.environ.get("BTL_ORACLE_LIBRARY") or os.path.join(_HERE, "liboracle.so")
 _lib = None
 
 ACT_EPS = 1e-5  # quantization.py:63
