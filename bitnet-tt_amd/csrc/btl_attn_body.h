@@ -1,0 +1,331 @@
+// Decode attention of one (user, key-value head) pair on one 512-thread
+// workgroup, shared by the standalone decode-attention kernel and the
+// persistent decode step (so both give the same bits).  The arithmetic
+// follows src/bitnet_tt/layers/attention.py:1040-1262 (head split
+// :1088-1096, RoPE :1103-1140, cache update :1153-1171, SDPA decode
+// :1177-1231, head concat :1239-1254; frequencies utils/rope.py:7-23).
+//
+// Caches [B, Hkv, S, D] bf16; D = 128; G <= 4 query heads per key-value head.
+// A round covers 512 cached positions, 64 per wave; every wave issues all of
+// its key and value loads (256 B per lane each) before computing, so a round
+// is one memory round trip (at context 512 the whole context is one round,
+// and the caller may issue it before the new token's q, k, v exist).
+//  - Scores: v_mfma_f32_16x16x32_bf16, the G rotated query rows (padded to
+//    16 with zeros) against 16 cached key rows per MFMA (keys contiguous
+//    along D, the contraction, so the B operands load straight from the
+//    cache).
+//  - Softmax: the running (online) form in fp32 per wave and head.
+//  - Probability-weighted values: MFMA as well.  The wave's value rows go
+//    to LDS 32 at a time (rows padded by 8 bytes, so the four position
+//    groups of an operand read fall in different banks) and are read back as
+//    B operands (8 positions of one dimension per lane); the probabilities
+//    enter as two bf16 parts, p = hi + lo, which keeps them to ~16 bits.
+//  - The waves' (max, sum, output) partials and the new position (rotated k,
+//    v) merge in LDS in a fixed order.
+#pragma once
+
+#include "btl_act_row.h"
+#include "btl_common.h"
+
+namespace btl {
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kAtD = 128;                        // head dimension
+constexpr int kAtWaves = 8;                      // waves per workgroup
+constexpr int kAtPosWave = 64;                   // positions per wave and round
+constexpr int kAtRound = kAtWaves * kAtPosWave;  // positions per round
+constexpr int kAtMaxG = 4;                       // query heads per key-value head
+constexpr int kAtVPitch = kAtD + 4;              // bf16 per LDS value row (8-byte pad)
+constexpr int kAtVRows = 32;                     // value rows of a wave staged at once
+
+struct AttnSmem {
+  uint16_t in[kAtMaxG + 2][kAtD];                   // the new token's q rows, k row, v row (as produced)
+  uint16_t q[kAtMaxG][kAtD];                        // rotated query rows
+  uint16_t nw[2][kAtD];                             // the new k (rotated) and v rows
+  float snew[kAtMaxG];                              // scores of the new position
+  float ml[kAtWaves][kAtMaxG][2];                   // each wave's running max and sum
+  uint16_t p[kAtWaves][2][kAtMaxG][kAtPosWave];     // probabilities hi, lo
+  // 32 value rows of each wave; after the last round, each wave's
+  // unnormalised output [G][D] fp32 (the LDS is reused)
+  uint16_t v[kAtWaves][kAtVRows][kAtVPitch];
+};
+static_assert(sizeof(float) * kAtWaves * kAtMaxG * kAtD <= sizeof(uint16_t) * kAtWaves * kAtVRows * kAtVPitch,
+              "output partials fit in the value buffer");
+
+struct AttnPair {
+  const float* rcos;  // [S, D/2] cos of position x frequency i
+  const float* rsin;  // [S, D/2]
+  uint16_t* kc;       // [B, Hkv, S, D]
+  uint16_t* vc;
+  int Hkv, G, S, b, hk, pos;
+  float scale;
+  int adjacent;  // 1: RoPE pairs (2i, 2i+1); 0: (i, i + D/2)
+  __device__ __forceinline__ bool pos_ok() const { return pos >= 0 && pos < S; }
+  __device__ __forceinline__ int nold() const { return pos_ok() ? pos : 0; }  // cached positions [0, nold)
+  __device__ __forceinline__ int64_t kv_base() const { return ((int64_t)b * Hkv + hk) * S; }
+};
+
+// Rotates one pair (x0, x1) by the angle of frequency i at the position.
+__device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, float& y0, float& y1) {
+  y0 = x0 * c - x1 * s;
+  y1 = x1 * c + x0 * s;
+}
+
+// Max and sum over the 16 lanes of a row (lanes 0..15 hold the values).
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, xor_partner<8>(v));
+  v = fmaxf(v, xor_partner<4>(v));
+  v = fmaxf(v, xor_partner<2>(v));
+  v = fmaxf(v, xor_partner<1>(v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v = v + xor_partner<8>(v);
+  v = v + xor_partner<4>(v);
+  v = v + xor_partner<2>(v);
+  v = v + xor_partner<1>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+}
+
+__device__ __forceinline__ float wexp(float m, float M) { return m == -__builtin_inff() ? 0.0f : __expf(m - M); }
+
+// A wave's key and value rows of round rd: K operands (4 blocks of 16
+// positions x 4 k-steps) and value pieces (dims 8 r16 .. + 8 of row 4 t + grp).
+struct AttnRound {
+  uint4 kr[4][kAtD / 32];
+  uint4 vr[16];
+};
+
+__device__ __forceinline__ void att_load_round(const AttnPair& a, int rd, AttnRound& r) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int base = rd * kAtRound + kAtPosWave * wv;
+  const int64_t kvb = a.kv_base();
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    const int row = min(base + 16 * blk + r16, a.S - 1);
+    const uint16_t* kp = a.kc + (kvb + row) * kAtD + 8 * grp;
+#pragma unroll
+    for (int ks = 0; ks < kAtD / 32; ++ks) r.kr[blk][ks] = *reinterpret_cast<const uint4*>(kp + 32 * ks);
+  }
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    const int row = min(base + 4 * t + grp, a.S - 1);
+    r.vr[t] = *reinterpret_cast<const uint4*>(a.vc + (kvb + row) * kAtD + 8 * r16);
+  }
+}
+
+// Whether this wave has cached positions in round 0 (then the caller issues
+// att_load_round(a, 0, r) before att_body).
+__device__ __forceinline__ bool att_wave_work(const AttnPair& a) {
+  return kAtPosWave * (int)(threadIdx.x >> 6) < a.nold();
+}
+
+// Everything after the first round's loads: RoPE of the group's query rows
+// and the new k row (the new rows go to LDS and to the caches), scores,
+// online softmax, probability-weighted values, merge.  s.in holds the new
+// token's rows (q rows 0..G-1, k at kAtMaxG, v at kAtMaxG + 1) and every
+// thread has passed a barrier since they were written.  Returns, for
+// threads tid < G D (head tid / D, dimension tid % D), the bf16 output
+// (zero for a position outside [0, S)); the other threads return 0.  Ends
+// with every LDS access of the body complete (the caller may reuse s after
+// a barrier).
+__device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, AttnRound& r) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int G = a.G;
+  const bool pos_ok = a.pos_ok();
+  const int nold = a.nold();
+  const int nrounds = (nold + kAtRound - 1) / kAtRound;
+  const int pc = pos_ok ? a.pos : 0;
+  const int64_t kvb = a.kv_base();
+  const int half = kAtD / 2;
+  const int r16 = lane & 15, grp = lane >> 4;
+  {
+    const int i = tid & (half - 1);
+    const int d0 = a.adjacent ? 2 * i : i, d1 = a.adjacent ? 2 * i + 1 : i + half;
+    const float rc = a.rcos[pc * half + i], rs = a.rsin[pc * half + i];
+    const int u = tid / half;  // 0..7: query rows 0..3, then the k row, then v
+    if (u < kAtMaxG) {
+      float y0 = 0.0f, y1 = 0.0f;
+      if (u < G && pos_ok) rope_pair(bf2f(s.in[u][d0]), bf2f(s.in[u][d1]), rc, rs, y0, y1);
+      s.q[u][d0] = f2bf(y0);
+      s.q[u][d1] = f2bf(y1);
+    } else if (u == kAtMaxG) {
+      float y0, y1;
+      rope_pair(bf2f(s.in[kAtMaxG][d0]), bf2f(s.in[kAtMaxG][d1]), rc, rs, y0, y1);
+      const uint16_t k0 = f2bf(y0), k1 = f2bf(y1);
+      s.nw[0][d0] = k0;
+      s.nw[0][d1] = k1;
+      if (pos_ok) {
+        uint16_t* dst = a.kc + (kvb + a.pos) * kAtD;
+        dst[d0] = k0;
+        dst[d1] = k1;
+      }
+    } else if (u == kAtMaxG + 1) {
+      const int d = 2 * i;
+      const uint32_t vnew = *reinterpret_cast<const uint32_t*>(&s.in[kAtMaxG + 1][d]);
+      *reinterpret_cast<uint32_t*>(&s.nw[1][d]) = vnew;
+      if (pos_ok) *reinterpret_cast<uint32_t*>(a.vc + (kvb + a.pos) * kAtD + d) = vnew;
+    }
+  }
+  __syncthreads();
+  if (wv < G) {  // score of the new position for head wv (lanes over D, fixed-order sum)
+    const float d = bf2f(s.q[wv][2 * lane]) * bf2f(s.nw[0][2 * lane]) +
+                    bf2f(s.q[wv][2 * lane + 1]) * bf2f(s.nw[0][2 * lane + 1]);
+    const float sn = wave_xor_sum(d) * a.scale;
+    if (lane == 0) s.snew[wv] = sn;
+  }
+  // query operands (A: row r16 = head, k-step ks: dims 32 ks + 8 grp ..)
+  v8bf qa[kAtD / 32];
+#pragma unroll
+  for (int ks = 0; ks < kAtD / 32; ++ks) {
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (r16 < G) v = *reinterpret_cast<const uint4*>(&s.q[r16][32 * ks + 8 * grp]);
+    qa[ks] = __builtin_bit_cast(v8bf, v);
+  }
+
+  // running softmax state of this wave, per head (lanes 0..15 hold the
+  // output rows: acc o[m][j] = head j, dimension 16 m + r16)
+  float mrun[kAtMaxG], lrun[kAtMaxG];
+  v4f o[kAtD / 16];
+#pragma unroll
+  for (int g = 0; g < kAtMaxG; ++g) {
+    mrun[g] = -__builtin_inff();
+    lrun[g] = 0.0f;
+  }
+#pragma unroll
+  for (int m = 0; m < kAtD / 16; ++m) o[m] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  for (int rd = 0; rd < nrounds; ++rd) {
+    const int base = rd * kAtRound + kAtPosWave * wv;
+    if (base >= nold) break;  // wave-uniform: nothing cached from here on
+    if (rd > 0) att_load_round(a, rd, r);
+    // scores: 4 blocks of 16 positions
+    v4f sc[4];
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      sc[blk] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < kAtD / 32; ++ks)
+        sc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], __builtin_bit_cast(v8bf, r.kr[blk][ks]), sc[blk], 0,
+                                                          0, 0);
+    }
+    // online softmax per head over the wave's 64 positions (lanes 0..15:
+    // block blk's position 16 blk + lane)
+#pragma unroll
+    for (int g = 0; g < kAtMaxG; ++g) {
+      float s4[4];
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        const bool ok = lane < 16 && base + 16 * blk + lane < nold;
+        s4[blk] = ok ? sc[blk][g] * a.scale : -__builtin_inff();
+        mx = fmaxf(mx, s4[blk]);
+      }
+      mx = row16_max(mx);
+      const float mn = fmaxf(mrun[g], mx);
+      const float alpha = wexp(mrun[g], mn);
+      float sm = 0.0f;
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        const float e = wexp(s4[blk], mn);
+        sm += e;
+        if (lane < 16) {
+          const uint16_t hi = f2bf(e);
+          s.p[wv][0][g][16 * blk + lane] = hi;
+          s.p[wv][1][g][16 * blk + lane] = f2bf(e - bf2f(hi));
+        }
+      }
+      sm = row16_sum(sm);
+      lrun[g] = lrun[g] * alpha + sm;
+      mrun[g] = mn;
+      // rows j of the output accumulators are heads: lanes 0..15 hold them
+#pragma unroll
+      for (int m = 0; m < kAtD / 16; ++m) o[m][g] *= alpha;
+    }
+    // probability-weighted values: 2 k-steps of 32 positions x 8 column
+    // blocks of 16 dimensions, probabilities as hi + lo parts; each k-step's
+    // 32 value rows staged in LDS just before it (rows past the context as
+    // zeros, whatever the cache holds there: a zero probability times a
+    // non-finite value is NaN)
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int tt = 8 * k2 + t;
+        const bool ok = base + 4 * tt + grp < nold;
+        const uint4 v = ok ? r.vr[tt] : make_uint4(0u, 0u, 0u, 0u);
+        uint2* dst = reinterpret_cast<uint2*>(&s.v[wv][4 * t + grp][8 * r16]);
+        dst[0] = make_uint2(v.x, v.y);
+        dst[1] = make_uint2(v.z, v.w);
+      }
+      __builtin_amdgcn_wave_barrier();  // the wave's own LDS writes are read back by other lanes
+      v8bf pa[2];
+#pragma unroll
+      for (int part = 0; part < 2; ++part) {
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (r16 < G) v = *reinterpret_cast<const uint4*>(&s.p[wv][part][r16][32 * k2 + 8 * grp]);
+        pa[part] = __builtin_bit_cast(v8bf, v);
+      }
+#pragma unroll
+      for (int m = 0; m < kAtD / 16; ++m) {
+        // B operand: dimension 16 m + r16 of positions 32 k2 + 8 grp + [0, 8)
+        const uint16_t* col = &s.v[wv][8 * grp][16 * m + r16];
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = (uint32_t)col[(2 * e) * kAtVPitch] | ((uint32_t)col[(2 * e + 1) * kAtVPitch] << 16);
+        const v8bf vb = __builtin_bit_cast(v8bf, make_uint4(w[0], w[1], w[2], w[3]));
+        o[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vb, o[m], 0, 0, 0);
+        o[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vb, o[m], 0, 0, 0);
+      }
+      __builtin_amdgcn_wave_barrier();  // reads done before the buffers are rewritten
+    }
+  }
+
+  // merge: every wave's partial, then the new position, in a fixed order
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < kAtMaxG; ++g) {
+      s.ml[wv][g][0] = mrun[g];
+      s.ml[wv][g][1] = lrun[g];
+    }
+  }
+  __syncthreads();  // every wave is done with its value rows: the output partials reuse them
+  float(*s_o)[kAtMaxG][kAtD] = reinterpret_cast<float(*)[kAtMaxG][kAtD]>(&s.v[0][0][0]);
+  if (lane < 16) {
+#pragma unroll
+    for (int m = 0; m < kAtD / 16; ++m)
+#pragma unroll
+      for (int g = 0; g < kAtMaxG; ++g) s_o[wv][g][16 * m + lane] = o[m][g];
+  }
+  __syncthreads();
+  uint16_t res = 0;
+  {
+    const int g = tid / kAtD, d = tid % kAtD;  // 512 threads: 4 heads x 128 dims
+    if (g < G) {
+      const float snew = s.snew[g];
+      float M = snew;
+#pragma unroll
+      for (int w = 0; w < kAtWaves; ++w) M = fmaxf(M, s.ml[w][g][0]);
+      const float wn = __expf(snew - M);
+      float L = wn;
+      float O = wn * bf2f(s.nw[1][d]);
+#pragma unroll
+      for (int w = 0; w < kAtWaves; ++w) {
+        const float ww = wexp(s.ml[w][g][0], M);
+        L += ww * s.ml[w][g][1];
+        O += ww * s_o[w][g][d];
+      }
+      const float inv = pos_ok ? 1.0f / L : 0.0f;
+      res = f2bf(O * inv);
+    }
+  }
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this thread's LDS reads are done
+  return res;
+}
+
+}  // namespace btl
