@@ -359,6 +359,46 @@ def full_step_timing(step, torch, s, args, ctx=512):
     torch.cuda.synchronize()
     us_full = (time.perf_counter() - t0) * 1e6 / args.steps
     del g
+    # the same step as one launch (btl_decode_step_full): attention on the
+    # GEMM workgroups between QKV and o_proj; its bits equal step_full's
+    state = (step.hidden.clone(), [(kv.key_cache.clone(), kv.value_cache.clone()) for kv in step.kv])
+
+    def restore():
+        step.hidden.copy_(state[0])
+        for kv, (k, v) in zip(step.kv, state[1]):
+            kv.key_cache.copy_(k)
+            kv.value_cache.copy_(v)
+
+    with torch.cuda.stream(s):
+        restore()
+        step.step_full()
+    torch.cuda.synchronize()
+    ref = step.hidden.clone()
+    with torch.cuda.stream(s):
+        restore()
+        step.step_persistent_full()
+    torch.cuda.synchronize()
+    step.check()
+    full_bits_equal = bool(torch.equal(step.hidden.view(torch.int16), ref.view(torch.int16)))
+    gp = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gp, stream=s):
+        step.step_persistent_full()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        for _ in range(max(args.warmup, 1)):
+            gp.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with torch.cuda.stream(s):
+        e0.record(s)
+        for _ in range(args.steps):
+            gp.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    us_one = (time.perf_counter() - t0) * 1e6 / args.steps
+    us_one_event = e0.elapsed_time(e1) * 1e3 / args.steps
+    step.check()
+    del gp, state
     n = len(step.layers)
     ga = torch.cuda.CUDAGraph()
     with torch.cuda.graph(ga, stream=s):
@@ -387,6 +427,9 @@ def full_step_timing(step, torch, s, args, ctx=512):
     return {
         "workload": f"30 layers x (QKV, decode attention over context {ctx}, o_proj, gate||up, down), batch 32",
         "us_per_step": round(us_full, 1),
+        "us_per_step_one_launch": round(us_one, 1),
+        "us_per_step_one_launch_event": round(us_one_event, 1),
+        "one_launch_bits_equal": full_bits_equal,
         "attention_us_per_layer": round(us_att, 2),
         "attention_bytes_per_launch": nbytes,
         "attention_GBps": round(nbytes / (us_att * 1e-6) / 1e9, 1),
@@ -829,7 +872,8 @@ def main():
     full = None
     if not args.no_attention:
         full = full_step_timing(step, torch, s, args)
-        log(f"[bench] full step with decode attention (context 512): {full['us_per_step']:.1f} us; attention "
+        log(f"[bench] full step with decode attention (context 512): {full['us_per_step']:.1f} us as 150 launches, "
+            f"{full['us_per_step_one_launch']:.1f} us as one launch (bits equal: {full['one_launch_bits_equal']}); attention "
             f"{full['attention_us_per_layer']:.2f} us per layer, {full['attention_GBps']:.0f} GB/s, "
             f"{100 * full['attention_roofline_frac']:.1f} % of HBM")
 

@@ -109,6 +109,11 @@ EXPORTS = {
     "btl_decode_step": ([_I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P, _P, _SZ, _P], _I),
     "btl_decode_step_floor": ([_I64, _I64, _I64, _I64, _I64, _P, _SZ, _P], _I),
     "btl_decode_step_clear_share": ([_I, _I64, _P, _I64], _I),
+    "btl_decode_step_attention_prepare": ([_I64, _I64, _I64, _I64, _I64, _P, _P, _P, _SZ], _I),
+    "btl_decode_step_full": (
+        [_I64, _I64, _I64, _I64, _I64, _F, _I64, _I64, _P, _P, _P, _I, _F, _P, _P, _P, _P, _P, _SZ, _P],
+        _I,
+    ),
     "btl_gemm_i8t2_dot4": ([_P, _P, _I64, _I64, _I64, _P, _P, _P], _I),
     "btl_lm_head_weight_bytes": ([_I64, _I64], _I64),
     "btl_lm_head_workspace_bytes": ([], _I64),

@@ -345,12 +345,13 @@ class BitLinearDecodeStep:
             self._st = arr
         return self._st
 
-    def step_persistent(self):
-        """The whole step's BitLinears as one btl_decode_step launch (every
-        layer's QKV, o_proj, gate||up and down; o_proj reads the attention
-        output buffer).  Bit-identical to step_per_call.  The first call on a
-        stream prepares that stream's workspace (a synchronous copy of the
-        weight table), so it must happen before a graph capture."""
+    def _step_workspace(self, attention: bool):
+        """This stream's workspace of the one-launch step, prepared for the
+        weight table (and, with ``attention``, for the KV-cache table) by
+        synchronous copies: the first call on a stream must come before a
+        graph capture."""
+        import ctypes
+
         import torch
 
         c = self.config
@@ -359,9 +360,6 @@ class BitLinearDecodeStep:
         if qd != H:
             raise ValueError(f"btl_decode_step needs the attention width ({qd}) equal to hidden ({H})")
         nl = len(self.layers)
-        for t, name in ((self.hidden, "hidden"), (self.attn_out, "attn_out"), (self.qkv_out, "qkv_out"),
-                        (self.ffn_h, "ffn_h")):
-            N.require_cuda(t, name)
         L = N.lib()
         table = self._step_table()
         dev = self.hidden.device
@@ -370,7 +368,14 @@ class BitLinearDecodeStep:
         if capturing and not N.has_workspace(dev, nbytes, "step"):
             raise RuntimeError("run one eager decode step on this stream before capturing it in a graph")
         ws = N.workspace(dev, nbytes, kind="step", error_offset=int(L.btl_decode_step_error_offset()))
-        if N.workspace_prepared_for(ws) is not table:
+        caches = None
+        if attention:
+            if getattr(self, "kv", None) is None:
+                raise RuntimeError("step_persistent_full needs alloc_attention() first")
+            caches = tuple((kv.key_cache.data_ptr(), kv.value_cache.data_ptr()) for kv in self.kv)
+        ready = getattr(self, "_ws_caches", {})
+        self._ws_caches = ready
+        if N.workspace_prepared_for(ws) is not table or (attention and ready.get(ws.data_ptr()) != caches):
             if capturing:
                 raise RuntimeError("run one eager decode step on this stream before capturing it in a graph")
             torch.cuda.current_stream(dev).synchronize()  # earlier launches on this workspace are done
@@ -379,13 +384,69 @@ class BitLinearDecodeStep:
                 N.check(L.btl_decode_step_prepare(B, H, F, c.qkv_dim, nl, table, N.ptr(ws), ws.numel()),
                         "btl_decode_step_prepare")
                 N.set_workspace_prepared_for(ws, table)
+                cached = ready.get(ws.data_ptr())
+                if cached is not None:
+                    kp = (ctypes.c_void_p * nl)(*[k for k, _ in cached])
+                    vp = (ctypes.c_void_p * nl)(*[v for _, v in cached])
+                    N.check(L.btl_decode_step_attention_prepare(B, H, F, c.qkv_dim, nl, kp, vp, N.ptr(ws),
+                                                                ws.numel()),
+                            "btl_decode_step_attention_prepare")
 
+            if attention:
+                ready[ws.data_ptr()] = caches
             prepare()
             N.set_workspace_reset(ws, prepare)
+        return ws
+
+    def step_persistent(self):
+        """The whole step's BitLinears as one btl_decode_step launch (every
+        layer's QKV, o_proj, gate||up and down; o_proj reads the attention
+        output buffer).  Bit-identical to step_per_call.  The first call on a
+        stream prepares that stream's workspace (a synchronous copy of the
+        weight table), so it must happen before a graph capture."""
+        c = self.config
+        B = self.batch
+        H, F = c.hidden_size, c.intermediate_size
+        nl = len(self.layers)
+        for t, name in ((self.hidden, "hidden"), (self.attn_out, "attn_out"), (self.qkv_out, "qkv_out"),
+                        (self.ffn_h, "ffn_h")):
+            N.require_cuda(t, name)
+        ws = self._step_workspace(attention=False)
+        L = N.lib()
+        dev = self.hidden.device
         N.check(
             L.btl_decode_step(B, H, F, c.qkv_dim, nl, float(self.eps), N.ptr(self.attn_out), N.ptr(self.hidden),
                               N.ptr(self.qkv_out), N.ptr(self.ffn_h), N.ptr(ws), ws.numel(), N.stream_of(dev)),
             "btl_decode_step",
+        )
+        return self.hidden
+
+    def step_persistent_full(self):
+        """The whole decode step, attention included, as one
+        btl_decode_step_full launch: per layer QKV, the decode attention (RoPE,
+        KV-cache update at ``pos``, SDPA over the cached context), o_proj,
+        gate||up and down (generator_batch32.py:713-761).  Needs
+        alloc_attention(); bit-identical to step_full.  The first call on a
+        stream (and the first after the caches move) prepares the workspace
+        synchronously, so it must happen before a graph capture."""
+        c = self.config
+        B = self.batch
+        H, F = c.hidden_size, c.intermediate_size
+        nl = len(self.layers)
+        for t, name in ((self.hidden, "hidden"), (self.attn_out, "attn_out"), (self.qkv_out, "qkv_out"),
+                        (self.ffn_h, "ffn_h")):
+            N.require_cuda(t, name)
+        ws = self._step_workspace(attention=True)
+        att = self.attention
+        L = N.lib()
+        dev = self.hidden.device
+        N.check(
+            L.btl_decode_step_full(B, H, F, c.qkv_dim, nl, float(self.eps), att.num_kv_heads, att.max_seq_len,
+                                   N.ptr(self.pos), N.ptr(att.rope_cos), N.ptr(att.rope_sin),
+                                   int(att.use_fused_rope), float(att.scale), N.ptr(self.hidden),
+                                   N.ptr(self.qkv_out), N.ptr(self.attn_out), N.ptr(self.ffn_h), N.ptr(ws),
+                                   ws.numel(), N.stream_of(dev)),
+            "btl_decode_step_full",
         )
         return self.hidden
 

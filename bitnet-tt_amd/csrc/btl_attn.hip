@@ -57,7 +57,7 @@ __global__ __launch_bounds__(64 * kAtWaves, 1) void k_decode_attention(AttnArgs 
   a.adjacent = p.adjacent;
   if (!a.pos_ok() && tid == 0 && a.hk == 0) st_coherent(p.error, 1);
   AttnRound r;
-  if (att_wave_work(a)) att_load_round(a, 0, r);
+  att_load_round(a, 0, r);
   BTL_TRACE_AT(1);
   // the new token's rows of the group: q rows hk G .. hk G + G - 1, k row hk, v row hk
   const uint16_t* qrow = p.qkv + (int64_t)a.b * p.ldq;

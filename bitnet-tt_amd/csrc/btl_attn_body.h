@@ -26,6 +26,7 @@
 
 #include "btl_act_row.h"
 #include "btl_common.h"
+#include "btl_trace.h"
 
 namespace btl {
 
@@ -96,34 +97,47 @@ __device__ __forceinline__ float wexp(float m, float M) { return m == -__builtin
 struct AttnRound {
   uint4 kr[4][kAtD / 32];
   uint4 vr[16];
+  float rc, rs;  // this thread's RoPE factors at the position (loaded with the first round)
 };
+
+// Buffer loads: the pair's rows [S][D] of a cache as one resource, so every
+// load takes a 32-bit lane offset and an immediate (the k-steps and the value
+// row groups), not a 64-bit address per load.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t att_rows(const uint16_t* c, const AttnPair& a) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(c + a.kv_base() * kAtD), (short)0,
+                                           a.S * kAtD * 2, 0x00020000);
+}
+__device__ __forceinline__ uint4 att_ld(__amdgpu_buffer_rsrc_t r, int voff, int imm) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + imm, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
 
 __device__ __forceinline__ void att_load_round(const AttnPair& a, int rd, AttnRound& r) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (rd == 0) {  // the RoPE factors of frequency tid & 63 at the position, with the first round
+    const int i = threadIdx.x & (kAtD / 2 - 1), pc = a.pos_ok() ? a.pos : 0;
+    r.rc = a.rcos[pc * (kAtD / 2) + i];
+    r.rs = a.rsin[pc * (kAtD / 2) + i];
+  }
   const int r16 = lane & 15, grp = lane >> 4;
   const int base = rd * kAtRound + kAtPosWave * wv;
-  const int64_t kvb = a.kv_base();
+  const __amdgpu_buffer_rsrc_t kc = att_rows(a.kc, a), vc = att_rows(a.vc, a);
 #pragma unroll
   for (int blk = 0; blk < 4; ++blk) {
     const int row = min(base + 16 * blk + r16, a.S - 1);
-    const uint16_t* kp = a.kc + (kvb + row) * kAtD + 8 * grp;
+    const int off = (row * kAtD + 8 * grp) * 2;
 #pragma unroll
-    for (int ks = 0; ks < kAtD / 32; ++ks) r.kr[blk][ks] = *reinterpret_cast<const uint4*>(kp + 32 * ks);
+    for (int ks = 0; ks < kAtD / 32; ++ks) r.kr[blk][ks] = att_ld(kc, off, 64 * ks);
   }
 #pragma unroll
   for (int t = 0; t < 16; ++t) {
     const int row = min(base + 4 * t + grp, a.S - 1);
-    r.vr[t] = *reinterpret_cast<const uint4*>(a.vc + (kvb + row) * kAtD + 8 * r16);
+    r.vr[t] = att_ld(vc, (row * kAtD + 8 * r16) * 2, 0);
   }
 }
 
-// Whether this wave has cached positions in round 0 (then the caller issues
-// att_load_round(a, 0, r) before att_body).
-__device__ __forceinline__ bool att_wave_work(const AttnPair& a) {
-  return kAtPosWave * (int)(threadIdx.x >> 6) < a.nold();
-}
-
-// Everything after the first round's loads: RoPE of the group's query rows
+// Everything after the first round's loads (att_load_round(a, 0, r), issued
+// by the caller in every wave): RoPE of the group's query rows
 // and the new k row (the new rows go to LDS and to the caches), scores,
 // online softmax, probability-weighted values, merge.  s.in holds the new
 // token's rows (q rows 0..G-1, k at kAtMaxG, v at kAtMaxG + 1) and every
@@ -145,7 +159,7 @@ __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, Att
   {
     const int i = tid & (half - 1);
     const int d0 = a.adjacent ? 2 * i : i, d1 = a.adjacent ? 2 * i + 1 : i + half;
-    const float rc = a.rcos[pc * half + i], rs = a.rsin[pc * half + i];
+    const float rc = r.rc, rs = r.rs;
     const int u = tid / half;  // 0..7: query rows 0..3, then the k row, then v
     if (u < kAtMaxG) {
       float y0 = 0.0f, y1 = 0.0f;
@@ -170,7 +184,8 @@ __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, Att
       if (pos_ok) *reinterpret_cast<uint32_t*>(a.vc + (kvb + a.pos) * kAtD + d) = vnew;
     }
   }
-  __syncthreads();
+  lds_barrier();  // the rotated rows are in LDS (the cache-row stores need no acknowledgement)
+  BTL_TRACE_AT(3);
   if (wv < G) {  // score of the new position for head wv (lanes over D, fixed-order sum)
     const float d = bf2f(s.q[wv][2 * lane]) * bf2f(s.nw[0][2 * lane]) +
                     bf2f(s.q[wv][2 * lane + 1]) * bf2f(s.nw[0][2 * lane + 1]);
@@ -245,6 +260,7 @@ __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, Att
 #pragma unroll
       for (int m = 0; m < kAtD / 16; ++m) o[m][g] *= alpha;
     }
+    if (rd == 0) BTL_TRACE_AT(4);
     // probability-weighted values: 2 k-steps of 32 positions x 8 column
     // blocks of 16 dimensions, probabilities as hi + lo parts; each k-step's
     // 32 value rows staged in LDS just before it (rows past the context as
@@ -293,7 +309,8 @@ __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, Att
       s.ml[wv][g][1] = lrun[g];
     }
   }
-  __syncthreads();  // every wave is done with its value rows: the output partials reuse them
+  BTL_TRACE_AT(6);
+  lds_barrier();  // every wave is done with its value rows: the output partials reuse them
   float(*s_o)[kAtMaxG][kAtD] = reinterpret_cast<float(*)[kAtMaxG][kAtD]>(&s.v[0][0][0]);
   if (lane < 16) {
 #pragma unroll
@@ -301,7 +318,8 @@ __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, Att
 #pragma unroll
       for (int g = 0; g < kAtMaxG; ++g) s_o[wv][g][16 * m + lane] = o[m][g];
   }
-  __syncthreads();
+  lds_barrier();
+  BTL_TRACE_AT(7);
   uint16_t res = 0;
   {
     const int g = tid / kAtD, d = tid % kAtD;  // 512 threads: 4 heads x 128 dims

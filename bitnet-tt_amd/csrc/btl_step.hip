@@ -51,6 +51,7 @@
 #include <algorithm>
 
 #include "btl_act_row.h"
+#include "btl_attn_body.h"
 #include "btl_mfma.h"
 #include "btl_trace.h"
 
@@ -103,7 +104,11 @@ struct StepOp {
   int pad[3];
 };
 static_assert(sizeof(StepOp) == 64, "op table entry");
-constexpr int64_t kStHeader = kStTable + (int64_t)kStepMaxLayers * kStepOps * sizeof(StepOp);
+// The KV caches of each layer (device addresses: key cache, value cache),
+// for the instances that run the decode attention between QKV and o_proj
+// (copied in by btl_decode_step_attention_prepare).
+constexpr int64_t kStAttn = kStTable + (int64_t)kStepMaxLayers * kStepOps * sizeof(StepOp);
+constexpr int64_t kStHeader = kStAttn + (int64_t)kStepMaxLayers * 16;
 
 // GEMM unit shapes.  gate||up units cover all 32 rows (v_mfma_i32_32x32x32_i8:
 // each unpacked weight dword feeds one MFMA) with a gate tile and its up
@@ -145,6 +150,18 @@ struct StepArgs {
   char* layers;          // the hand-off region
   int64_t off_xa[kStepOps], off_flag, off_out[kStepOps];
   unsigned spin_limit;
+  // Decode attention between QKV and o_proj (the ATT instances): per layer
+  // the caches [M][Hkv][S][128] (kv: [L][2] in the workspace), each user's
+  // position, the RoPE tables [S][64], the score scale; the attention output
+  // goes to the rows as tagged words (off_att) and to the caller (attn_out).
+  const uint64_t* kv;
+  const int32_t* pos;
+  const float* rcos;
+  const float* rsin;
+  uint16_t* attn_out;
+  int64_t off_att;
+  int Hkv, G, S, adjacent;
+  float scale;
 };
 
 // Operand-tile byte between two uses: -128, which absmax quantisation never
@@ -177,6 +194,10 @@ __device__ __forceinline__ uint64_t* flag_of(const StepArgs& p, int l, int j, in
 __device__ __forceinline__ uint64_t* out_of(const StepArgs& p, int l, int j) {
   return reinterpret_cast<uint64_t*>(layer_base(p, l) + p.off_out[j]);
 }
+// Tagged words of the attention output (ATT instances): bf16 pairs [32][H / 2].
+__device__ __forceinline__ uint64_t* att_of(const StepArgs& p) {
+  return reinterpret_cast<uint64_t*>(p.layers + p.off_att);
+}
 
 // Loads of an operand tile.  Every layer reuses the tile's addresses, and a
 // CU's L1 may still hold lines it read one layer earlier, so the loads are
@@ -205,8 +226,9 @@ struct WaitState {
   bool reread;  // take the operand re-read path every time (set by a test through the workspace)
 };
 // The error word names the first wait that ran out: kind (1 row words, 2 row
-// flags, 3 operand tile) | (layer*4 + BitLinear) << 8 | workgroup << 16.
-enum { WAIT_WORDS = 1, WAIT_FLAGS = 2, WAIT_TILE = 3 };
+// flags, 3 operand tile, 4 an attention unit's QKV words; 5: a user's
+// position outside [0, S)) | (layer*4 + BitLinear) << 8 | workgroup << 16.
+enum { WAIT_WORDS = 1, WAIT_FLAGS = 2, WAIT_TILE = 3, WAIT_ATT_WORDS = 4, BAD_POSITION = 5 };
 __device__ __forceinline__ void set_error_word(const StepArgs& p, int kind, uint32_t want) {
   uint32_t expected = 0u;
   const uint32_t code = (uint32_t)kind | ((want & 0xffu) << 8) | (blockIdx.x << 16);
@@ -426,7 +448,7 @@ __device__ __forceinline__ void residual_add(uint32_t (&hid)[4], const uint32_t 
 // words of the previous BitLinear, then for every earlier memory operation of
 // this thread (the last tile clear among them), publish, then clear the
 // previous BitLinear's tile slice, whose readers are all done.
-template <int CF>
+template <int CF, bool ATT>
 __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t E, float* s_sum, float* s_max,
                          int* s_rs) {
   constexpr int CH = 1;
@@ -457,21 +479,40 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       STEP_TRACE(l, 1);
       if (l > 0) clear_tile_share<CF>(tile_of(p, l - 1, S_DN), m, p.KSF);
     }
-    // ---- O: the user's QKV row, then RMSNorm(attn; attn_sub_norm)
+    // ---- O: RMSNorm(attn; attn_sub_norm) of the user's attention output row
     {
       float g[CH][8];
       load_gain<CH>(ops[S_O].gamma, nh, g);
-      // the attention output row: an input of the step, loaded before the wait
-      uint4 raw = make_uint4(0u, 0u, 0u, 0u);
-      if (live && tid < nh) raw = *reinterpret_cast<const uint4*>(p.attn + (int64_t)m * p.H + 8 * tid);
       uint32_t pr[CH][4];
-      wait_row_words<CH>(p, out_of(p, l, S_QKV) + (int64_t)m * (p.NQKV >> 1), p.NQKV, step_tag(E, l, S_QKV), pr, ws);
-      wait_memory();
-      STEP_TRACE(l, 2);
-      pr[0][0] = raw.x;
-      pr[0][1] = raw.y;
-      pr[0][2] = raw.z;
-      pr[0][3] = raw.w;
+      if (ATT) {
+        // the row from the attention units of this user's key-value heads,
+        // which read all of the user's QKV row first.  A row past the batch
+        // has no attention units: it waits for its QKV row itself (the tile
+        // clear below needs every QKV unit of its half done) and takes zeros.
+        if (live) {
+          wait_row_words<CH>(p, att_of(p) + (int64_t)m * (p.H >> 1), p.H, step_tag(E, l, 0), pr, ws);
+        } else {
+          wait_row_words<CH>(p, out_of(p, l, S_QKV) + (int64_t)m * (p.NQKV >> 1), p.NQKV, step_tag(E, l, S_QKV), pr,
+                             ws);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) pr[0][k] = 0u;
+        }
+        wait_memory();
+        STEP_TRACE(l, 2);
+      } else {
+        // the attention output stand-in (an input of the step, loaded before
+        // the wait) once the user's QKV row, which attention would read, is in
+        uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+        if (live && tid < nh) raw = *reinterpret_cast<const uint4*>(p.attn + (int64_t)m * p.H + 8 * tid);
+        wait_row_words<CH>(p, out_of(p, l, S_QKV) + (int64_t)m * (p.NQKV >> 1), p.NQKV, step_tag(E, l, S_QKV), pr,
+                           ws);
+        wait_memory();
+        STEP_TRACE(l, 2);
+        pr[0][0] = raw.x;
+        pr[0][1] = raw.y;
+        pr[0][2] = raw.z;
+        pr[0][3] = raw.w;
+      }
       float v[CH][8];
       pairs_to_floats<CH>(pr, v);
       publish_row<CH>(p, l, S_O, m, p.H, p.KSH, v, g, step_tag(E, l, S_O), s_sum, s_max, s_rs);
@@ -580,17 +621,22 @@ __device__ __forceinline__ void wave_ks(int sb0, int sb1, int wv, int& wb, int& 
 
 // Weights of this wave's superblocks of unit u of BitLinear J into w
 // (slot t * NSW + i); slots past the wave's range re-read its last superblock.
+// Every slot the BitLinear reads is written (zeros where the unit or wave has
+// no work), so the buffer's previous contents are dead from here on and its
+// registers free in between (the decode attention runs there).
 template <int J, int NSW>
 __device__ __forceinline__ void load_unit_weights(const StepArgs& p, const StepOp* sops, int l, int u,
                                                   v4i (&w)[kStepWSlots]) {
   static_assert(OpShape<J>::TPW * NSW <= kStepWSlots, "weight slots");
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (u >= op_units<J>(p)) return;
   const int KS = op_ks(p, J);
-  int tile0, h, wb, we;
-  unit_of<J>(p, u, tile0, h);
-  wave_ks(0, KS, wv, wb, we);
-  if (wb >= we) return;
+  int tile0 = 0, h = 0, wb = 0, we = 0;
+  const bool unit = u < op_units<J>(p);
+  if (unit) {
+    unit_of<J>(p, u, tile0, h);
+    wave_ks(0, KS, wv, wb, we);
+  }
+  const bool work = unit && wb < we;
   const uint32_t* wdev = sops[l * kStepOps + J].wdev;
 #pragma unroll
   for (int t = 0; t < OpShape<J>::TPW; ++t) {
@@ -598,7 +644,7 @@ __device__ __forceinline__ void load_unit_weights(const StepArgs& p, const StepO
 #pragma unroll
     for (int i = 0; i < NSW; ++i) {
       const int sb = wb + i < we ? wb + i : we - 1;
-      w[t * NSW + i] = ldg128(wdev + (((int64_t)tile * KS + sb) * 64 + lane) * 4);
+      w[t * NSW + i] = work ? ldg128(wdev + (((int64_t)tile * KS + sb) * 64 + lane) * 4) : (v4i){0, 0, 0, 0};
     }
   }
 }
@@ -892,8 +938,73 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
   if (nl < p.L) load_unit_weights<NJ, NNSW>(p, sops, nl, gi, wn);
 }
 
+// ------------------------------------------------------------ attention ----
+// Decode attention of user b = gi / Hkv and key-value head hk = gi % Hkv (ATT
+// instances; src/bitnet_tt/inference/generator_batch32.py:728-746), run by
+// GEMM workgroup gi between its QKV and o_proj units.  The first round of the
+// pair's cached keys and values does not depend on this step, so its loads
+// are issued first; then the new token's rows (the group's G query heads, its
+// key and value head) come in as row b's tagged QKV output words, and the
+// body shared with btl_decode_attention runs on the workgroup (the same code,
+// so the same bits).  Its G x 128 outputs leave as tagged bf16 pairs, which
+// row b's workgroup polls for its o_proj stage, and as the caller's copy.
+__device__ void step_attention(const StepArgs& p, int l, int gi, uint32_t E, int32_t* lds, WaitState& ws) {
+  if (gi >= p.M * p.Hkv) return;
+  const int tid = threadIdx.x;
+  AttnSmem& s = *reinterpret_cast<AttnSmem*>(lds);
+  AttnPair a;
+  a.rcos = p.rcos;
+  a.rsin = p.rsin;
+  a.kc = reinterpret_cast<uint16_t*>(p.kv[2 * l]);
+  a.vc = reinterpret_cast<uint16_t*>(p.kv[2 * l + 1]);
+  a.Hkv = p.Hkv;
+  a.G = p.G;
+  a.S = p.S;
+  a.b = gi / p.Hkv;
+  a.hk = gi % p.Hkv;
+  a.pos = p.pos[a.b];
+  a.scale = p.scale;
+  a.adjacent = p.adjacent;
+  if (!a.pos_ok() && tid == 0) set_error_word(p, BAD_POSITION, (uint32_t)(l * 4 + S_O));
+  AttnRound r;
+  att_load_round(a, 0, r);
+  STEP_TRACE(l, 4);
+  // the new rows: thread t < 6 x 64 takes word t % 64 (two values) of row
+  // segment t / 64 (query rows 0..G-1, the key row at kAtMaxG, the value row
+  // at kAtMaxG + 1)
+  const uint32_t want = step_tag(E, l, S_QKV);
+  const uint64_t* row = out_of(p, l, S_QKV) + (int64_t)a.b * (p.NQKV >> 1);
+  const int Hq = p.G * p.Hkv;
+  if (tid < (kAtMaxG + 2) * (kAtD / 2)) {
+    const int u = tid / (kAtD / 2), w = tid % (kAtD / 2);
+    if (u >= kAtMaxG || u < p.G) {
+      const int head = u < kAtMaxG ? a.hk * p.G + u : u == kAtMaxG ? Hq + a.hk : Hq + p.Hkv + a.hk;
+      const uint64_t* wp = row + head * (kAtD / 2) + w;
+      unsigned n = 0;
+      uint64_t v = 0;
+      while (!ws.dead) {
+        v = ld_coherent(wp);
+        if ((uint32_t)(v >> 32) == want) break;
+        if (should_stop(p, ++n, ws, WAIT_ATT_WORDS, want)) break;
+        __builtin_amdgcn_s_sleep(BTL_STEP_POLL_SLEEP);
+      }
+      *reinterpret_cast<uint32_t*>(&s.in[u][2 * w]) = (uint32_t)v;
+    }
+  }
+  lds_barrier();  // the new rows are in LDS (the cache loads stay in flight)
+  const uint32_t o = att_body(a, s, r);
+  const uint32_t pair = o | (xor_partner_u<1>(o) << 16);  // dims d, d + 1 of a head (a DPP lane swap)
+  if (tid < p.G * kAtD && (tid & 1) == 0) {
+    const int col = a.hk * p.G * kAtD + tid;  // heads hk G + tid / 128, dimension tid % 128
+    st_coherent(att_of(p) + (int64_t)a.b * (p.H >> 1) + (col >> 1), ((uint64_t)step_tag(E, l, 0) << 32) | pair);
+    *reinterpret_cast<uint32_t*>(p.attn_out + (int64_t)a.b * p.H + col) = pair;
+  }
+  STEP_TRACE(l, 5);
+  lds_barrier();  // the LDS is the next BitLinear's again
+}
+
 // NQ: superblocks per wave of a unit of QKV, O and GU (K = H); NDN: of DN (K = F).
-template <int NQ, int NDN>
+template <int NQ, int NDN, bool ATT>
 __device__ void step_gemm(const StepArgs& p, const StepOp* sops, int gi, uint32_t E, int32_t* lds) {
   // Word kStError + 64 of the workspace: bit 0 makes every GEMM unit take the
   // re-read path of its sentinel check (a test of that rare path; the results
@@ -902,14 +1013,22 @@ __device__ void step_gemm(const StepArgs& p, const StepOp* sops, int gi, uint32_
   v4i wa[kStepWSlots], wb[kStepWSlots];
   load_unit_weights<S_QKV, NQ>(p, sops, 0, gi, wa);
   for (int l = 0; l < p.L; ++l) {
-    step_gemm_op<S_QKV, NQ, S_O, NQ>(p, sops, l, gi, E, wa, wb, l, lds, ws);
+    // An attention unit loads its o_proj weights after the attention (whose
+    // key and value rows take the registers meanwhile): o_proj's operands
+    // arrive microseconds later, through the rows' o_proj stage.
+    const bool att_unit = ATT && gi < p.M * p.Hkv;
+    step_gemm_op<S_QKV, NQ, S_O, NQ>(p, sops, l, gi, E, wa, wb, att_unit ? p.L : l, lds, ws);
+    if (att_unit) {
+      step_attention(p, l, gi, E, lds, ws);
+      load_unit_weights<S_O, NQ>(p, sops, l, gi, wb);
+    }
     step_gemm_op<S_O, NQ, S_GU, NQ>(p, sops, l, gi, E, wb, wa, l, lds, ws);
     step_gemm_op<S_GU, NQ, S_DN, NDN>(p, sops, l, gi, E, wa, wb, l, lds, ws);
     step_gemm_op<S_DN, NDN, S_QKV, NQ>(p, sops, l, gi, E, wb, wa, l + 1, lds, ws);
   }
 }
 
-template <int CF, int NQ, int NDN>
+template <int CF, int NQ, int NDN, bool ATT>
 __global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
   // GEMM: reductions [8][2][16][64] int32 + 32 row sums; rows: 24 words.  The op table
   // (up to 16 KiB) is copied into LDS above them, so reading a weight address or a
@@ -919,6 +1038,7 @@ __global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
   __shared__ __attribute__((aligned(16))) int32_t lds[24576];
   constexpr int kTableInts = kStepMaxLayers * kStepOps * (int)sizeof(StepOp) / 4;
   static_assert(kStepWaves * 2 * 16 * 64 + 64 + kTableInts <= 24576, "LDS layout");
+  static_assert(sizeof(AttnSmem) <= (24576 - kTableInts) * 4, "the attention body's LDS below the op table");
   StepOp* sops = reinterpret_cast<StepOp*>(lds + (24576 - kTableInts));
   {
     const uint4* src = reinterpret_cast<const uint4*>(p.ops);
@@ -931,9 +1051,9 @@ __global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
   const uint32_t E = p.epoch[b] + 1u;  // this launch (written by the previous launch of the step)
   if (b < kStepRows) {
     float* f = reinterpret_cast<float*>(lds);
-    step_row<CF>(p, sops, b, E, f, f + kActWaves, reinterpret_cast<int*>(lds) + 2 * kActWaves);
+    step_row<CF, ATT>(p, sops, b, E, f, f + kActWaves, reinterpret_cast<int*>(lds) + 2 * kActWaves);
   } else {
-    step_gemm<NQ, NDN>(p, sops, b - kStepRows, E, lds);
+    step_gemm<NQ, NDN, ATT>(p, sops, b - kStepRows, E, lds);
   }
   if (threadIdx.x == 0) p.epoch[b] = E;
 }
@@ -1023,7 +1143,7 @@ __global__ __launch_bounds__(512) void k_decode_step_floor(StepArgs p) {
 
 // ---------------------------------------------------------------- host ----
 struct StepSizes {
-  int64_t off_xa[kStepOps], tiles_end, off_flag, off_out[kStepOps], layer_bytes, total;
+  int64_t off_xa[kStepOps], tiles_end, off_flag, off_out[kStepOps], off_att, layer_bytes, total;
 };
 
 static StepSizes step_sizes(int64_t H, int64_t F, int64_t NQKV) {
@@ -1043,6 +1163,8 @@ static StepSizes step_sizes(int64_t H, int64_t F, int64_t NQKV) {
     z.off_out[j] = off;
     off += round_up(32 * words[j] * 8, 4096);
   }
+  z.off_att = off;  // the attention output's tagged words (ATT instances)
+  off += round_up(32 * (H / 2) * 8, 4096);
   z.layer_bytes = round_up(off, 65536);
   z.total = kStHeader + z.layer_bytes;
   return z;
@@ -1055,14 +1177,19 @@ static int step_grid() {
   return cus;
 }
 
-// The step's instance for F (the down projection's row chunks per thread).
-static const void* step_kernel(int64_t F, bool floor) {
+// The step's instance for F (the down projection's row chunks per thread),
+// with or without the decode attention.
+static void (*step_kernel_fn(int64_t F, bool att))(StepArgs) {
+  const int cf = act_cpt(F);
+  if (cf == 1) return att ? k_decode_step<1, 3, 7, true> : k_decode_step<1, 3, 7, false>;
+  if (cf == 2) return att ? k_decode_step<2, 3, 7, true> : k_decode_step<2, 3, 7, false>;
+  return nullptr;
+}
+static const void* step_kernel(int64_t F, bool floor, bool att = false) {
   const int cf = act_cpt(F);
   if (floor) return cf == 1 ? reinterpret_cast<const void*>(k_decode_step_floor<1>)
                             : reinterpret_cast<const void*>(k_decode_step_floor<2>);
-  if (cf == 1) return reinterpret_cast<const void*>(k_decode_step<1, 3, 7>);
-  if (cf == 2) return reinterpret_cast<const void*>(k_decode_step<2, 3, 7>);
-  return nullptr;
+  return reinterpret_cast<const void*>(step_kernel_fn(F, att));
 }
 
 static int step_check_shape(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L) {
@@ -1086,6 +1213,43 @@ static int step_check_shape(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64
     return set_error(BTL_ERR_SHAPE, "btl_decode_step: %lld GEMM units do not fit %d workgroups", (long long)units,
                      grid - kStepRows);
   return BTL_OK;
+}
+
+static StepArgs step_args(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, float eps, uint16_t* hidden,
+                          uint16_t* qkv_out, uint16_t* ffn_h, char* ws, const StepSizes& z) {
+  StepArgs a = {};
+  a.ops = reinterpret_cast<const StepOp*>(ws + kStTable);
+  a.L = (int)L;
+  a.M = (int)M;
+  a.H = (int)H;
+  a.F = (int)F;
+  a.NQKV = (int)NQKV;
+  a.KSH = (int)ksb(H);
+  a.KSF = (int)ksb(F);
+  a.eps = eps;
+  a.hidden = hidden;
+  a.qkv_out = qkv_out;
+  a.ffn_h = ffn_h;
+  a.epoch = reinterpret_cast<uint32_t*>(ws + kStEpoch);
+  a.error = reinterpret_cast<uint32_t*>(ws + kStError);
+  a.layers = ws + kStHeader;
+  for (int j = 0; j < kStepOps; ++j) {
+    a.off_xa[j] = z.off_xa[j];
+    a.off_out[j] = z.off_out[j];
+  }
+  a.off_flag = z.off_flag;
+  a.spin_limit = 1u << 18;
+  return a;
+}
+
+static int launch_step(const StepArgs& a, int64_t F, bool att, const char* who, hipStream_t s) {
+  void (*k)(StepArgs) = step_kernel_fn(F, att);
+  if (!k) return set_error(BTL_ERR_SHAPE, "%s: no kernel instance for F=%lld", who, (long long)F);
+  const int grid = step_grid();
+  const int rc = check_coresident_launch(who, reinterpret_cast<const void*>(k), 512, grid, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(512), 0, s, a);
+  return check_launch(who);
 }
 
 }  // namespace btl
@@ -1189,42 +1353,82 @@ int btl_decode_step(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, fl
   if ((int64_t)workspace_bytes < z.total)
     return set_error(BTL_ERR_WORKSPACE, "btl_decode_step: workspace %zu < %lld bytes", workspace_bytes,
                      (long long)z.total);
-  char* ws = (char*)workspace;
-  StepArgs a = {};
-  a.ops = reinterpret_cast<const StepOp*>(ws + kStTable);
-  a.L = (int)L;
-  a.M = (int)M;
-  a.H = (int)H;
-  a.F = (int)F;
-  a.NQKV = (int)NQKV;
-  a.KSH = (int)ksb(H);
-  a.KSF = (int)ksb(F);
-  a.eps = eps;
+  StepArgs a = step_args(M, H, F, NQKV, L, eps, hidden, qkv_out, ffn_h, (char*)workspace, z);
   a.attn = attn;
-  a.hidden = hidden;
-  a.qkv_out = qkv_out;
-  a.ffn_h = ffn_h;
-  a.epoch = reinterpret_cast<uint32_t*>(ws + kStEpoch);
-  a.error = reinterpret_cast<uint32_t*>(ws + kStError);
-  a.layers = ws + kStHeader;
-  for (int j = 0; j < kStepOps; ++j) {
-    a.off_xa[j] = z.off_xa[j];
-    a.off_out[j] = z.off_out[j];
-  }
-  a.off_flag = z.off_flag;
-  a.spin_limit = 1u << 18;
-  const int grid = step_grid();
-  const int cf = act_cpt(F);
-  hipStream_t s = (hipStream_t)stream;
-  rc = check_coresident_launch("btl_decode_step", step_kernel(F, false), 512, grid, s);
+  return launch_step(a, F, false, "btl_decode_step", (hipStream_t)stream);
+}
+
+int btl_decode_step_attention_prepare(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L,
+                                      const uint16_t* const* k_caches, const uint16_t* const* v_caches,
+                                      void* workspace, size_t workspace_bytes) {
+  clear_error();
+  int rc = step_check_shape(M, H, F, NQKV, L);
   if (rc) return rc;
-  if (cf == 1)
-    hipLaunchKernelGGL((k_decode_step<1, 3, 7>), dim3(grid), dim3(512), 0, s, a);
-  else if (cf == 2)
-    hipLaunchKernelGGL((k_decode_step<2, 3, 7>), dim3(grid), dim3(512), 0, s, a);
-  else
-    return set_error(BTL_ERR_SHAPE, "btl_decode_step: no kernel instance for H=%lld F=%lld", (long long)H, (long long)F);
-  return check_launch("decode step");
+  if (!k_caches || !v_caches || !workspace)
+    return set_error(BTL_ERR_NULL, "btl_decode_step_attention_prepare: null pointer");
+  if (!aligned(workspace, 256))
+    return set_error(BTL_ERR_ALIGN, "btl_decode_step_attention_prepare: workspace must be 256-byte aligned");
+  const StepSizes z = step_sizes(H, F, NQKV);
+  if ((int64_t)workspace_bytes < z.total)
+    return set_error(BTL_ERR_WORKSPACE, "btl_decode_step_attention_prepare: workspace %zu < %lld bytes",
+                     workspace_bytes, (long long)z.total);
+  uint64_t table[2 * kStepMaxLayers];
+  for (int64_t l = 0; l < L; ++l) {
+    if (!k_caches[l] || !v_caches[l])
+      return set_error(BTL_ERR_NULL, "btl_decode_step_attention_prepare: layer %lld cache is NULL", (long long)l);
+    if (!aligned(k_caches[l], 16) || !aligned(v_caches[l], 16))
+      return set_error(BTL_ERR_ALIGN, "btl_decode_step_attention_prepare: layer %lld cache must be 16-byte aligned",
+                       (long long)l);
+    table[2 * l] = reinterpret_cast<uint64_t>(k_caches[l]);
+    table[2 * l + 1] = reinterpret_cast<uint64_t>(v_caches[l]);
+  }
+  if (hipMemcpy((char*)workspace + kStAttn, table, 16 * L, hipMemcpyHostToDevice) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(BTL_ERR_LAUNCH, "btl_decode_step_attention_prepare: copying the cache table failed");
+  }
+  return BTL_OK;
+}
+
+int btl_decode_step_full(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, float eps, int64_t Hkv, int64_t S,
+                         const int32_t* pos, const float* rope_cos, const float* rope_sin, int rope_adjacent,
+                         float scale, uint16_t* hidden, uint16_t* qkv_out, uint16_t* attn_out, uint16_t* ffn_h,
+                         void* workspace, size_t workspace_bytes, btl_stream_t stream) {
+  clear_error();
+  int rc = step_check_shape(M, H, F, NQKV, L);
+  if (rc) return rc;
+  const int64_t Hq = H / kAtD;
+  if (H % kAtD || Hkv <= 0 || Hq % Hkv || Hq / Hkv > kAtMaxG || NQKV != H + 2 * Hkv * kAtD || S <= 0 ||
+      S > (1 << 20))
+    return set_error(BTL_ERR_SHAPE,
+                     "btl_decode_step_full: H=%lld (128-wide heads), Hkv=%lld (at most %d query heads each), "
+                     "NQKV=%lld (must be H + 2 Hkv 128), S=%lld",
+                     (long long)H, (long long)Hkv, kAtMaxG, (long long)NQKV, (long long)S);
+  if (M * Hkv > step_grid() - kStepRows)
+    return set_error(BTL_ERR_SHAPE, "btl_decode_step_full: %lld attention units do not fit %d workgroups",
+                     (long long)(M * Hkv), step_grid() - kStepRows);
+  if (!pos || !rope_cos || !rope_sin || !hidden || !qkv_out || !attn_out || !ffn_h || !workspace)
+    return set_error(BTL_ERR_NULL, "btl_decode_step_full: null pointer");
+  if (!aligned(hidden, 16) || !aligned(workspace, 256) || !aligned(qkv_out, 4) || !aligned(ffn_h, 4) ||
+      !aligned(attn_out, 4) || !aligned(pos, 4) || !aligned(rope_cos, 4) || !aligned(rope_sin, 4))
+    return set_error(BTL_ERR_ALIGN, "btl_decode_step_full: hidden must be 16-byte aligned, the other buffers 4, "
+                     "workspace 256");
+  const StepSizes z = step_sizes(H, F, NQKV);
+  if ((int64_t)workspace_bytes < z.total)
+    return set_error(BTL_ERR_WORKSPACE, "btl_decode_step_full: workspace %zu < %lld bytes", workspace_bytes,
+                     (long long)z.total);
+  StepArgs a = step_args(M, H, F, NQKV, L, eps, hidden, qkv_out, ffn_h, (char*)workspace, z);
+  a.kv = reinterpret_cast<const uint64_t*>((char*)workspace + kStAttn);
+  a.pos = pos;
+  a.rcos = rope_cos;
+  a.rsin = rope_sin;
+  a.attn_out = attn_out;
+  a.off_att = z.off_att;
+  a.Hkv = (int)Hkv;
+  a.G = (int)(Hq / Hkv);
+  a.S = (int)S;
+  a.adjacent = rope_adjacent ? 1 : 0;
+  a.scale = scale;
+  return launch_step(a, F, true, "btl_decode_step_full", (hipStream_t)stream);
 }
 
 int btl_decode_step_floor(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, void* workspace,

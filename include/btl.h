@@ -272,7 +272,10 @@ typedef struct {
  * waits on the others: nothing else may hold the GPU's CUs during the launch
  * (a wait that runs out sets the word at btl_decode_step_error_offset and the
  * outputs are invalid; the workspace must then be zero-filled and prepared
- * again before the next btl_decode_step). */
+ * again before the next btl_decode_step).  The error word names the first
+ * failure: bits 0-7 the kind (1 row words, 2 row flags, 3 operand tile, 4 an
+ * attention unit's QKV words, 5 a position outside the cache), bits 8-15
+ * layer x 4 + BitLinear, bits 16-31 the workgroup. */
 int64_t btl_decode_step_workspace_bytes(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L);
 int64_t btl_decode_step_error_offset(void);
 int btl_decode_step_prepare(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L,
@@ -280,6 +283,33 @@ int btl_decode_step_prepare(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64
 int btl_decode_step(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, float eps, const uint16_t* attn,
                     uint16_t* hidden, uint16_t* qkv_out, uint16_t* ffn_h, void* workspace, size_t workspace_bytes,
                     btl_stream_t stream);
+
+/* The whole decode step, attention included, as one launch: per layer
+ * QKV -> decode attention -> o_proj -> gate||up -> down, as
+ * src/bitnet_tt/inference/generator_batch32.py:713-761 runs it (attention
+ * :728-746, the body of src/bitnet_tt/layers/attention.py:1040-1262).  The
+ * attention of each (user, key-value head) runs on one GEMM workgroup between
+ * its QKV and o_proj units, with the same code as btl_decode_attention (the
+ * same bits); the rows' o_proj stage reads its output.  Same shapes as
+ * btl_decode_step with the attention width H = Hq x 128 (Hq query heads of
+ * 128, Hq / Hkv <= 4 per key-value head, NQKV = H + 2 Hkv 128) and M x Hkv
+ * attention units within the GEMM workgroups.  The caches are [M][Hkv][S][128]
+ * bf16 per layer, their addresses copied into the workspace by
+ * btl_decode_step_attention_prepare (synchronously: not under graph capture;
+ * again whenever they move); pos [M] int32 (device), the RoPE tables
+ * [S][64] fp32 (rope_adjacent: pairs (2i, 2i+1), else (i, i+64)) and the score
+ * scale as for btl_decode_attention.  Writes hidden (in/out), the last
+ * layer's qkv_out [M][NQKV], attn_out [M][H] and ffn_h [M][F], and each
+ * layer's cache row at pos.  A position outside [0, S) sets the error word
+ * (kind 5) and the outputs are invalid.  The workspace is btl_decode_step's,
+ * prepared by btl_decode_step_prepare as well. */
+int btl_decode_step_attention_prepare(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L,
+                                      const uint16_t* const* k_caches, const uint16_t* const* v_caches,
+                                      void* workspace, size_t workspace_bytes);
+int btl_decode_step_full(int64_t M, int64_t H, int64_t F, int64_t NQKV, int64_t L, float eps, int64_t Hkv, int64_t S,
+                         const int32_t* pos, const float* rope_cos, const float* rope_sin, int rope_adjacent,
+                         float scale, uint16_t* hidden, uint16_t* qkv_out, uint16_t* attn_out, uint16_t* ffn_h,
+                         void* workspace, size_t workspace_bytes, btl_stream_t stream);
 
 /* Measurement aid with no counterpart in the reference: btl_decode_step's
  * launch structure with no arithmetic.  The same workgroups, waits and

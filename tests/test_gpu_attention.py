@@ -155,3 +155,94 @@ def test_full_layer_chain(orc):
     h = orc.bitlinear(r["h"], wkn(w.down), list(w.down.segment_scales), gamma_bf16=H.bits_of(w.ffn_sub_norm),
                       norm_eps=step.eps, residual_bf16=h)["out"]
     assert np.array_equal(H.bits_of(step.hidden), h)
+
+
+def _full_state(step):
+    return (step.hidden.clone(), [(kv.key_cache.clone(), kv.value_cache.clone()) for kv in step.kv])
+
+
+def _restore(step, state):
+    hid, caches = state
+    step.hidden.copy_(hid)
+    for kv, (k, v) in zip(step.kv, caches):
+        kv.key_cache.copy_(k)
+        kv.value_cache.copy_(v)
+    torch.cuda.synchronize()
+
+
+def _outputs(step):
+    torch.cuda.synchronize()
+    return {"hidden": H.bits_of(step.hidden).copy(), "qkv": H.bits_of(step.qkv_out).copy(),
+            "attn": H.bits_of(step.attn_out).copy(), "ffn_h": H.bits_of(step.ffn_h).copy(),
+            "k": [H.bits_of(kv.key_cache).copy() for kv in step.kv],
+            "v": [H.bits_of(kv.value_cache).copy() for kv in step.kv]}
+
+
+def _compare(a, b, what):
+    for key in ("hidden", "qkv", "attn", "ffn_h"):
+        bad = int((a[key] != b[key]).sum())
+        assert bad == 0, f"{what}: {key} differs in {bad} of {a[key].size} values"
+    for i, (ka, kb, va, vb) in enumerate(zip(a["k"], b["k"], a["v"], b["v"])):
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb), f"{what}: layer {i} cache differs"
+
+
+@pytest.mark.parametrize("layers,batch,pos", [(2, 8, 200), (3, 5, None)])
+def test_persistent_full_step_matches_step_full_mini(orc, layers, batch, pos):
+    """The one-launch step with the decode attention (btl_decode_step_full)
+    against step_full (QKV, attention and the other BitLinears as separate
+    launches, each pinned to the oracle elsewhere): hidden, the last layer's
+    qkv / attention / FFN rows and every layer's cache, bit for bit; spread
+    positions per user in the second case."""
+    from bitnet_tt.config import BitNetMiniConfig
+    from bitnet_tt.decode import BitLinearDecodeStep
+
+    cfg = BitNetMiniConfig(num_layers=layers, num_attention_heads=4, num_key_value_heads=1, hidden_size=512,
+                           intermediate_size=512)
+    print(f"persistent full step mini layers={layers} batch={batch} pos={pos}", flush=True)
+    step = BitLinearDecodeStep.random_init(cfg, H.dev(), seed=91 + layers, batch=batch).alloc_buffers(seed=92)
+    step.alloc_attention(max_seq_len=256, pos=pos if pos is not None else 0)
+    if pos is None:
+        step.pos.copy_(torch.from_numpy(np.random.default_rng(3).integers(0, 256, batch).astype(np.int32)))
+    state = _full_state(step)
+    step.step_full()
+    step.check()
+    ref = _outputs(step)
+    _restore(step, state)
+    step.step_persistent_full()
+    step.check()
+    _compare(_outputs(step), ref, "persistent full step")
+
+
+def test_persistent_full_step_matches_step_full_2b(orc):
+    """The 2B model (30 layers, 20 query / 5 key-value heads, batch 32, every
+    user at position 511 of a 512 context), the one-launch step with
+    attention against step_full, bit for bit; then three graph replays of the
+    one-launch step from the same state give the same bits again."""
+    from bitnet_tt.config import BitNet2B4TConfig
+    from bitnet_tt.decode import BitLinearDecodeStep
+
+    print("persistent full step 2B", flush=True)
+    step = BitLinearDecodeStep.random_init(BitNet2B4TConfig(), H.dev(), seed=95).alloc_buffers(seed=96)
+    step.alloc_attention(max_seq_len=512)
+    state = _full_state(step)
+    step.step_full()
+    step.check()
+    ref = _outputs(step)
+    _restore(step, state)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step.step_persistent_full()
+    s.synchronize()
+    step.check()
+    _compare(_outputs(step), ref, "persistent full step")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step.step_persistent_full()
+    for rep in range(3):
+        _restore(step, state)
+        g.replay()
+        torch.cuda.synchronize()
+        _ = torch.ones(1024, device=H.dev()).sum().item()  # eager work between replays
+        _compare(_outputs(step), ref, f"graph replay {rep}")
+    step.check()
