@@ -10,16 +10,19 @@
 // its key and value loads (256 B per lane each) before computing, so a round
 // is one memory round trip (at context 512 the whole context is one round,
 // and the caller may issue it before the new token's q, k, v exist).
-//  - Scores: v_mfma_f32_16x16x32_bf16, the G rotated query rows (padded to
-//    16 with zeros) against 16 cached key rows per MFMA (keys contiguous
-//    along D, the contraction, so the B operands load straight from the
-//    cache).
-//  - Softmax: the running (online) form in fp32 per wave and head.
+//  - Scores: v_mfma_f32_16x16x32_bf16, the G rotated query rows (head g at
+//    row 4 g, the other rows zero) against 16 cached key rows per MFMA (keys
+//    contiguous along D, the contraction, so the B operands load straight
+//    from the cache).  Row 4 g of the result lies in lane group g, so lane
+//    16 g + j holds head g's score of position j of the block.
+//  - Softmax: the running (online) form in fp32 per wave and head, every
+//    head in its own lane group (one butterfly over 16 lanes serves all
+//    heads).
 //  - Probability-weighted values: MFMA as well.  The wave's value rows go
-//    to LDS 32 at a time (rows padded by 8 bytes, so the four position
-//    groups of an operand read fall in different banks) and are read back as
-//    B operands (8 positions of one dimension per lane); the probabilities
-//    enter as two bf16 parts, p = hi + lo, which keeps them to ~16 bits.
+//    to LDS 32 at a time (rows padded by 8 bytes) and come back as B operands
+//    (8 positions of one dimension per lane) through two transposing LDS
+//    reads each; the probabilities enter as two bf16 parts, p = hi + lo,
+//    which keeps them to ~16 bits.
 //  - The waves' (max, sum, output) partials and the new position (rotated k,
 //    v) merge in LDS in a fixed order.
 #pragma once
@@ -74,23 +77,35 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, 
   y1 = x1 * c + x0 * s;
 }
 
-// Max and sum over the 16 lanes of a row (lanes 0..15 hold the values).
+// Max and sum over each group of 16 lanes (an xor butterfly 8, 4, 2, 1:
+// every lane of a group ends with its group's value).
 __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, xor_partner<8>(v));
   v = fmaxf(v, xor_partner<4>(v));
   v = fmaxf(v, xor_partner<2>(v));
   v = fmaxf(v, xor_partner<1>(v));
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  return v;
 }
 __device__ __forceinline__ float row16_sum(float v) {
   v = v + xor_partner<8>(v);
   v = v + xor_partner<4>(v);
   v = v + xor_partner<2>(v);
   v = v + xor_partner<1>(v);
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  return v;
 }
 
 __device__ __forceinline__ float wexp(float m, float M) { return m == -__builtin_inff() ? 0.0f : __expf(m - M); }
+
+// ds_read_b64_tr_b16: in each group of 16 lanes, lane j receives, for
+// r = 0..3, element j % 4 of the four 16-bit values that lane 4 r + j / 4
+// addresses (measured on gfx950).  With lane 4 r + q addressing row r,
+// columns 4 q .. 4 q + 3 of a row-major block, lane j gets column j of rows
+// 0..3: a transposed 4 x 16 read.
+typedef short v4s __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v4s lds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(__attribute__((address_space(3))) void*)p);
+}
 
 // A wave's key and value rows of round rd: K operands (4 blocks of 16
 // positions x 4 k-steps) and value pieces (dims 8 r16 .. + 8 of row 4 t + grp).
@@ -104,8 +119,13 @@ struct AttnRound {
 // load takes a 32-bit lane offset and an immediate (the k-steps and the value
 // row groups), not a 64-bit address per load.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t att_rows(const uint16_t* c, const AttnPair& a) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(c + a.kv_base() * kAtD), (short)0,
-                                           a.S * kAtD * 2, 0x00020000);
+  // the pair's base is the same in every lane: one scalar descriptor, no
+  // per-lane (waterfall) resource loop around each load
+  const uint64_t base = reinterpret_cast<uint64_t>(c + a.kv_base() * kAtD);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
+                                           __builtin_amdgcn_readfirstlane(a.S * kAtD * 2), 0x00020000);
 }
 __device__ __forceinline__ uint4 att_ld(__amdgpu_buffer_rsrc_t r, int voff, int imm) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + imm, 0, 0);
@@ -192,24 +212,22 @@ __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, Att
     const float sn = wave_xor_sum(d) * a.scale;
     if (lane == 0) s.snew[wv] = sn;
   }
-  // query operands (A: row r16 = head, k-step ks: dims 32 ks + 8 grp ..)
+  // query operands (A: row 4 g = head g, k-step ks: dims 32 ks + 8 grp ..)
+  const bool qrow = (r16 & 3) == 0 && (r16 >> 2) < G;
   v8bf qa[kAtD / 32];
 #pragma unroll
   for (int ks = 0; ks < kAtD / 32; ++ks) {
     uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (r16 < G) v = *reinterpret_cast<const uint4*>(&s.q[r16][32 * ks + 8 * grp]);
+    if (qrow) v = *reinterpret_cast<const uint4*>(&s.q[r16 >> 2][32 * ks + 8 * grp]);
     qa[ks] = __builtin_bit_cast(v8bf, v);
   }
 
-  // running softmax state of this wave, per head (lanes 0..15 hold the
-  // output rows: acc o[m][j] = head j, dimension 16 m + r16)
-  float mrun[kAtMaxG], lrun[kAtMaxG];
+  // running softmax state of this wave for head gh = lane group (lanes
+  // 16 gh + j; element 0 of the output accumulator o[m] is head gh,
+  // dimension 16 m + j)
+  const int gh = grp, j16 = r16;
+  float mrun = -__builtin_inff(), lrun = 0.0f;
   v4f o[kAtD / 16];
-#pragma unroll
-  for (int g = 0; g < kAtMaxG; ++g) {
-    mrun[g] = -__builtin_inff();
-    lrun[g] = 0.0f;
-  }
 #pragma unroll
   for (int m = 0; m < kAtD / 16; ++m) o[m] = (v4f){0.f, 0.f, 0.f, 0.f};
 
@@ -227,38 +245,36 @@ __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, Att
         sc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], __builtin_bit_cast(v8bf, r.kr[blk][ks]), sc[blk], 0,
                                                           0, 0);
     }
-    // online softmax per head over the wave's 64 positions (lanes 0..15:
-    // block blk's position 16 blk + lane)
-#pragma unroll
-    for (int g = 0; g < kAtMaxG; ++g) {
+    // online softmax of head gh over the wave's 64 positions (lane
+    // 16 gh + j: block blk's position 16 blk + j)
+    {
       float s4[4];
       float mx = -__builtin_inff();
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk) {
-        const bool ok = lane < 16 && base + 16 * blk + lane < nold;
-        s4[blk] = ok ? sc[blk][g] * a.scale : -__builtin_inff();
+        const bool ok = gh < G && base + 16 * blk + j16 < nold;
+        s4[blk] = ok ? sc[blk][0] * a.scale : -__builtin_inff();
         mx = fmaxf(mx, s4[blk]);
       }
       mx = row16_max(mx);
-      const float mn = fmaxf(mrun[g], mx);
-      const float alpha = wexp(mrun[g], mn);
+      const float mn = fmaxf(mrun, mx);
+      const float alpha = wexp(mrun, mn);
       float sm = 0.0f;
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk) {
         const float e = wexp(s4[blk], mn);
         sm += e;
-        if (lane < 16) {
+        if (gh < G) {
           const uint16_t hi = f2bf(e);
-          s.p[wv][0][g][16 * blk + lane] = hi;
-          s.p[wv][1][g][16 * blk + lane] = f2bf(e - bf2f(hi));
+          s.p[wv][0][gh][16 * blk + j16] = hi;
+          s.p[wv][1][gh][16 * blk + j16] = f2bf(e - bf2f(hi));
         }
       }
       sm = row16_sum(sm);
-      lrun[g] = lrun[g] * alpha + sm;
-      mrun[g] = mn;
-      // rows j of the output accumulators are heads: lanes 0..15 hold them
+      lrun = lrun * alpha + sm;
+      mrun = mn;
 #pragma unroll
-      for (int m = 0; m < kAtD / 16; ++m) o[m][g] *= alpha;
+      for (int m = 0; m < kAtD / 16; ++m) o[m][0] *= alpha;
     }
     if (rd == 0) BTL_TRACE_AT(4);
     // probability-weighted values: 2 k-steps of 32 positions x 8 column
@@ -282,18 +298,19 @@ __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, Att
 #pragma unroll
       for (int part = 0; part < 2; ++part) {
         uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (r16 < G) v = *reinterpret_cast<const uint4*>(&s.p[wv][part][r16][32 * k2 + 8 * grp]);
+        if (qrow) v = *reinterpret_cast<const uint4*>(&s.p[wv][part][r16 >> 2][32 * k2 + 8 * grp]);
         pa[part] = __builtin_bit_cast(v8bf, v);
       }
 #pragma unroll
       for (int m = 0; m < kAtD / 16; ++m) {
-        // B operand: dimension 16 m + r16 of positions 32 k2 + 8 grp + [0, 8)
-        const uint16_t* col = &s.v[wv][8 * grp][16 * m + r16];
-        uint32_t w[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          w[e] = (uint32_t)col[(2 * e) * kAtVPitch] | ((uint32_t)col[(2 * e + 1) * kAtVPitch] << 16);
-        const v8bf vb = __builtin_bit_cast(v8bf, make_uint4(w[0], w[1], w[2], w[3]));
+        // B operand: dimension 16 m + r16 of positions 32 k2 + 8 grp + [0, 8):
+        // lane 4 r + q of the group reads row 8 grp + 4 h + r, dimensions
+        // 16 m + 4 q .. + 3, for the halves h = 0, 1
+        const int rr = r16 >> 2, qq = r16 & 3;
+        const v4s lo = lds_read_tr16(&s.v[wv][8 * grp + rr][16 * m + 4 * qq]);
+        const v4s hi = lds_read_tr16(&s.v[wv][8 * grp + 4 + rr][16 * m + 4 * qq]);
+        typedef short v8s __attribute__((ext_vector_type(8)));
+        const v8bf vb = __builtin_bit_cast(v8bf, (v8s){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w});
         o[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vb, o[m], 0, 0, 0);
         o[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vb, o[m], 0, 0, 0);
       }
@@ -302,21 +319,16 @@ __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, Att
   }
 
   // merge: every wave's partial, then the new position, in a fixed order
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < kAtMaxG; ++g) {
-      s.ml[wv][g][0] = mrun[g];
-      s.ml[wv][g][1] = lrun[g];
-    }
+  if (j16 == 0) {
+    s.ml[wv][gh][0] = mrun;
+    s.ml[wv][gh][1] = lrun;
   }
   BTL_TRACE_AT(6);
   lds_barrier();  // every wave is done with its value rows: the output partials reuse them
   float(*s_o)[kAtMaxG][kAtD] = reinterpret_cast<float(*)[kAtMaxG][kAtD]>(&s.v[0][0][0]);
-  if (lane < 16) {
+  if (gh < G) {
 #pragma unroll
-    for (int m = 0; m < kAtD / 16; ++m)
-#pragma unroll
-      for (int g = 0; g < kAtMaxG; ++g) s_o[wv][g][16 * m + lane] = o[m][g];
+    for (int m = 0; m < kAtD / 16; ++m) s_o[wv][gh][16 * m + j16] = o[m][0];
   }
   lds_barrier();
   BTL_TRACE_AT(7);

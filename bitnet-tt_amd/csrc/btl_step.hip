@@ -1003,6 +1003,50 @@ __device__ void step_attention(const StepArgs& p, int l, int gi, uint32_t E, int
   lds_barrier();  // the LDS is the next BitLinear's again
 }
 
+// Cache warming for the attention (ATT instances).  GEMM workgroups with no
+// QKV, o_proj, down or attention unit of their own (at the 2B shape the last
+// 64: gate||up-only units and spare workgroups) are idle from the end of
+// their gate||up unit of one layer to the next; there they touch every 128-byte
+// line of the next layer's cached keys and values [0, pos) of the attention
+// units on their XCD (workgroup w runs on XCD (w + c) mod 8 under round-robin
+// dispatch, so workgroups 8 apart share an XCD and its L2), so that the
+// attention units' loads hit the L2 or the last-level cache instead of HBM.
+// The touches are direct-to-LDS loads of one dword per lane into a 256-byte
+// sink no other code of these workgroups uses: no register holds their data,
+// and nothing waits for them until the workgroup's next wait.  Reading the
+// caches this way changes nothing: positions < pos are not written during the
+// step, and a line of position pos brought in early is never read back (the
+// attention takes the new row from its own registers).
+constexpr int kStepSinkInt = 18432;  // int offset of the sink (72 KiB), past the reductions and row sums
+__device__ int step_first_spare(const StepArgs& p) {
+  const int units = max(max(op_units<S_QKV>(p), op_units<S_O>(p)), op_units<S_DN>(p));
+  return max(units, p.M * p.Hkv);
+}
+__device__ void step_warm_kv(const StepArgs& p, int l, int gi, int32_t* lds) {
+  const int first = step_first_spare(p), nunits = (int)gridDim.x - kStepRows;
+  if (gi < first || l >= p.L) return;
+  const int natt = p.M * p.Hkv, rho = gi & 7;
+  const int first_rho = first + ((rho - (first & 7)) & 7);  // the first spare workgroup of this residue
+  const int kp = (gi - first_rho) >> 3;
+  const int np = (nunits - first_rho + 7) >> 3;  // spare workgroups of this residue
+  if (np <= 0) return;
+  const uint16_t* kc = reinterpret_cast<const uint16_t*>(p.kv[2 * l]);
+  const uint16_t* vc = reinterpret_cast<const uint16_t*>(p.kv[2 * l + 1]);
+  int8_t* sink = reinterpret_cast<int8_t*>(lds + kStepSinkInt);
+  for (int ga = rho, ia = 0; ga < natt; ga += 8, ++ia) {
+    if (ia % np != kp) continue;
+    const int b = ga / p.Hkv, hk = ga % p.Hkv;
+    const int pos = p.pos[b];
+    const int nold = pos >= 0 && pos < p.S ? pos : 0;
+    const int64_t base = ((int64_t)b * p.Hkv + hk) * p.S * kAtD;  // elements
+    const int lines = nold * (kAtD * 2 / 128);                     // 128-byte lines of [0, nold) per cache
+    for (int c = threadIdx.x; c < 2 * lines; c += blockDim.x) {
+      const uint16_t* src = (c < lines ? kc : vc) + base + (int64_t)(c < lines ? c : c - lines) * 64;
+      __builtin_amdgcn_global_load_lds(const_cast<uint16_t*>(src), sink, 4, 0, 0);
+    }
+  }
+}
+
 // NQ: superblocks per wave of a unit of QKV, O and GU (K = H); NDN: of DN (K = F).
 template <int NQ, int NDN, bool ATT>
 __device__ void step_gemm(const StepArgs& p, const StepOp* sops, int gi, uint32_t E, int32_t* lds) {
@@ -1012,7 +1056,13 @@ __device__ void step_gemm(const StepArgs& p, const StepOp* sops, int gi, uint32_
   WaitState ws{false, (__builtin_amdgcn_readfirstlane(p.error[16]) & 1u) != 0u};
   v4i wa[kStepWSlots], wb[kStepWSlots];
   load_unit_weights<S_QKV, NQ>(p, sops, 0, gi, wa);
+  if (ATT) step_warm_kv(p, 0, gi, lds);
   for (int l = 0; l < p.L; ++l) {
+    // With the attention, the unit index is made opaque to the compiler each
+    // layer, so that the per-unit offsets derived from it are recomputed (a
+    // few scalar and VALU operations) rather than kept live across the layer
+    // loop, where the attention body needs the registers.
+    if (ATT) __asm__ volatile("" : "+s"(gi));
     // An attention unit loads its o_proj weights after the attention (whose
     // key and value rows take the registers meanwhile): o_proj's operands
     // arrive microseconds later, through the rows' o_proj stage.
@@ -1024,6 +1074,7 @@ __device__ void step_gemm(const StepArgs& p, const StepOp* sops, int gi, uint32_
     }
     step_gemm_op<S_O, NQ, S_GU, NQ>(p, sops, l, gi, E, wb, wa, l, lds, ws);
     step_gemm_op<S_GU, NQ, S_DN, NDN>(p, sops, l, gi, E, wa, wb, l, lds, ws);
+    if (ATT) step_warm_kv(p, l + 1, gi, lds);
     step_gemm_op<S_DN, NDN, S_QKV, NQ>(p, sops, l, gi, E, wb, wa, l + 1, lds, ws);
   }
 }
@@ -1039,6 +1090,8 @@ __global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
   constexpr int kTableInts = kStepMaxLayers * kStepOps * (int)sizeof(StepOp) / 4;
   static_assert(kStepWaves * 2 * 16 * 64 + 64 + kTableInts <= 24576, "LDS layout");
   static_assert(sizeof(AttnSmem) <= (24576 - kTableInts) * 4, "the attention body's LDS below the op table");
+  static_assert(kStepSinkInt >= kStepWaves * 2 * 16 * 64 + 64 && kStepSinkInt + 64 <= 24576 - kTableInts,
+                "the cache-warming sink between the row sums and the op table");
   StepOp* sops = reinterpret_cast<StepOp*>(lds + (24576 - kTableInts));
   {
     const uint4* src = reinterpret_cast<const uint4*>(p.ops);
