@@ -1018,6 +1018,7 @@ __device__ void step_attention(const StepArgs& p, int l, int gi, uint32_t E, int
 // step, and a line of position pos brought in early is never read back (the
 // attention takes the new row from its own registers).
 constexpr int kStepSinkInt = 18432;  // int offset of the sink (72 KiB), past the reductions and row sums
+constexpr int kStepIdxInt = 20400;   // int offset of the unit index read back each layer (above the attention's LDS)
 __device__ int step_first_spare(const StepArgs& p) {
   const int units = max(max(op_units<S_QKV>(p), op_units<S_O>(p)), op_units<S_DN>(p));
   return max(units, p.M * p.Hkv);
@@ -1056,13 +1057,18 @@ __device__ void step_gemm(const StepArgs& p, const StepOp* sops, int gi, uint32_
   WaitState ws{false, (__builtin_amdgcn_readfirstlane(p.error[16]) & 1u) != 0u};
   v4i wa[kStepWSlots], wb[kStepWSlots];
   load_unit_weights<S_QKV, NQ>(p, sops, 0, gi, wa);
-  if (ATT) step_warm_kv(p, 0, gi, lds);
+  if (ATT) {
+    step_warm_kv(p, 0, gi, lds);
+    if (threadIdx.x == 0) lds[kStepIdxInt] = gi;
+    lds_barrier();
+  }
   for (int l = 0; l < p.L; ++l) {
-    // With the attention, the unit index is made opaque to the compiler each
-    // layer, so that the per-unit offsets derived from it are recomputed (a
-    // few scalar and VALU operations) rather than kept live across the layer
-    // loop, where the attention body needs the registers.
-    if (ATT) __asm__ volatile("" : "+s"(gi));
+    // With the attention, the unit index is read back from LDS each layer
+    // (a value the compiler cannot see through), so that the per-unit offsets
+    // derived from it are recomputed (a few scalar and VALU operations)
+    // rather than kept live across the layer loop, where the attention body
+    // needs the registers.
+    if (ATT) gi = __builtin_amdgcn_readfirstlane(*reinterpret_cast<volatile int32_t*>(lds + kStepIdxInt));
     // An attention unit loads its o_proj weights after the attention (whose
     // key and value rows take the registers meanwhile): o_proj's operands
     // arrive microseconds later, through the rows' o_proj stage.
@@ -1092,6 +1098,8 @@ __global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
   static_assert(sizeof(AttnSmem) <= (24576 - kTableInts) * 4, "the attention body's LDS below the op table");
   static_assert(kStepSinkInt >= kStepWaves * 2 * 16 * 64 + 64 && kStepSinkInt + 64 <= 24576 - kTableInts,
                 "the cache-warming sink between the row sums and the op table");
+  static_assert(kStepIdxInt * 4 >= (int)sizeof(AttnSmem) && kStepIdxInt < 24576 - kTableInts,
+                "the unit index word between the attention's LDS and the op table");
   StepOp* sops = reinterpret_cast<StepOp*>(lds + (24576 - kTableInts));
   {
     const uint4* src = reinterpret_cast<const uint4*>(p.ops);
