@@ -69,9 +69,9 @@ __global__ __launch_bounds__(64 * kAtWaves, 1) void k_decode_attention(AttnArgs 
   }
   __syncthreads();
   BTL_TRACE_AT(2);
-  const uint16_t o = att_body(a, s, r);
+  const uint16_t o = att_body(a, s, r, true);
   if (tid < a.G * kAtD) p.out[(int64_t)a.b * p.H * kAtD + (a.hk * a.G) * kAtD + tid] = o;
-  BTL_TRACE_AT(5);
+  BTL_TRACE_AT(7);
 }
 
 }  // namespace btl

@@ -166,7 +166,9 @@ __device__ __forceinline__ void att_load_round(const AttnPair& a, int rd, AttnRo
 // (zero for a position outside [0, S)); the other threads return 0.  Ends
 // with every LDS access of the body complete (the caller may reuse s after
 // a barrier).
-__device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, AttnRound& r) {
+// Measurement builds (-DBTL_TRACE) stamp events 3-6 (RoPE done, first
+// round's softmax done, its values done, merge barriers passed) when trace is set.
+__device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, AttnRound& r, bool trace = false) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int G = a.G;
   const bool pos_ok = a.pos_ok();
@@ -205,7 +207,7 @@ __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, Att
     }
   }
   lds_barrier();  // the rotated rows are in LDS (the cache-row stores need no acknowledgement)
-  BTL_TRACE_AT(3);
+  if (trace) BTL_TRACE_AT(3);
   if (wv < G) {  // score of the new position for head wv (lanes over D, fixed-order sum)
     const float d = bf2f(s.q[wv][2 * lane]) * bf2f(s.nw[0][2 * lane]) +
                     bf2f(s.q[wv][2 * lane + 1]) * bf2f(s.nw[0][2 * lane + 1]);
@@ -276,7 +278,7 @@ __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, Att
 #pragma unroll
       for (int m = 0; m < kAtD / 16; ++m) o[m][0] *= alpha;
     }
-    if (rd == 0) BTL_TRACE_AT(4);
+    if (rd == 0 && trace) BTL_TRACE_AT(4);
     // probability-weighted values: 2 k-steps of 32 positions x 8 column
     // blocks of 16 dimensions, probabilities as hi + lo parts; each k-step's
     // 32 value rows staged in LDS just before it (rows past the context as
@@ -323,7 +325,7 @@ __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, Att
     s.ml[wv][gh][0] = mrun;
     s.ml[wv][gh][1] = lrun;
   }
-  BTL_TRACE_AT(6);
+  if (trace) BTL_TRACE_AT(5);
   lds_barrier();  // every wave is done with its value rows: the output partials reuse them
   float(*s_o)[kAtMaxG][kAtD] = reinterpret_cast<float(*)[kAtMaxG][kAtD]>(&s.v[0][0][0]);
   if (gh < G) {
@@ -331,7 +333,7 @@ __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, Att
     for (int m = 0; m < kAtD / 16; ++m) s_o[wv][gh][16 * m + j16] = o[m][0];
   }
   lds_barrier();
-  BTL_TRACE_AT(7);
+  if (trace) BTL_TRACE_AT(6);
   uint16_t res = 0;
   {
     const int g = tid / kAtD, d = tid % kAtD;  // 512 threads: 4 heads x 128 dims

@@ -968,7 +968,7 @@ __device__ void step_attention(const StepArgs& p, int l, int gi, uint32_t E, int
   if (!a.pos_ok() && tid == 0) set_error_word(p, BAD_POSITION, (uint32_t)(l * 4 + S_O));
   AttnRound r;
   att_load_round(a, 0, r);
-  STEP_TRACE(l, 4);
+  STEP_TRACE(l, 0);
   // the new rows: thread t < 6 x 64 takes word t % 64 (two values) of row
   // segment t / 64 (query rows 0..G-1, the key row at kAtMaxG, the value row
   // at kAtMaxG + 1)
@@ -992,14 +992,15 @@ __device__ void step_attention(const StepArgs& p, int l, int gi, uint32_t E, int
     }
   }
   lds_barrier();  // the new rows are in LDS (the cache loads stay in flight)
-  const uint32_t o = att_body(a, s, r);
+  STEP_TRACE(l, 1);
+  const uint32_t o = att_body(a, s, r, l == BTL_STEP_TRACE_LAYER);
   const uint32_t pair = o | (xor_partner_u<1>(o) << 16);  // dims d, d + 1 of a head (a DPP lane swap)
   if (tid < p.G * kAtD && (tid & 1) == 0) {
     const int col = a.hk * p.G * kAtD + tid;  // heads hk G + tid / 128, dimension tid % 128
     st_coherent(att_of(p) + (int64_t)a.b * (p.H >> 1) + (col >> 1), ((uint64_t)step_tag(E, l, 0) << 32) | pair);
     *reinterpret_cast<uint32_t*>(p.attn_out + (int64_t)a.b * p.H + col) = pair;
   }
-  STEP_TRACE(l, 5);
+  STEP_TRACE(l, 7);
   lds_barrier();  // the LDS is the next BitLinear's again
 }
 
