@@ -324,13 +324,29 @@ def prefill_mfma(torch, N, dev, shapes=PREFILL_SHAPES, pmc_reps=0):
         us_bl = graph_time_us(torch, dev, bitlinear)
         ops = 2.0 * M * K * Nf
         tops = ops / (us * 1e-6) / 1e12
+        # The vendor library's int8 GEMM on the same shape (torch._int_mm, hipBLASLt on ROCm): int8 operands
+        # already unpacked, int32 output, no scale epilogue -- a reference point, not this path.
+        us_lib = None
+        try:
+            glib = torch.Generator(device=dev)
+            glib.manual_seed(PREFILL_SEED + 1)
+            a8 = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev, generator=glib)
+            b8 = torch.randint(-1, 2, (Nf, K), dtype=torch.int8, device=dev, generator=glib)
+            c32 = torch.empty((M, Nf), dtype=torch.int32, device=dev)
+            us_lib = graph_time_us(torch, dev, lambda i: torch._int_mm(a8, b8.t(), out=c32))
+            del a8, b8, c32
+        except (RuntimeError, TypeError) as e:
+            log(f"[bench] torch._int_mm unavailable for {M}x{K}x{Nf}: {e}")
         tl = N.gemm_tiling(M, K, Nf)
         tiling = (f"{tl['rows']}x{32 * tl['col_tiles']}" + (f" wq{tl['k_groups']}" if tl["kind"] == "wide" else "")
                   + (f" sk{tl['splitk']}" if tl["splitk"] > 1 else ""))
         out.append({"M": M, "K": K, "N": Nf, "tiling": tiling,
                     "us": round(us, 2), "tops": round(tops, 1), "mfma_i8_util": round(tops / MFMA_I8_PEAK_TOPS, 4),
                     "us_bitlinear": round(us_bl, 2),
-                    "mfma_i8_util_bitlinear": round(ops / (us_bl * 1e-6) / 1e12 / MFMA_I8_PEAK_TOPS, 4)})
+                    "mfma_i8_util_bitlinear": round(ops / (us_bl * 1e-6) / 1e12 / MFMA_I8_PEAK_TOPS, 4),
+                    "us_hipblaslt_int8": None if us_lib is None else round(us_lib, 2),
+                    "mfma_i8_util_hipblaslt_int8": None if us_lib is None else
+                    round(ops / (us_lib * 1e-6) / 1e12 / MFMA_I8_PEAK_TOPS, 4)})
         del pws
     return out
 
@@ -905,8 +921,10 @@ def main():
     if not args.no_prefill:
         prefill = prefill_mfma(torch, N, dev)
         for p in prefill:
+            lib = ("" if p["us_hipblaslt_int8"] is None else
+                   f"; hipBLASLt int8 GEMM {p['us_hipblaslt_int8']} us ({100 * p['mfma_i8_util_hipblaslt_int8']:.1f}%)")
             log(f"[bench] prefill M={p['M']} K={p['K']} N={p['N']}: {p['us']} us, {p['tops']} TOPS, "
-                f"MFMA-i8 {100 * p['mfma_i8_util']:.1f}%")
+                f"MFMA-i8 {100 * p['mfma_i8_util']:.1f}% (BitLinear {100 * p['mfma_i8_util_bitlinear']:.1f}%){lib}")
 
     head = None
     if not args.no_lm_head:
