@@ -115,24 +115,27 @@ constexpr int64_t kStHeader = kStAttn + (int64_t)kStepMaxLayers * 16;
 // tile.  QKV, o_proj and down run 16-row halves (v_mfma_i32_16x16x64_i8), so
 // that a unit reads half of its operand tile: QKV with two adjacent column
 // tiles per unit (its 120 tiles make 120 units), o_proj and down with one.
-// Every unit covers all of K and writes bf16 outputs (two per tagged word).
+// With the decode attention (A = true) QKV units cover all 32 rows of two
+// adjacent tiles (60 units at the 2B shape), so that the attention can run on
+// units with no QKV work.  Every unit covers all of K and writes bf16 outputs
+// (two per tagged word).
 enum { MODE_SCALE = 0, MODE_RELU2 = 1 };
-template <int J>
+template <int J, bool A = false>
 struct OpShape;
-template <>
-struct OpShape<S_QKV> {
-  static constexpr int TPW = 2, HALF = 1, MODE = MODE_SCALE;
+template <bool A>
+struct OpShape<S_QKV, A> {
+  static constexpr int TPW = 2, HALF = A ? 0 : 1, MODE = MODE_SCALE;
 };
-template <>
-struct OpShape<S_O> {
+template <bool A>
+struct OpShape<S_O, A> {
   static constexpr int TPW = 1, HALF = 1, MODE = MODE_SCALE;
 };
-template <>
-struct OpShape<S_GU> {
+template <bool A>
+struct OpShape<S_GU, A> {
   static constexpr int TPW = 2, HALF = 0, MODE = MODE_RELU2;
 };
-template <>
-struct OpShape<S_DN> {
+template <bool A>
+struct OpShape<S_DN, A> {
   static constexpr int TPW = 1, HALF = 1, MODE = MODE_SCALE;
 };
 
@@ -573,23 +576,23 @@ __device__ __forceinline__ int op_n(const StepArgs& p, int j) {  // output colum
   return j == S_QKV ? p.NQKV : j == S_GU ? 2 * p.F : p.H;
 }
 __device__ __forceinline__ int op_ks(const StepArgs& p, int j) { return j == S_DN ? p.KSF : p.KSH; }
-template <int J>
+template <int J, bool A = false>
 __device__ __forceinline__ int op_units(const StepArgs& p) {
   const int NT = op_n(p, J) / 32;
-  return J == S_GU ? NT / 2 : OpShape<J>::HALF ? 2 * NT / OpShape<J>::TPW : NT;
+  return J == S_GU ? NT / 2 : OpShape<J, A>::HALF ? 2 * NT / OpShape<J, A>::TPW : NT / OpShape<J, A>::TPW;
 }
 
 // Unit u of BitLinear J: its first tile (GU: the gate tile; the up tile is
-// F/32 further) and, for 16-row units, its row half h.  16-row units take
-// groups of TPW adjacent tiles; the two halves of a group are 8 workgroups
-// apart, so round-robin dispatch puts them on one XCD and its L2 fetches
-// their weights once.
-template <int J>
+// F/32 further) and, for 16-row units, its row half h.  Units take groups of
+// TPW adjacent tiles (GU: one gate/up pair); the two halves of a 16-row group
+// are 8 workgroups apart, so round-robin dispatch puts them on one XCD and
+// its L2 fetches their weights once.
+template <int J, bool A = false>
 __device__ __forceinline__ void unit_of(const StepArgs& p, int u, int& tile0, int& h) {
-  const int NG = op_n(p, J) / 32 / (OpShape<J>::HALF ? OpShape<J>::TPW : 1);
+  const int NG = op_n(p, J) / 32 / (OpShape<J, A>::HALF ? OpShape<J, A>::TPW : 1);
   h = 0;
-  if (!OpShape<J>::HALF) {
-    tile0 = u;
+  if (!OpShape<J, A>::HALF) {
+    tile0 = J == S_GU ? u : u * OpShape<J, A>::TPW;
     return;
   }
   const int g8 = NG & ~7;
@@ -602,7 +605,7 @@ __device__ __forceinline__ void unit_of(const StepArgs& p, int u, int& tile0, in
     g = g8 + i % rem;
     h = i / rem;
   }
-  tile0 = g * OpShape<J>::TPW;
+  tile0 = g * OpShape<J, A>::TPW;
 }
 template <int J>
 __device__ __forceinline__ int unit_tile(const StepArgs& p, int tile0, int t) {
@@ -624,22 +627,22 @@ __device__ __forceinline__ void wave_ks(int sb0, int sb1, int wv, int& wb, int& 
 // Every slot the BitLinear reads is written (zeros where the unit or wave has
 // no work), so the buffer's previous contents are dead from here on and its
 // registers free in between (the decode attention runs there).
-template <int J, int NSW>
+template <int J, int NSW, bool A = false>
 __device__ __forceinline__ void load_unit_weights(const StepArgs& p, const StepOp* sops, int l, int u,
                                                   v4i (&w)[kStepWSlots]) {
-  static_assert(OpShape<J>::TPW * NSW <= kStepWSlots, "weight slots");
+  static_assert(OpShape<J, A>::TPW * NSW <= kStepWSlots, "weight slots");
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int KS = op_ks(p, J);
   int tile0 = 0, h = 0, wb = 0, we = 0;
-  const bool unit = u < op_units<J>(p);
+  const bool unit = u < op_units<J, A>(p);
   if (unit) {
-    unit_of<J>(p, u, tile0, h);
+    unit_of<J, A>(p, u, tile0, h);
     wave_ks(0, KS, wv, wb, we);
   }
   const bool work = unit && wb < we;
   const uint32_t* wdev = sops[l * kStepOps + J].wdev;
 #pragma unroll
-  for (int t = 0; t < OpShape<J>::TPW; ++t) {
+  for (int t = 0; t < OpShape<J, A>::TPW; ++t) {
     const int tile = unit_tile<J>(p, tile0, t);
 #pragma unroll
     for (int i = 0; i < NSW; ++i) {
@@ -709,26 +712,26 @@ __device__ __forceinline__ void wait_tile_piece(const StepArgs& p, __amdgpu_buff
 // One BitLinear J of layer l on GEMM workgroup gi: wait for the operand
 // tile's rows, MFMA against the weights held in w, reduce the waves in LDS,
 // epilogue (tagged bf16 pairs), then issue the next BitLinear's weights into wn.
-template <int J, int NSW, int NJ, int NNSW>
+template <int J, int NSW, int NJ, int NNSW, bool A>
 __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int gi, uint32_t E,
                              const v4i (&w)[kStepWSlots], v4i (&wn)[kStepWSlots], int nl, int32_t* lds,
                              WaitState& ws) {
-  constexpr int TPW = OpShape<J>::TPW, MODE = OpShape<J>::MODE;
+  constexpr int TPW = OpShape<J, A>::TPW, MODE = OpShape<J, A>::MODE;
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  if (gi >= op_units<J>(p)) {
-    if (nl < p.L) load_unit_weights<NJ, NNSW>(p, sops, nl, gi, wn);
+  if (gi >= op_units<J, A>(p)) {
+    if (nl < p.L) load_unit_weights<NJ, NNSW, A>(p, sops, nl, gi, wn);
     return;
   }
   const StepOp& op = sops[l * kStepOps + J];
   int tile0, h, wb, we;
-  unit_of<J>(p, gi, tile0, h);
+  unit_of<J, A>(p, gi, tile0, h);
   wave_ks(0, op_ks(p, J), wv, wb, we);
   const int cnt = we - wb;
   const uint32_t want = step_tag(E, l, J);
   int32_t* red = lds;                                // reductions
   int32_t* s_rsum = lds + kStepWaves * 2 * 16 * 64;  // [32] row sums from the flags
   float* s_adq = reinterpret_cast<float*>(s_rsum + 32);  // [32] a/127 from the flags
-  constexpr int NR = OpShape<J>::HALF ? 16 : 32;     // rows of the unit
+  constexpr int NR = OpShape<J, A>::HALF ? 16 : 32;  // rows of the unit
   if (wv == kStepPollWave) wait_flags(p, l, J, 16 * h, NR, want, s_rsum, s_adq, ws);
   lds_barrier();  // the rows' flags are in (no wait for loads in flight)
   STEP_TRACE(l, 8 + 2 * J);
@@ -736,7 +739,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
   uint64_t* outw = out_of(p, l, J);
   const int n_out = J == S_QKV ? p.NQKV : J == S_GU ? p.F : p.H;
 
-  if constexpr (OpShape<J>::HALF) {
+  if constexpr (OpShape<J, A>::HALF) {
     // ---- rows 16h .. 16h + 15 on v_mfma_i32_16x16x64_i8, two MFMAs (columns
     // 0-15, 16-31) per 64 k.  A: lane l takes row 16h + (l & 15), k-group l >> 4
     // of the 64-k step straight from the tile (32-k step 2p + (G >> 1), half
@@ -799,7 +802,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
           wait_tile_piece(p, xa, (a_step * 64 + a_lane) * 16 + ((wb + i) * 4 + 2 * pp) * 1024, tries, ws, want);
       load();
       v4i wr[kStepWSlots];
-      load_unit_weights<J, NSW>(p, sops, l, gi, wr);
+      load_unit_weights<J, NSW, A>(p, sops, l, gi, wr);
       (void)mfma(wr);
     }
 #pragma unroll
@@ -834,7 +837,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     const int jc = lane & 31;
     // segment scales: LDS reads of the op table, issued early, off the epilogue's path
     const float sc0 = op_seg_scale(op, tile0 * 32 + jc);
-    const float sc1 = MODE == MODE_SCALE ? sc0 : op_seg_scale(op, unit_tile<J>(p, tile0, 1) * 32 + jc);
+    const float sc1 = TPW == 1 ? sc0 : op_seg_scale(op, unit_tile<J>(p, tile0, 1) * 32 + jc);
     float ad_r[2];
     int32_t rs_r[2];
 #pragma unroll
@@ -880,7 +883,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
         for (int q = 0; q < 4; ++q) wait_tile_piece(p, xa, lane * 16 + ((wb + i) * 4 + q) * 1024, tries, ws, want);
       load();
       v4i wr[kStepWSlots];
-      load_unit_weights<J, NSW>(p, sops, l, gi, wr);
+      load_unit_weights<J, NSW, A>(p, sops, l, gi, wr);
       (void)mfma(wr);
     }
 #pragma unroll
@@ -912,44 +915,49 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
       const int i = acc_row(wv + kStepWaves * rr, lane);
-      const int n = tile0 * 32 + jc;
-      uint32_t o;
-      if (MODE == MODE_SCALE) {
-        o = f2bf((float)v[0][rr] * (sc0 * ad_r[rr]));
-      } else {
-        const float gg = bf2f(f2bf((float)v[0][rr] * (sc0 * ad_r[rr])));
-        const float uu = bf2f(f2bf((float)v[TPW - 1][rr] * (sc1 * ad_r[rr])));
-        const float gr = gg > 0.0f ? gg : 0.0f;
-        const float sq = bf2f(f2bf(gr * gr));
-        o = f2bf(sq * uu);
-      }
-      const uint32_t pair = o | (xor_partner_u<1>(o) << 16);  // lanes jc, jc+1 share the row (a DPP swap)
-      if ((jc & 1) == 0) {
-        st_coherent(outw + (int64_t)i * (n_out >> 1) + (n >> 1), ((uint64_t)want << 32) | pair);
-        // the caller's copy: the same pair as one 4-byte store
-        if (J == S_QKV && i < p.M) *reinterpret_cast<uint32_t*>(p.qkv_out + (int64_t)i * p.NQKV + n) = pair;
-        if (J == S_GU && i < p.M) *reinterpret_cast<uint32_t*>(p.ffn_h + (int64_t)i * p.F + n) = pair;
+      // scale mode: one output per tile; relu2 mode: one from the gate/up pair
+      constexpr int NO = MODE == MODE_SCALE ? TPW : 1;
+#pragma unroll
+      for (int t = 0; t < NO; ++t) {
+        const int n = unit_tile<J>(p, tile0, t) * 32 + jc;
+        uint32_t o;
+        if (MODE == MODE_SCALE) {
+          o = f2bf((float)v[t][rr] * ((t == 0 ? sc0 : sc1) * ad_r[rr]));
+        } else {
+          const float gg = bf2f(f2bf((float)v[0][rr] * (sc0 * ad_r[rr])));
+          const float uu = bf2f(f2bf((float)v[TPW - 1][rr] * (sc1 * ad_r[rr])));
+          const float gr = gg > 0.0f ? gg : 0.0f;
+          const float sq = bf2f(f2bf(gr * gr));
+          o = f2bf(sq * uu);
+        }
+        const uint32_t pair = o | (xor_partner_u<1>(o) << 16);  // lanes jc, jc+1 share the row (a DPP swap)
+        if ((jc & 1) == 0) {
+          st_coherent(outw + (int64_t)i * (n_out >> 1) + (n >> 1), ((uint64_t)want << 32) | pair);
+          // the caller's copy: the same pair as one 4-byte store
+          if (J == S_QKV && i < p.M) *reinterpret_cast<uint32_t*>(p.qkv_out + (int64_t)i * p.NQKV + n) = pair;
+          if (J == S_GU && i < p.M) *reinterpret_cast<uint32_t*>(p.ffn_h + (int64_t)i * p.F + n) = pair;
+        }
       }
     }
   }
   STEP_TRACE(l, 9 + 2 * J);
   // The next BitLinear's weights, issued after this one's last wait: its
   // hand-off takes longer than the loads, and no wait here covers them.
-  if (nl < p.L) load_unit_weights<NJ, NNSW>(p, sops, nl, gi, wn);
+  if (nl < p.L) load_unit_weights<NJ, NNSW, A>(p, sops, nl, gi, wn);
 }
 
 // ------------------------------------------------------------ attention ----
-// Decode attention of user b = gi / Hkv and key-value head hk = gi % Hkv (ATT
-// instances; src/bitnet_tt/inference/generator_batch32.py:728-746), run by
-// GEMM workgroup gi between its QKV and o_proj units.  The first round of the
-// pair's cached keys and values does not depend on this step, so its loads
-// are issued first; then the new token's rows (the group's G query heads, its
+// Decode attention of user b = ai / Hkv and key-value head hk = ai % Hkv (ATT
+// instances; src/bitnet_tt/inference/generator_batch32.py:728-746), item ai of
+// the layer, run by a GEMM workgroup between its QKV and o_proj units.  The
+// first round of the pair's cached keys and values does not depend on this
+// step, so its loads are issued first; then the new token's rows (the group's G query heads, its
 // key and value head) come in as row b's tagged QKV output words, and the
 // body shared with btl_decode_attention runs on the workgroup (the same code,
 // so the same bits).  Its G x 128 outputs leave as tagged bf16 pairs, which
 // row b's workgroup polls for its o_proj stage, and as the caller's copy.
-__device__ void step_attention(const StepArgs& p, int l, int gi, uint32_t E, int32_t* lds, WaitState& ws) {
-  if (gi >= p.M * p.Hkv) return;
+__device__ void step_attention(const StepArgs& p, int l, int ai, uint32_t E, int32_t* lds, WaitState& ws) {
+  if (ai < 0 || ai >= p.M * p.Hkv) return;
   const int tid = threadIdx.x;
   AttnSmem& s = *reinterpret_cast<AttnSmem*>(lds);
   AttnPair a;
@@ -960,8 +968,8 @@ __device__ void step_attention(const StepArgs& p, int l, int gi, uint32_t E, int
   a.Hkv = p.Hkv;
   a.G = p.G;
   a.S = p.S;
-  a.b = gi / p.Hkv;
-  a.hk = gi % p.Hkv;
+  a.b = ai / p.Hkv;
+  a.hk = ai % p.Hkv;
   a.pos = p.pos[a.b];
   a.scale = p.scale;
   a.adjacent = p.adjacent;
@@ -1004,49 +1012,13 @@ __device__ void step_attention(const StepArgs& p, int l, int gi, uint32_t E, int
   lds_barrier();  // the LDS is the next BitLinear's again
 }
 
-// Cache warming for the attention (ATT instances).  GEMM workgroups with no
-// QKV, o_proj, down or attention unit of their own (at the 2B shape the last
-// 64: gate||up-only units and spare workgroups) are idle from the end of
-// their gate||up unit of one layer to the next; there they touch every 128-byte
-// line of the next layer's cached keys and values [0, pos) of the attention
-// units on their XCD (workgroup w runs on XCD (w + c) mod 8 under round-robin
-// dispatch, so workgroups 8 apart share an XCD and its L2), so that the
-// attention units' loads hit the L2 or the last-level cache instead of HBM.
-// The touches are direct-to-LDS loads of one dword per lane into a 256-byte
-// sink no other code of these workgroups uses: no register holds their data,
-// and nothing waits for them until the workgroup's next wait.  Reading the
-// caches this way changes nothing: positions < pos are not written during the
-// step, and a line of position pos brought in early is never read back (the
-// attention takes the new row from its own registers).
-constexpr int kStepSinkInt = 18432;  // int offset of the sink (72 KiB), past the reductions and row sums
-constexpr int kStepIdxInt = 20400;   // int offset of the unit index read back each layer (above the attention's LDS)
-__device__ int step_first_spare(const StepArgs& p) {
-  const int units = max(max(op_units<S_QKV>(p), op_units<S_O>(p)), op_units<S_DN>(p));
-  return max(units, p.M * p.Hkv);
-}
-__device__ void step_warm_kv(const StepArgs& p, int l, int gi, int32_t* lds) {
-  const int first = step_first_spare(p), nunits = (int)gridDim.x - kStepRows;
-  if (gi < first || l >= p.L) return;
-  const int natt = p.M * p.Hkv, rho = gi & 7;
-  const int first_rho = first + ((rho - (first & 7)) & 7);  // the first spare workgroup of this residue
-  const int kp = (gi - first_rho) >> 3;
-  const int np = (nunits - first_rho + 7) >> 3;  // spare workgroups of this residue
-  if (np <= 0) return;
-  const uint16_t* kc = reinterpret_cast<const uint16_t*>(p.kv[2 * l]);
-  const uint16_t* vc = reinterpret_cast<const uint16_t*>(p.kv[2 * l + 1]);
-  int8_t* sink = reinterpret_cast<int8_t*>(lds + kStepSinkInt);
-  for (int ga = rho, ia = 0; ga < natt; ga += 8, ++ia) {
-    if (ia % np != kp) continue;
-    const int b = ga / p.Hkv, hk = ga % p.Hkv;
-    const int pos = p.pos[b];
-    const int nold = pos >= 0 && pos < p.S ? pos : 0;
-    const int64_t base = ((int64_t)b * p.Hkv + hk) * p.S * kAtD;  // elements
-    const int lines = nold * (kAtD * 2 / 128);                     // 128-byte lines of [0, nold) per cache
-    for (int c = threadIdx.x; c < 2 * lines; c += blockDim.x) {
-      const uint16_t* src = (c < lines ? kc : vc) + base + (int64_t)(c < lines ? c : c - lines) * 64;
-      __builtin_amdgcn_global_load_lds(const_cast<uint16_t*>(src), sink, 4, 0, 0);
-    }
-  }
+constexpr int kStepIdxInt = 20400;  // int offset of the unit index read back each layer (above the attention's LDS)
+
+// The first GEMM unit with an attention item: the items take the last M * Hkv
+// units, which at the 2B shape (160 items, 60 QKV units of 224) have no QKV
+// work, so each issues its cached keys and values at the start of the layer.
+__device__ __forceinline__ int step_first_att(const StepArgs& p) {
+  return (int)gridDim.x - kStepRows - p.M * p.Hkv;
 }
 
 // NQ: superblocks per wave of a unit of QKV, O and GU (K = H); NDN: of DN (K = F).
@@ -1057,9 +1029,8 @@ __device__ void step_gemm(const StepArgs& p, const StepOp* sops, int gi, uint32_
   // are the same bits).
   WaitState ws{false, (__builtin_amdgcn_readfirstlane(p.error[16]) & 1u) != 0u};
   v4i wa[kStepWSlots], wb[kStepWSlots];
-  load_unit_weights<S_QKV, NQ>(p, sops, 0, gi, wa);
+  load_unit_weights<S_QKV, NQ, ATT>(p, sops, 0, gi, wa);
   if (ATT) {
-    step_warm_kv(p, 0, gi, lds);
     if (threadIdx.x == 0) lds[kStepIdxInt] = gi;
     lds_barrier();
   }
@@ -1073,16 +1044,16 @@ __device__ void step_gemm(const StepArgs& p, const StepOp* sops, int gi, uint32_
     // An attention unit loads its o_proj weights after the attention (whose
     // key and value rows take the registers meanwhile): o_proj's operands
     // arrive microseconds later, through the rows' o_proj stage.
-    const bool att_unit = ATT && gi < p.M * p.Hkv;
-    step_gemm_op<S_QKV, NQ, S_O, NQ>(p, sops, l, gi, E, wa, wb, att_unit ? p.L : l, lds, ws);
+    const int ai = ATT ? gi - step_first_att(p) : -1;
+    const bool att_unit = ai >= 0;
+    step_gemm_op<S_QKV, NQ, S_O, NQ, ATT>(p, sops, l, gi, E, wa, wb, att_unit ? p.L : l, lds, ws);
     if (att_unit) {
-      step_attention(p, l, gi, E, lds, ws);
-      load_unit_weights<S_O, NQ>(p, sops, l, gi, wb);
+      step_attention(p, l, ai, E, lds, ws);
+      load_unit_weights<S_O, NQ, ATT>(p, sops, l, gi, wb);
     }
-    step_gemm_op<S_O, NQ, S_GU, NQ>(p, sops, l, gi, E, wb, wa, l, lds, ws);
-    step_gemm_op<S_GU, NQ, S_DN, NDN>(p, sops, l, gi, E, wa, wb, l, lds, ws);
-    if (ATT) step_warm_kv(p, l + 1, gi, lds);
-    step_gemm_op<S_DN, NDN, S_QKV, NQ>(p, sops, l, gi, E, wb, wa, l + 1, lds, ws);
+    step_gemm_op<S_O, NQ, S_GU, NQ, ATT>(p, sops, l, gi, E, wb, wa, l, lds, ws);
+    step_gemm_op<S_GU, NQ, S_DN, NDN, ATT>(p, sops, l, gi, E, wa, wb, l, lds, ws);
+    step_gemm_op<S_DN, NDN, S_QKV, NQ, ATT>(p, sops, l, gi, E, wb, wa, l + 1, lds, ws);
   }
 }
 
@@ -1097,8 +1068,6 @@ __global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
   constexpr int kTableInts = kStepMaxLayers * kStepOps * (int)sizeof(StepOp) / 4;
   static_assert(kStepWaves * 2 * 16 * 64 + 64 + kTableInts <= 24576, "LDS layout");
   static_assert(sizeof(AttnSmem) <= (24576 - kTableInts) * 4, "the attention body's LDS below the op table");
-  static_assert(kStepSinkInt >= kStepWaves * 2 * 16 * 64 + 64 && kStepSinkInt + 64 <= 24576 - kTableInts,
-                "the cache-warming sink between the row sums and the op table");
   static_assert(kStepIdxInt * 4 >= (int)sizeof(AttnSmem) && kStepIdxInt < 24576 - kTableInts,
                 "the unit index word between the attention's LDS and the op table");
   StepOp* sops = reinterpret_cast<StepOp*>(lds + (24576 - kTableInts));
