@@ -55,6 +55,7 @@ __global__ __launch_bounds__(64 * kAtWaves, 1) void k_decode_attention(AttnArgs 
   a.pos = p.pos[a.b];
   a.scale = p.scale;
   a.adjacent = p.adjacent;
+  a.tid = tid;
   if (!a.pos_ok() && tid == 0 && a.hk == 0) st_coherent(p.error, 1);
   AttnRound r;
   att_load_round(a, 0, r);

@@ -66,6 +66,11 @@ struct AttnPair {
   int Hkv, G, S, b, hk, pos;
   float scale;
   int adjacent;  // 1: RoPE pairs (2i, 2i+1); 0: (i, i + D/2)
+  // This thread's index in the workgroup.  A caller that runs the body inside
+  // a longer loop passes an index the compiler cannot prove loop-invariant,
+  // so that the per-lane offsets and masks derived from it are recomputed
+  // (a few VALU operations) rather than held, or spilled, across the loop.
+  int tid;
   __device__ __forceinline__ bool pos_ok() const { return pos >= 0 && pos < S; }
   __device__ __forceinline__ int nold() const { return pos_ok() ? pos : 0; }  // cached positions [0, nold)
   __device__ __forceinline__ int64_t kv_base() const { return ((int64_t)b * Hkv + hk) * S; }
@@ -133,9 +138,9 @@ __device__ __forceinline__ uint4 att_ld(__amdgpu_buffer_rsrc_t r, int voff, int 
 }
 
 __device__ __forceinline__ void att_load_round(const AttnPair& a, int rd, AttnRound& r) {
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = a.tid & 63, wv = __builtin_amdgcn_readfirstlane(a.tid >> 6);
   if (rd == 0) {  // the RoPE factors of frequency tid & 63 at the position, with the first round
-    const int i = threadIdx.x & (kAtD / 2 - 1), pc = a.pos_ok() ? a.pos : 0;
+    const int i = a.tid & (kAtD / 2 - 1), pc = a.pos_ok() ? a.pos : 0;
     r.rc = a.rcos[pc * (kAtD / 2) + i];
     r.rs = a.rsin[pc * (kAtD / 2) + i];
   }
@@ -169,7 +174,7 @@ __device__ __forceinline__ void att_load_round(const AttnPair& a, int rd, AttnRo
 // Measurement builds (-DBTL_TRACE) stamp events 3-6 (RoPE done, first
 // round's softmax done, its values done, merge barriers passed) when trace is set.
 __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, AttnRound& r, bool trace = false) {
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = a.tid, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = a.G;
   const bool pos_ok = a.pos_ok();
   const int nold = a.nold();

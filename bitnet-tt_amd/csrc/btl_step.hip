@@ -947,6 +947,9 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
 }
 
 // ------------------------------------------------------------ attention ----
+// LDS words of the attention instances' GEMM workgroups, above the attention's
+// LDS: the unit index (read back each layer) and a zero (read by the attention).
+constexpr int kStepIdxInt = 20400;
 // Decode attention of user b = ai / Hkv and key-value head hk = ai % Hkv (ATT
 // instances; src/bitnet_tt/inference/generator_batch32.py:728-746), item ai of
 // the layer, run by a GEMM workgroup between its QKV and o_proj units.  The
@@ -973,6 +976,10 @@ __device__ void step_attention(const StepArgs& p, int l, int ai, uint32_t E, int
   a.pos = p.pos[a.b];
   a.scale = p.scale;
   a.adjacent = p.adjacent;
+  // the thread index plus a zero read back from LDS on every call: the body's
+  // per-lane values are recomputed in each layer rather than kept (spilled)
+  // across the layer loop
+  a.tid = tid + *reinterpret_cast<volatile int32_t*>(lds + kStepIdxInt + 1);
   if (!a.pos_ok() && tid == 0) set_error_word(p, BAD_POSITION, (uint32_t)(l * 4 + S_O));
   AttnRound r;
   att_load_round(a, 0, r);
@@ -1012,7 +1019,6 @@ __device__ void step_attention(const StepArgs& p, int l, int ai, uint32_t E, int
   lds_barrier();  // the LDS is the next BitLinear's again
 }
 
-constexpr int kStepIdxInt = 20400;  // int offset of the unit index read back each layer (above the attention's LDS)
 
 // The first GEMM unit with an attention item: the items take the last M * Hkv
 // units, which at the 2B shape (160 items, 60 QKV units of 224) have no QKV
@@ -1031,7 +1037,10 @@ __device__ void step_gemm(const StepArgs& p, const StepOp* sops, int gi, uint32_
   v4i wa[kStepWSlots], wb[kStepWSlots];
   load_unit_weights<S_QKV, NQ, ATT>(p, sops, 0, gi, wa);
   if (ATT) {
-    if (threadIdx.x == 0) lds[kStepIdxInt] = gi;
+    if (threadIdx.x == 0) {
+      lds[kStepIdxInt] = gi;
+      lds[kStepIdxInt + 1] = 0;  // the attention body's opaque zero
+    }
     lds_barrier();
   }
   for (int l = 0; l < p.L; ++l) {
@@ -1068,8 +1077,8 @@ __global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
   constexpr int kTableInts = kStepMaxLayers * kStepOps * (int)sizeof(StepOp) / 4;
   static_assert(kStepWaves * 2 * 16 * 64 + 64 + kTableInts <= 24576, "LDS layout");
   static_assert(sizeof(AttnSmem) <= (24576 - kTableInts) * 4, "the attention body's LDS below the op table");
-  static_assert(kStepIdxInt * 4 >= (int)sizeof(AttnSmem) && kStepIdxInt < 24576 - kTableInts,
-                "the unit index word between the attention's LDS and the op table");
+  static_assert(kStepIdxInt * 4 >= (int)sizeof(AttnSmem) && kStepIdxInt + 2 <= 24576 - kTableInts,
+                "the unit index and zero words between the attention's LDS and the op table");
   StepOp* sops = reinterpret_cast<StepOp*>(lds + (24576 - kTableInts));
   {
     const uint4* src = reinterpret_cast<const uint4*>(p.ops);
