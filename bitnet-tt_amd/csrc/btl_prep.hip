@@ -12,6 +12,7 @@
 
 #include <mutex>
 
+#include "btl_act_row.h"
 #include "btl_common.h"
 
 namespace btl {
@@ -169,19 +170,77 @@ __device__ float pw_abs(const float* a, int n) {
   }
 }
 
-__global__ void k_wq_block_sums(const float* __restrict__ w, int64_t n, float* __restrict__ part) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// Blocks b0, b0 + 1, ... one thread each (the partial last block).
+__global__ void k_wq_block_sums(const float* __restrict__ w, int64_t n, float* __restrict__ part, int64_t b0) {
+  const int64_t b = b0 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t start = b * 8192;
   if (start >= n) return;
   const int len = (int)((n - start) < 8192 ? (n - start) : 8192);
   part[b] = pw_abs(w + start, len);
 }
 
-__global__ void k_wq_finalize(const float* __restrict__ part, int64_t nblocks, int64_t n, float eps,
-                              float* __restrict__ scale_out) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// Full 8192-blocks, one wave each.  The split tree of 8192 is balanced (every
+// split at n / 2, a multiple of 8) down to 64 leaves of 128: lane j sums leaf j
+// (elements 128 j .. 128 j + 127) as pw_leaf_abs does, and each of the six
+// levels above adds adjacent subtrees, one xor butterfly step (float addition
+// is commutative, so which lane of a pair holds the left subtree does not
+// matter).  The same sums as the one-thread walk, in a 64th of the passes.
+__global__ __launch_bounds__(256) void k_wq_block_sums_wave(const float* __restrict__ w, int64_t nfull,
+                                                            float* __restrict__ part) {
+  const int64_t b = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (b >= nfull) return;  // wave-uniform
+  const float4* a = reinterpret_cast<const float4*>(w + b * 8192 + lane * 128);
+  float r[8];
+  {
+    const float4 x0 = a[0], x1 = a[1];
+    r[0] = fabsf(x0.x), r[1] = fabsf(x0.y), r[2] = fabsf(x0.z), r[3] = fabsf(x0.w);
+    r[4] = fabsf(x1.x), r[5] = fabsf(x1.y), r[6] = fabsf(x1.z), r[7] = fabsf(x1.w);
+  }
+#pragma unroll
+  for (int i = 1; i < 16; ++i) {
+    const float4 x0 = a[2 * i], x1 = a[2 * i + 1];
+    r[0] += fabsf(x0.x), r[1] += fabsf(x0.y), r[2] += fabsf(x0.z), r[3] += fabsf(x0.w);
+    r[4] += fabsf(x1.x), r[5] += fabsf(x1.y), r[6] += fabsf(x1.z), r[7] += fabsf(x1.w);
+  }
+  float v = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+  v = v + xor_partner<1>(v);
+  v = v + xor_partner<2>(v);
+  v = v + xor_partner<4>(v);
+  v = v + xor_partner<8>(v);
+  v = v + xor_partner<16>(v);
+  v = v + xor_partner<32>(v);
+  if (lane == 0) part[b] = v;
+}
+
+// The blocks' sums in block order (numpy adds its buffered blocks one after
+// another): 256 threads stage up to 8192 partials at a time in LDS, and
+// thread 0 adds them in order, four per LDS read.
+__global__ __launch_bounds__(256) void k_wq_finalize(const float* __restrict__ part, int64_t nblocks, int64_t n,
+                                                     float eps, float* __restrict__ scale_out) {
+  __shared__ __attribute__((aligned(16))) float sp[8192];
+  const int tid = threadIdx.x;
   float acc = 0.0f;
-  for (int64_t b = 0; b < nblocks; ++b) acc += part[b];
+  for (int64_t b0 = 0; b0 < nblocks; b0 += 8192) {
+    const int cnt = nblocks - b0 < 8192 ? (int)(nblocks - b0) : 8192;
+    for (int i = tid; i < cnt; i += 256) sp[i] = part[b0 + i];
+    __syncthreads();
+    if (tid == 0) {
+      const float4* s4 = reinterpret_cast<const float4*>(sp);
+      int i = 0;
+#pragma unroll 8
+      for (; i + 4 <= cnt; i += 4) {
+        const float4 q = s4[i >> 2];
+        acc += q.x;
+        acc += q.y;
+        acc += q.z;
+        acc += q.w;
+      }
+      for (; i < cnt; ++i) acc += sp[i];
+    }
+    __syncthreads();
+  }
+  if (tid != 0) return;
   // numpy: float32(float64(sum) / float64(count)), then np.maximum(., eps).
   float mean = (float)((double)acc / (double)n);
   scale_out[0] = mean > eps ? mean : eps;
@@ -321,10 +380,16 @@ int btl_weight_quant_ternary(const float* w, int64_t n, float eps, int8_t* q, fl
     return set_error(BTL_ERR_WORKSPACE, "btl_weight_quant_ternary: scratch %zu < %lld", scratch_bytes,
                      (long long)btl_weight_quant_scratch_bytes(n));
   hipStream_t s = (hipStream_t)stream;
-  const int64_t nb = (n + 8191) / 8192;
+  const int64_t nb = (n + 8191) / 8192, nfull = n / 8192;
   float* part = (float*)scratch;
-  hipLaunchKernelGGL(k_wq_block_sums, dim3(grid_for(nb, 64)), dim3(64), 0, s, w, n, part);
-  hipLaunchKernelGGL(k_wq_finalize, dim3(1), dim3(64), 0, s, part, nb, n, eps, scale_out);
+  // full blocks one wave each (float4 loads: w 16-byte aligned), else one thread a block
+  if (aligned(w, 16)) {
+    if (nfull > 0) hipLaunchKernelGGL(k_wq_block_sums_wave, dim3(grid_for(nfull * 64, 256)), dim3(256), 0, s, w, nfull, part);
+    if (nb > nfull) hipLaunchKernelGGL(k_wq_block_sums, dim3(1), dim3(64), 0, s, w, n, part, nfull);
+  } else {
+    hipLaunchKernelGGL(k_wq_block_sums, dim3(grid_for(nb, 64)), dim3(64), 0, s, w, n, part, (int64_t)0);
+  }
+  hipLaunchKernelGGL(k_wq_finalize, dim3(1), dim3(256), 0, s, part, nb, n, eps, scale_out);
   const int64_t blocks = grid_for(n, 256) < 65536 ? grid_for(n, 256) : 65536;
   hipLaunchKernelGGL(k_wq_quant, dim3((unsigned)blocks), dim3(256), 0, s, w, n, scale_out, q);
   return check_launch("btl_weight_quant_ternary");
