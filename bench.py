@@ -61,7 +61,8 @@ def parse():
     ap.add_argument("--step-trace", action="store_true",
                     help="load the -DBTL_TRACE build (bitnet_tt/_lib/libbtl_trace.so, from "
                          "python bitnet-tt_amd/bitnet_tt/_build.py --trace), run persistent steps and print the "
-                         "phase table of layer 10, then exit")
+                         "phase table of layer 10 (then that of the one-launch step with the decode attention, "
+                         "unless --no-attention), then exit")
     ap.add_argument("--prefill-pmc-pass", action="store_true",
                     help="run only the prefill GEMMs (5 launches per configured shape) for rocprofv3 --pmc and exit")
     return ap.parse_args()
@@ -725,13 +726,23 @@ STEP_TRACE_EVENTS = {
     14: "GEMM: down rows seen", 15: "GEMM: down outputs stored",
 }
 STEP_TRACE_ORDER = (0, 1, 8, 9, 2, 3, 10, 11, 4, 5, 12, 13, 6, 7, 14, 15)
+# The full step (btl_decode_step_full): the attention units' events 0-7 (GEMM
+# workgroups) come between QKV and o_proj; row event 2 is then "the user's
+# attention output words in".
+STEP_TRACE_ATT_EVENTS = {
+    100: "attention: cache loads issued", 101: "attention: QKV rows in", 103: "attention: RoPE done",
+    104: "attention: softmax done", 105: "attention: values done", 106: "attention: merge barriers passed",
+    107: "attention: outputs stored",
+}
+STEP_TRACE_FULL_ORDER = (0, 1, 8, 9, 100, 101, 103, 104, 105, 106, 107, 2, 3, 10, 11, 4, 5, 12, 13, 6, 7, 14, 15)
 
 
-def step_trace(step, torch, N, runs=5):
+def step_trace(step, torch, N, runs=5, full=False):
     """Phase timestamps (s_memrealtime, 100 MHz) of layer 10 of the persistent
     step from the -DBTL_TRACE build: per event, min / median / max over the
     workgroups that record it, in us from the first row workgroup's start;
-    the median over `runs` launches of each statistic."""
+    the median over `runs` launches of each statistic.  full: the one-launch
+    step with the decode attention (context 512) instead of the BitLinears."""
     import ctypes
 
     import numpy as np
@@ -741,28 +752,33 @@ def step_trace(step, torch, N, runs=5):
     rd.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
     rd.restype = ctypes.c_int
     buf = np.zeros((2048, 16, 16), dtype=np.uint64)
+    fn = step.step_persistent_full if full else step.step_persistent
+    order = STEP_TRACE_FULL_ORDER if full else STEP_TRACE_ORDER
+    names = {**STEP_TRACE_EVENTS, **STEP_TRACE_ATT_EVENTS}
+    if full:
+        names[2] = "row: attention words in"
     for _ in range(3):
-        step.step_persistent()
+        fn()
     torch.cuda.synchronize()
     rd(buf.ctypes.data, buf.nbytes)  # clears the table
-    stats = {ev: [] for ev in STEP_TRACE_ORDER}
+    stats = {ev: [] for ev in order}
     for _ in range(runs):
-        step.step_persistent()
+        fn()
         torch.cuda.synchronize()
         rd(buf.ctypes.data, buf.nbytes)
         t0 = int(buf[:32, 0, 0][buf[:32, 0, 0] > 0].min())
-        for ev in STEP_TRACE_ORDER:
-            v = buf[:32, 0, ev] if ev < 8 else buf[32:, 0, ev]
+        for ev in order:
+            v = buf[:32, 0, ev] if ev < 8 else buf[32:, 0, ev % 100]
             v = v[v > 0].astype(np.int64)
             if len(v):
                 d = (v - t0) / 100.0
                 stats[ev].append((d.min(), np.median(d), d.max(), len(v)))
     step.check()
     rows = []
-    for ev in STEP_TRACE_ORDER:
+    for ev in order:
         if stats[ev]:
             a = np.array(stats[ev])
-            rows.append({"event": STEP_TRACE_EVENTS[ev], "workgroups": int(a[0, 3]),
+            rows.append({"event": names[ev], "workgroups": int(a[0, 3]),
                          "min_us": round(float(np.median(a[:, 0])), 2), "median_us": round(float(np.median(a[:, 1])), 2),
                          "max_us": round(float(np.median(a[:, 2])), 2)})
     return rows
@@ -808,6 +824,13 @@ def main():
         print(f"{'event (layer 10)':36s} {'WGs':>4s} {'min':>7s} {'median':>7s} {'max':>7s}  (us)")
         for r in rows:
             print(f"{r['event']:36s} {r['workgroups']:4d} {r['min_us']:7.2f} {r['median_us']:7.2f} {r['max_us']:7.2f}")
+        if not args.no_attention:
+            step.alloc_attention(max_seq_len=512)
+            rows = step_trace(step, torch, N, full=True)
+            print(f"\nfull step with decode attention (context 512), {'event (layer 10)':36s}")
+            for r in rows:
+                print(f"{r['event']:36s} {r['workgroups']:4d} {r['min_us']:7.2f} {r['median_us']:7.2f} "
+                      f"{r['max_us']:7.2f}")
         return
 
     s = torch.cuda.Stream(device=dev)
