@@ -213,6 +213,30 @@ def test_persistent_full_step_matches_step_full_mini(orc, layers, batch, pos):
     _compare(_outputs(step), ref, "persistent full step")
 
 
+def test_persistent_full_step_attention_on_qkv_units(orc):
+    """More attention items than GEMM units without QKV work (26 users x 8
+    key-value heads = 208 items; 64 QKV units of 224), so that units 16-63
+    run a QKV unit and then an attention item in each layer: the one-launch
+    step against step_full, bit for bit."""
+    from bitnet_tt.config import BitNetMiniConfig
+    from bitnet_tt.decode import BitLinearDecodeStep
+
+    cfg = BitNetMiniConfig(num_layers=2, num_attention_heads=16, num_key_value_heads=8, hidden_size=2048,
+                           intermediate_size=512)
+    print("persistent full step, attention on QKV units: batch 26, 8 kv heads", flush=True)
+    step = BitLinearDecodeStep.random_init(cfg, H.dev(), seed=97, batch=26).alloc_buffers(seed=98)
+    step.alloc_attention(max_seq_len=128, pos=0)
+    step.pos.copy_(torch.from_numpy(np.random.default_rng(5).integers(0, 128, 26).astype(np.int32)))
+    state = _full_state(step)
+    step.step_full()
+    step.check()
+    ref = _outputs(step)
+    _restore(step, state)
+    step.step_persistent_full()
+    step.check()
+    _compare(_outputs(step), ref, "persistent full step, attention on QKV units")
+
+
 def test_persistent_full_step_matches_step_full_2b(orc):
     """The 2B model (30 layers, 20 query / 5 key-value heads, batch 32, every
     user at position 511 of a 512 context), the one-launch step with

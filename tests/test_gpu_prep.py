@@ -24,6 +24,20 @@ def test_weight_quant_device_matches_numpy(orc, shape):
     assert np.array_equal(q_d.cpu().numpy(), q_h)
 
 
+def test_weight_quant_device_unaligned_and_partial(orc):
+    """Full 8192-blocks plus a partial last block, from a buffer that is not
+    16-byte aligned (the one-thread block sums) and from an aligned one (one
+    wave per full block): the scale and codes equal numpy's either way."""
+    w = H.latent(1, 3 * 8192 + 12, seed=41).reshape(-1)
+    d = H.to_dev(w)
+    print("weight quant unaligned / aligned, n=%d" % (w.size - 1), flush=True)
+    for view, host in ((d[1:], w[1:]), (d[:-1], w[:-1])):
+        q_d, s_d = Q.weight_quant_ternary(view)
+        q_h, s_h = orc.weight_quant_ternary(np.ascontiguousarray(host))
+        assert np.float32(s_d) == s_h
+        assert np.array_equal(q_d.cpu().numpy(), q_h)
+
+
 def test_weight_quant_device_special_cases(orc):
     z = torch.zeros((4, 64), dtype=torch.float32, device=H.dev())
     q, s = Q.weight_quant_ternary(z)
