@@ -11,6 +11,15 @@
 //     BitLinear.  The weights of a unit are loaded into registers one
 //     BitLinear ahead (while the GEMMs of the current one wait for their
 //     operand tile), so no weight load is on the hand-off chain.
+//   With the decode attention (the ATT instances, btl_decode_step_full), the
+//     last M * Hkv GEMM workgroups also take one (user, key-value head)
+//     attention item each per layer, between QKV and o_proj: they issue the
+//     item's cached keys and values when they reach the layer, poll the
+//     user's QKV words, run the attention body shared with
+//     btl_decode_attention, and publish the heads' outputs as tagged words,
+//     which the user's row workgroup polls for its o_proj stage.  QKV units
+//     cover all 32 rows of two column tiles in these instances, so that at
+//     the 2B shape no attention unit has QKV work.
 //
 // Per layer (BitLinear j = QKV, O, GU, DN):
 //   row:  y = RMSNorm(h; input_layernorm) -> int8 tile[QKV]                 publish
