@@ -237,6 +237,48 @@ def test_persistent_full_step_attention_on_qkv_units(orc):
     _compare(_outputs(step), ref, "persistent full step, attention on QKV units")
 
 
+def test_persistent_full_step_2b_layer_against_oracle(orc):
+    """One 2B layer (20 query / 5 key-value heads, batch 32, every user at
+    position 511 of a 512 context) through the one-launch step with the
+    attention, against the oracle: QKV bit-exact, the attention within the
+    oracle tolerance (with the new cache rows), and o_proj, gate||up and down
+    from the kernel's attention output bit-exact."""
+    from bitnet_tt.config import BitNet2B4TConfig
+    from bitnet_tt.decode import BitLinearDecodeStep
+
+    cfg = BitNet2B4TConfig()
+    print("persistent full step, one 2B layer against the oracle", flush=True)
+    step = BitLinearDecodeStep.random_init(cfg, H.dev(), seed=99, num_layers=1).alloc_buffers(seed=100)
+    step.alloc_attention(max_seq_len=512)
+    B, Hq, Hkv, S = 32, cfg.num_attention_heads, cfg.num_key_value_heads, 512
+    kc0 = H.bits_of(step.kv[0].key_cache).reshape(B, Hkv, S, 128).copy()
+    vc0 = H.bits_of(step.kv[0].value_cache).reshape(B, Hkv, S, 128).copy()
+    hid = H.bits_of(step.hidden).copy()
+    pos = step.pos.cpu().numpy().astype(np.int64)
+    step.step_persistent_full()
+    step.check()
+    w = step.layers[0]
+
+    def wkn(pw):
+        return orc.devlayout_decode(pw.data.cpu().numpy().view(np.uint32), pw.in_features, pw.out_features)
+
+    qkv = orc.bitlinear(hid, wkn(w.qkv), list(w.qkv.segment_scales), list(w.qkv.segment_ends),
+                        gamma_bf16=H.bits_of(w.input_layernorm), norm_eps=step.eps)["out"]
+    assert np.array_equal(H.bits_of(step.qkv_out), qkv)
+    cos, sin = orc.rope_tables(128, S, cfg.rope_theta)
+    ref, kc2, vc2 = orc.decode_attention(qkv, kc0, vc0, pos, Hq, Hkv, cos, sin, False, step.attention.scale)
+    attn = H.bits_of(step.attn_out)
+    check(orc, attn, ref, step.kv[0], kc2, vc2)
+    h = orc.bitlinear(attn, wkn(w.o_proj), list(w.o_proj.segment_scales), gamma_bf16=H.bits_of(w.attn_sub_norm),
+                      norm_eps=step.eps, residual_bf16=hid)["out"]
+    r = orc.gate_up_relu2(h, wkn(w.gate_up), w.gate_up.segment_scales[0], w.gate_up.segment_scales[1],
+                          gamma_bf16=H.bits_of(w.post_attention_layernorm), norm_eps=step.eps)
+    assert np.array_equal(H.bits_of(step.ffn_h), r["h"])
+    h = orc.bitlinear(r["h"], wkn(w.down), list(w.down.segment_scales), gamma_bf16=H.bits_of(w.ffn_sub_norm),
+                      norm_eps=step.eps, residual_bf16=h)["out"]
+    assert np.array_equal(H.bits_of(step.hidden), h)
+
+
 def test_persistent_full_step_matches_step_full_2b(orc):
     """The 2B model (30 layers, 20 query / 5 key-value heads, batch 32, every
     user at position 511 of a 512 context), the one-launch step with
