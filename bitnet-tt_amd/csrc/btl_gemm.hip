@@ -389,7 +389,27 @@ __device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs
       for (int t = 0; t < TPW; ++t) b[t][i] = ld128(p.wdev + (((int64_t)tile[t] * p.KS + sb) * 64 + lane) * 4);
     }
   };
-  if (wb < we) load_b(wb, (we - wb) < NSB ? (we - wb) : NSB);
+  // The swaps above, in place: words 2p and 2p + 1 then hold columns 0-15 and
+  // 16-31 of 64-k step p.
+  auto regroup_b = [&]() {
+#pragma unroll
+    for (int i = 0; i < NSB; ++i)
+#pragma unroll
+      for (int t = 0; t < TPW; ++t)
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+          const auto s32 =
+              __builtin_amdgcn_permlane32_swap((uint32_t)b[t][i][2 * pp], (uint32_t)b[t][i][2 * pp + 1], false, false);
+          const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
+          b[t][i][2 * pp] = (int)s16[0];
+          b[t][i][2 * pp + 1] = (int)s16[1];
+        }
+  };
+  // The first weights are regrouped while the flags are awaited.
+  if (wb < we) {
+    load_b(wb, (we - wb) < NSB ? (we - wb) : NSB);
+    regroup_b();
+  }
 
   // the output elements this thread finishes: row 16h + er, column ec of every tile
   const int er = tid >> 5, ec = tid & 31;
@@ -413,7 +433,10 @@ __device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs
   const int a_step = lane >> 5;
   for (int base = wb; base < we; base += NSB) {
     const int cnt = (we - base) < NSB ? (we - base) : NSB;
-    if (base != wb) load_b(base, cnt);
+    if (base != wb) {
+      load_b(base, cnt);
+      regroup_b();
+    }
     v4i a[NSB][2];
 #pragma unroll
     for (int i = 0; i < NSB; ++i) {
@@ -428,11 +451,10 @@ __device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs
         for (int pp = 0; pp < 2; ++pp) {
 #pragma unroll
           for (int t = 0; t < TPW; ++t) {
-            const auto s32 =
-                __builtin_amdgcn_permlane32_swap((uint32_t)b[t][i][2 * pp], (uint32_t)b[t][i][2 * pp + 1], false, false);
-            const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
-            acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[0]), acc[t][0], 0, 0, 0);
-            acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[1]), acc[t][1], 0, 0, 0);
+            acc[t][0] =
+                __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b((uint32_t)b[t][i][2 * pp]), acc[t][0], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b((uint32_t)b[t][i][2 * pp + 1]),
+                                                              acc[t][1], 0, 0, 0);
           }
           acc_rs = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], ones, acc_rs, 0, 0, 0);
         }

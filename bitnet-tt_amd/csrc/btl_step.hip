@@ -721,9 +721,27 @@ __device__ __forceinline__ void wait_tile_piece(const StepArgs& p, __amdgpu_buff
 // One BitLinear J of layer l on GEMM workgroup gi: wait for the operand
 // tile's rows, MFMA against the weights held in w, reduce the waves in LDS,
 // epilogue (tagged bf16 pairs), then issue the next BitLinear's weights into wn.
+// The packed weight words of a 16-row unit regrouped in place for
+// v_mfma_i32_16x16x64_i8: a 32-lane and then a 16-lane swap of the words of
+// 32-k steps 2p and 2p + 1 give lane l column (l & 15) (word 2p) and column
+// 16 + (l & 15) (word 2p + 1), each with k-group l >> 4 of the 64-k step.
+template <int TPW, int NSW>
+__device__ __forceinline__ void regroup_half_weights(v4i (&w)[kStepWSlots]) {
+#pragma unroll
+  for (int s = 0; s < TPW * NSW; ++s)
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+      const auto s32 = __builtin_amdgcn_permlane32_swap((uint32_t)w[s][2 * pp], (uint32_t)w[s][2 * pp + 1], false,
+                                                        false);
+      const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
+      w[s][2 * pp] = (int)s16[0];
+      w[s][2 * pp + 1] = (int)s16[1];
+    }
+}
+
 template <int J, int NSW, int NJ, int NNSW, bool A>
 __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int gi, uint32_t E,
-                             const v4i (&w)[kStepWSlots], v4i (&wn)[kStepWSlots], int nl, int32_t* lds,
+                             v4i (&w)[kStepWSlots], v4i (&wn)[kStepWSlots], int nl, int32_t* lds,
                              WaitState& ws) {
   constexpr int TPW = OpShape<J, A>::TPW, MODE = OpShape<J, A>::MODE;
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -741,6 +759,9 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
   int32_t* s_rsum = lds + kStepWaves * 2 * 16 * 64;  // [32] row sums from the flags
   float* s_adq = reinterpret_cast<float*>(s_rsum + 32);  // [32] a/127 from the flags
   constexpr int NR = OpShape<J, A>::HALF ? 16 : 32;  // rows of the unit
+  // A 16-row unit's weight words are regrouped for its MFMA before the flags
+  // are awaited (they were loaded during the previous hand-off).
+  if constexpr (OpShape<J, A>::HALF) regroup_half_weights<TPW, NSW>(w);
   if (wv == kStepPollWave) wait_flags(p, l, J, 16 * h, NR, want, s_rsum, s_adq, ws);
   lds_barrier();  // the rows' flags are in (no wait for loads in flight)
   STEP_TRACE(l, 8 + 2 * J);
@@ -752,9 +773,8 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     // ---- rows 16h .. 16h + 15 on v_mfma_i32_16x16x64_i8, two MFMAs (columns
     // 0-15, 16-31) per 64 k.  A: lane l takes row 16h + (l & 15), k-group l >> 4
     // of the 64-k step straight from the tile (32-k step 2p + (G >> 1), half
-    // G & 1).  B: a 32-lane and then a 16-lane swap of the packed words of
-    // steps 2p and 2p + 1 give lane l column (l & 15) (+16) with its k-group.
-    // C: lane l, element j is row 4 (l >> 4) + j, column l & 15.
+    // G & 1).  B: the regrouped packed words 2p and 2p + 1 (columns 0-15 and
+    // 16-31).  C: lane l, element j is row 4 (l >> 4) + j, column l & 15.
     const int er = tid >> 5, ec = tid & 31;
     const int row = 16 * h + er;
     float sc[TPW];  // LDS reads, early: off the epilogue's path
@@ -794,11 +814,11 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
             mn = slot_min(mn, a[i][pp]);
 #pragma unroll
             for (int t = 0; t < TPW; ++t) {
-              const auto s32 = __builtin_amdgcn_permlane32_swap((uint32_t)ww[t * NSW + i][2 * pp],
-                                                                (uint32_t)ww[t * NSW + i][2 * pp + 1], false, false);
-              const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
-              acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[0]), acc[t][0], 0, 0, 0);
-              acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b(s16[1]), acc[t][1], 0, 0, 0);
+              const v4i& g = ww[t * NSW + i];
+              acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b((uint32_t)g[2 * pp]), acc[t][0],
+                                                                0, 0, 0);
+              acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], unpack_b((uint32_t)g[2 * pp + 1]),
+                                                                acc[t][1], 0, 0, 0);
             }
           }
       return mn;
@@ -812,6 +832,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
       load();
       v4i wr[kStepWSlots];
       load_unit_weights<J, NSW, A>(p, sops, l, gi, wr);
+      regroup_half_weights<TPW, NSW>(wr);
       (void)mfma(wr);
     }
 #pragma unroll
