@@ -9,10 +9,12 @@
 //  * the weights are repacked once into MFMA operand order: 16 vocab rows x
 //    32 k per KiB, lane l holding W[row l & 15][k0 + 8 (l >> 4) .. + 8], so a
 //    wave's operand is one coalesced 16-byte load per lane;
-//  * one workgroup per CU walks vocab tiles of 16 rows; its eight waves split
-//    K, each keeping its slice of the (up to 32) normalised rows in registers
-//    for the whole launch, and run v_mfma_f32_16x16x32_bf16 (one or two
-//    16-row blocks);
+//  * one workgroup per CU walks pairs of neighbouring vocab tiles of 16 rows;
+//    its eight waves split K, each keeping its slice of the (up to 32)
+//    normalised rows in registers for the whole launch, and run
+//    v_mfma_f32_16x16x32_bf16 (one or two 16-row blocks);
+//  * the fp32 logits wait in LDS and are written in whole lines after the
+//    weight stream;
 //  * the loads of the next tile are issued before the previous tile's partial
 //    sums are reduced through LDS, so the reduction runs under them;
 //  * every thread keeps the best (value, first index) of its two rows; the
@@ -32,7 +34,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kLmWaves = 8;
 constexpr int kLmMaxRows = 32;
-constexpr int kLmJunk = 384;  // workspace byte offset of the slot that out-of-range stores hit
+constexpr int kLmLgTiles = 32;  // tiles of logits a workgroup holds in LDS before writing them out
 
 struct LmArgs {
   const uint16_t* xn;  // [M, K] bf16, normalised rows
@@ -42,7 +44,6 @@ struct LmArgs {
   int32_t* tokens;    // [M]
   uint64_t* keys;     // [32] in the workspace (zero between calls)
   uint32_t* count;    // workgroups done (zero between calls)
-  float* junk;        // target of the stores of lanes outside [M, V)
 };
 
 // Total order of float bits as unsigned (larger float -> larger key).
@@ -52,20 +53,28 @@ __device__ __forceinline__ uint32_t float_order(float f) {
 }
 
 // RB row blocks of 16 (M <= 16 RB), NB k32 steps per wave (K <= 256 NB).
-// Tiles are 16 vocab rows; a workgroup takes tiles blockIdx.x + i * gridDim.x
-// and keeps two of them in flight (register sets b0 and b1): while one tile's
-// partial sums are reduced, the next one's loads are outstanding and the one
-// after is issued as soon as its registers are free.  The loop body is
-// straight-line (tiles past the end are clamped to a valid tile and their
-// results dropped; stores of lanes outside [M, V) go to a junk slot) so that
-// every wait counts exactly the loads it needs.
+// Tiles are 16 vocab rows, taken in pairs of neighbours: a workgroup takes
+// pairs blockIdx.x + j * gridDim.x, tiles 2 pair and 2 pair + 1 one after the
+// other.  It keeps two tiles in flight (register sets b0 and b1): while one
+// tile's partial sums are reduced, the next one's loads are outstanding and
+// the one after is issued as soon as its registers are free.  The loop body
+// is straight-line (tiles past the end are clamped to a valid tile and their
+// results dropped) so that every wait counts exactly the loads it needs.
+// The logits (LOGITS) collect in LDS, up to kLmLgTiles tiles, and leave in
+// whole 128-byte lines of a row (the two tiles of a pair) once the workgroup's
+// weight stream is done (or the buffer is full): stored tile by tile, 64 bytes
+// in each of 32 rows, the 16 MB of logits of 32 rows cost the stream 18 us.
 template <int RB, int NB, bool LOGITS>
 __global__ __launch_bounds__(512, 1) void k_lm_head(LmArgs p) {
   __shared__ float red[kLmWaves][RB][4][64];
+  __shared__ float lgb[LOGITS ? kLmLgTiles : 1][RB * 16][16];
   __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int G = gridDim.x;
-  const int mine = (p.VT - (int)blockIdx.x + G - 1) / G;  // >= 1: the grid is at most VT
+  const int P = (p.VT + 1) >> 1;                                 // tile pairs
+  const int mine_p = (P - (int)blockIdx.x + G - 1) / G;          // >= 1: the grid is at most P
+  const int last_pair = (int)blockIdx.x + (mine_p - 1) * G;
+  const int mine = 2 * mine_p - (2 * last_pair + 1 < p.VT ? 0 : 1);  // the last pair of an odd VT holds one tile
 
   v8bf a[RB][NB];
 #pragma unroll
@@ -87,7 +96,10 @@ __global__ __launch_bounds__(512, 1) void k_lm_head(LmArgs p) {
   float best = -__builtin_inff();
   int bidx = -1;
 
-  auto tile_of = [&](int i) { return (int)blockIdx.x + (i < mine ? i : mine - 1) * G; };
+  auto tile_of = [&](int i) {
+    const int c = i < mine ? i : mine - 1;
+    return 2 * ((int)blockIdx.x + (c >> 1) * G) + (c & 1);
+  };
   auto issue = [&](uint4 (&b)[NB], int t) {
     const uint4* src = p.w + ((int64_t)t * p.KS32 + wv * NB) * 64 + lane;
 #pragma unroll
@@ -113,8 +125,26 @@ __global__ __launch_bounds__(512, 1) void k_lm_head(LmArgs p) {
     __syncthreads();
     const int col = tile_of(i) * 16 + (e_l & 15);
     const bool ok = reducer && i < mine && row < p.M && col < p.V;
-    if (LOGITS) *(ok ? p.logits + (int64_t)row * p.V + col : p.junk) = s;
+    if (LOGITS && reducer && i < mine) lgb[i % kLmLgTiles][row][e_l & 15] = s;
     if (ok && s > best) best = s, bidx = col;  // a thread's columns only grow: ties keep the first
+  };
+  // Logits of tiles c0 .. c0 + cnt - 1 (c0 even) from LDS: a wave writes two
+  // rows of one pair, 32 consecutive columns each.
+  auto flush = [&](int c0, int cnt) {
+    __syncthreads();
+    const int cc = tid & 31, r0 = tid >> 5;
+    for (int pc = 0; pc < cnt; pc += 2) {
+      const int c = pc + (cc >> 4);
+      const int col = tile_of(c0 + c) * 16 + (cc & 15);
+#pragma unroll
+      for (int r = r0; r < RB * 16; r += 16)
+        if (c < cnt && r < p.M && col < p.V) p.logits[(int64_t)r * p.V + col] = lgb[c][r][cc & 15];
+    }
+    __syncthreads();
+  };
+  auto after = [&](int i) {  // uniform: every thread calls flush at the same tiles
+    if (LOGITS && i < mine && ((i + 1) % kLmLgTiles == 0 || i + 1 == mine))
+      flush(i - i % kLmLgTiles, i % kLmLgTiles + 1);
   };
 
   uint4 b0[NB], b1[NB];
@@ -123,8 +153,10 @@ __global__ __launch_bounds__(512, 1) void k_lm_head(LmArgs p) {
   for (int i = 0; i < mine; i += 2) {
     consume(b0, i);
     issue(b0, tile_of(i + 2));
+    after(i);
     consume(b1, i + 1);
     issue(b1, tile_of(i + 3));
+    after(i + 1);
   }
 
   // best of each row over the 16 lanes that hold its columns
@@ -248,12 +280,12 @@ int btl_lm_head(const uint16_t* xn, int64_t M, int64_t K, int64_t V, const uint1
   a.tokens = tokens;
   a.keys = reinterpret_cast<uint64_t*>(workspace);
   a.count = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(workspace) + 256);
-  a.junk = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + kLmJunk);
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       cus <= 0)
     cus = 256;
-  const dim3 grid((unsigned)(a.VT < cus ? a.VT : cus));
+  const int pairs = (a.VT + 1) / 2;
+  const dim3 grid((unsigned)(pairs < cus ? pairs : cus));
   hipStream_t s = (hipStream_t)stream;
   const int rb = M <= 16 ? 1 : 2;
   const bool lg = logits != nullptr;
