@@ -282,8 +282,9 @@ def test_persistent_full_step_2b_layer_against_oracle(orc):
 def test_persistent_full_step_matches_step_full_2b(orc):
     """The 2B model (30 layers, 20 query / 5 key-value heads, batch 32, every
     user at position 511 of a 512 context), the one-launch step with
-    attention against step_full, bit for bit; then three graph replays of the
-    one-launch step from the same state give the same bits again."""
+    attention against step_full, bit for bit; then graph replays of the
+    one-launch step from the same state give the same bits again (three
+    compared in full, 100 more on the hidden state)."""
     from bitnet_tt.config import BitNet2B4TConfig
     from bitnet_tt.decode import BitLinearDecodeStep
 
@@ -312,3 +313,15 @@ def test_persistent_full_step_matches_step_full_2b(orc):
         _ = torch.ones(1024, device=H.dev()).sum().item()  # eager work between replays
         _compare(_outputs(step), ref, f"graph replay {rep}")
     step.check()
+    # 100 more replays, the hidden state compared on the device: the hand-offs
+    # of the attention units (QKV words in, attention words out) every layer
+    ref_h = torch.from_numpy(ref["hidden"].view(np.int16)).to(H.dev())
+    bad = []
+    for rep in range(100):
+        _restore(step, state)
+        g.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(step.hidden.view(torch.int16), ref_h):
+            bad.append(rep)
+    step.check()
+    assert not bad, f"replays {bad[:10]} differ"

@@ -411,3 +411,34 @@ def test_c4_persistent_step_reread_path(orc, c4_model):
     finally:
         ws[off:off + 4] = 0
         torch.cuda.synchronize()
+
+
+def test_c4_persistent_step_many_replays(orc, c4_model):
+    """The 2B one-launch step replayed 300 times from a HIP graph, the inputs
+    restored between replays: every replay gives the oracle chain's bits and
+    no bounded wait runs out.  The hand-off protocol (flags behind unacknowledged
+    operand stores, sentinel bytes between uses, epochs as tags) is exercised
+    at every BitLinear of every replay, so a rare ordering gap would show as a
+    replay that differs or an error word."""
+    step, hiddens, _ = c4_model
+    ref = torch.from_numpy(np.ascontiguousarray(hiddens[-1]).view(np.int16)).to(H.dev())
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step.reset_hidden()
+        step.step_persistent()  # prepares this stream's workspace
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step.reset_hidden()
+        step.step_persistent()
+    bad = []
+    for rep in range(300):
+        g.replay()
+        s.synchronize()
+        if not torch.equal(step.hidden.view(torch.int16), ref):
+            bad.append(rep)
+        if rep % 100 == 99:
+            print(f"persistent step replay {rep + 1}", flush=True)
+    step.check()
+    assert not bad, f"replays {bad[:10]} differ from the oracle chain"
