@@ -179,7 +179,6 @@ __device__ __forceinline__ uint16_t att_body(const AttnPair& a, AttnSmem& s, Att
   const bool pos_ok = a.pos_ok();
   const int nold = a.nold();
   const int nrounds = (nold + kAtRound - 1) / kAtRound;
-  const int pc = pos_ok ? a.pos : 0;
   const int64_t kvb = a.kv_base();
   const int half = kAtD / 2;
   const int r16 = lane & 15, grp = lane >> 4;

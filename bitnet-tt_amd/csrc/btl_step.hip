@@ -82,6 +82,17 @@ enum { S_QKV = 0, S_O = 1, S_GU = 2, S_DN = 3, kStepOps = 4 };
 // the tagged words of (l+1, j) only after every row it covers has published
 // (l+1, j), which each row does after reading its words of (l, j).
 //
+// Operand tile layout.  A tile holds the A operands of the 32-row MFMA in
+// 1 KiB blocks, one per 32-k step: row r's 16 bytes of k-group g (k 16 g ..
+// 16 g + 15 of the step) at byte 32 r + 16 g of the block, so a 128-byte
+// line holds 32 bytes of each of 4 rows.  A wave's operand load (a 16-byte
+// piece per lane, of 32 rows or, in a 16-row unit, of 16 rows and two steps)
+// reads whole lines, and a row's store of 64 chunks of 8 bytes writes 32
+// bytes into each of 16 lines.  (The lane order of the MFMA operand itself,
+// row l & 31 and k-group l >> 5 in lane l, would put 8 rows' 16-byte pieces
+// in a line: every row store then fed twice the lines, and the row flags,
+// which follow the stores to memory, landed 0.2-0.5 us later.)
+//
 // Operand tiles between uses.  Row m writes its slice of tile j for (l, j)
 // (8-byte coherent stores, no acknowledgement wait).  Right after publishing
 // (l, j + 1), when it has all of its outputs of (l, j), it clears a share of
@@ -194,6 +205,12 @@ __device__ __forceinline__ uint32_t step_tag(uint32_t E, int l, int j) { return 
   } while (0)
 
 __device__ __forceinline__ char* layer_base(const StepArgs& p, int) { return p.layers; }
+// Byte offset of chunk c (operand bytes 8c .. 8c + 7) of row m in a tile (the
+// layout above): chunks 4i .. 4i + 3 of a row are 32 consecutive bytes of
+// block i.
+__host__ __device__ __forceinline__ int64_t tile_chunk_offset(int m, int c) {
+  return (int64_t)(c >> 2) * 1024 + (m & 31) * 32 + (c & 3) * 8;
+}
 __device__ __forceinline__ int8_t* tile_of(const StepArgs& p, int l, int j) {
   return reinterpret_cast<int8_t*>(layer_base(p, l) + p.off_xa[j]);
 }
@@ -404,7 +421,7 @@ __device__ void publish_row(const StepArgs& p, int l, int j, int m, int K, int K
 #pragma unroll
   for (int i = 0; i < C; ++i) {
     const int c = tid + kActThreads * i;
-    if (c < nch) store_chunk<true>(xa, m, c, KS, qlo[i], qhi[i]);
+    if (c < nch) st_coherent(reinterpret_cast<uint64_t*>(xa + tile_chunk_offset(m, c)), (uint64_t)qlo[i] | ((uint64_t)qhi[i] << 32));
   }
   lds_barrier();
   if (tid == 0) {
@@ -420,17 +437,16 @@ __device__ void publish_row(const StepArgs& p, int l, int j, int m, int K, int K
 // Row m's share of a tile back to the sentinel, in whole 128-byte lines (a
 // wave's store instruction writes four full lines).  The share lies in lines
 // that hold operand bytes of row m's 16-row half only: in each 1 KiB k-step
-// block, lines 0, 1, 4, 5 hold rows 0-15 and lines 2, 3, 6, 7 rows 16-31
-// (lane l of a block holds row l & 31).  The 16 rows of a half split their
-// half's 16 KS lines into shares of KS lines (16 KS 8-byte pieces each), so
-// the 32 shares cover the tile once.  Every clear being by half is what
+// block, lines 0-3 hold rows 0-15 and lines 4-7 rows 16-31.  The 16 rows of
+// a half split their half's 16 KS lines into shares of KS lines (16 KS 8-byte
+// pieces each), so the 32 shares cover the tile once.  Every clear being by half is what
 // orders it before the tile's next write: the next write of those lines is
 // by rows of the same half, and each of them publishes it only after
 // receiving outputs of units of that half which waited for row m's flag of a
 // later BitLinear (or, for gate||up, of units that waited for every row).
 __host__ __device__ __forceinline__ int64_t clear_piece_offset(int m, int KS, int pc) {
-  const int li = (m & 15) * KS + (pc >> 4), sub = li & 3;
-  return (int64_t)(li >> 2) * 1024 + ((sub & 1) + ((sub >> 1) << 2) + 2 * (m >> 4)) * 128 + (pc & 15) * 8;
+  const int li = (m & 15) * KS + (pc >> 4);
+  return (int64_t)(li >> 2) * 1024 + (m >> 4) * 512 + (li & 3) * 128 + (pc & 15) * 8;
 }
 template <int CP>
 __device__ __forceinline__ void clear_tile_share(int8_t* xa, int m, int KS) {
@@ -781,8 +797,8 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
 #pragma unroll
     for (int t = 0; t < TPW; ++t) sc[t] = op_seg_scale(op, unit_tile<J>(p, tile0, t) * 32 + ec);
     const float ad = s_adq[er];
-    const int a_lane = 16 * h + (lane & 15) + 32 * ((lane >> 4) & 1);
-    const int a_step = lane >> 5;
+    // lane l: row 16h + (l & 15), k-group (l >> 4) & 1 of 32-k step 2p + (l >> 5)
+    const int a_voff = (lane >> 5) * 1024 + (16 * h + (lane & 15)) * 32 + ((lane >> 4) & 1) * 16;
     // Operand loads, then the MFMAs as the data arrives, each operand's
     // 16-bit lanes folded into a running minimum on the way.  A piece that
     // still held the sentinel had not landed: then (rarely) the wave waits for
@@ -797,7 +813,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
         const bool mine = i < cnt;
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp)
-          a[i][pp] = ld_tile(xa, mine ? (a_step * 64 + a_lane) * 16 : 0, mine ? ((wb + i) * 4 + 2 * pp) * 1024 : 0);
+          a[i][pp] = ld_tile(xa, mine ? a_voff : 0, mine ? ((wb + i) * 4 + 2 * pp) * 1024 : 0);
         __builtin_amdgcn_sched_barrier(0);  // superblocks in order: the first MFMAs wait for the first loads
       }
     };
@@ -828,7 +844,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
       unsigned tries = 0;
       for (int i = 0; i < cnt; ++i)
         for (int pp = 0; pp < 2; ++pp)
-          wait_tile_piece(p, xa, (a_step * 64 + a_lane) * 16 + ((wb + i) * 4 + 2 * pp) * 1024, tries, ws, want);
+          wait_tile_piece(p, xa, a_voff + ((wb + i) * 4 + 2 * pp) * 1024, tries, ws, want);
       load();
       v4i wr[kStepWSlots];
       load_unit_weights<J, NSW, A>(p, sops, l, gi, wr);
@@ -877,14 +893,15 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
       rs_r[rr] = s_rsum[i];
     }
     // Operand loads, MFMAs with the sentinel fold, and the rare re-read, as
-    // in the 16-row body.
+    // in the 16-row body.  Lane l: row l & 31, k-group l >> 5.
+    const int a_voff = (lane & 31) * 32 + (lane >> 5) * 16;
     v4i a[NSW][4];
     auto load = [&]() {  // NSW superblocks in every wave, as in the 16-row body
 #pragma unroll
       for (int i = 0; i < NSW; ++i) {
         const bool mine = i < cnt;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) a[i][q] = ld_tile(xa, mine ? lane * 16 : 0, mine ? ((wb + i) * 4 + q) * 1024 : 0);
+        for (int q = 0; q < 4; ++q) a[i][q] = ld_tile(xa, mine ? a_voff : 0, mine ? ((wb + i) * 4 + q) * 1024 : 0);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -910,7 +927,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     if (__any(slot_stale(mfma(w))) || ws.reread) {
       unsigned tries = 0;
       for (int i = 0; i < cnt; ++i)
-        for (int q = 0; q < 4; ++q) wait_tile_piece(p, xa, lane * 16 + ((wb + i) * 4 + q) * 1024, tries, ws, want);
+        for (int q = 0; q < 4; ++q) wait_tile_piece(p, xa, a_voff + ((wb + i) * 4 + q) * 1024, tries, ws, want);
       load();
       v4i wr[kStepWSlots];
       load_unit_weights<J, NSW, A>(p, sops, l, gi, wr);

@@ -275,6 +275,12 @@ def test_noalloc_scratch_holds_every_decode_shape(L):
     assert L.btl_fused_workspace_bytes(2048, 6912, 2560, 0, 0) > limit
 
 
+def _line_rows(ln):
+    """Rows whose operand bytes line ln of a step tile holds (row r at bytes
+    32 r .. 32 r + 31 of each 1 KiB block)."""
+    return {(ln * 128 % 1024 + b) // 32 for b in range(0, 128, 32)}
+
+
 def _clear_share(L, m, KS):
     out = (ctypes.c_int64 * (16 * KS))()
     assert L.btl_decode_step_clear_share(m, KS, out, 16 * KS) == 0
@@ -285,8 +291,8 @@ def _clear_share(L, m, KS):
 def test_decode_step_tile_clear_shares(L, KS):
     """The persistent step's between-use clears of an operand tile (the
     function the kernel calls).  Operand layout of a tile: in each 1 KiB
-    k-step block, lane l's 16 bytes (offset 16 l) belong to row l & 31, so a
-    128-byte line holds rows of one 8-row group.  Each row's share must lie in
+    k-step block, row r's 32 bytes (both k-groups) start at offset 32 r, so a
+    128-byte line holds rows of one 4-row group.  Each row's share must lie in
     whole lines of its own 16-row half (a row of the other half may already be
     writing the tile's next use), be 8-byte aligned, and the 32 shares must
     cover the tile's 32*KS*128 bytes exactly once."""
@@ -301,7 +307,7 @@ def test_decode_step_tile_clear_shares(L, KS):
             assert o not in seen, f"piece {o} cleared by rows {seen[o]} and {m}"
             seen[o] = m
         for ln in lines:
-            rows = {(lane & 31) for lane in range((ln * 128 % 1024) // 16, (ln * 128 % 1024) // 16 + 8)}
+            rows = _line_rows(ln)
             assert {r >> 4 for r in rows} == {m >> 4}, f"row {m} clears line {ln} holding rows {sorted(rows)}"
     assert len(seen) == tile_bytes // 8
     # argument checks
@@ -319,7 +325,7 @@ def test_decode_step_tile_clear_planted_mistake_is_caught(L):
     crossing = 0
     for m, offs in bad.items():
         for ln in {o // 128 for o in offs}:
-            rows = {(lane & 31) for lane in range((ln * 128 % 1024) // 16, (ln * 128 % 1024) // 16 + 8)}
+            rows = _line_rows(ln)
             crossing += {r >> 4 for r in rows} != {m >> 4}
     assert crossing > 0
 
