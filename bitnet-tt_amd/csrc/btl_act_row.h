@@ -189,6 +189,19 @@ template <bool COHERENT>
 __device__ __forceinline__ void store_chunk(int8_t* xa, int m, int c, int KS, uint32_t lo, uint32_t hi) {
   store8<COHERENT>(xa + xa_offset(m, 8 * c, KS), lo, hi);
 }
+// The fused decode kernel's own operand tile (rows m < 32, written and read
+// inside one launch): the same 1 KiB block per 32-k step, but row m's 32
+// bytes (both k-groups) at byte 32 m of the block, so a 128-byte line holds 4
+// rows and a row's store of 64 chunks feeds 16 lines instead of 32 (the rows'
+// stores are acknowledged sooner).  Chunks 4i .. 4i + 3 are 32 consecutive
+// bytes of block i.
+__device__ __forceinline__ int64_t fused_chunk_offset(int m, int c) {
+  return (int64_t)(c >> 2) * 1024 + (m & 31) * 32 + (c & 3) * 8;
+}
+template <bool FUSED>
+__device__ __forceinline__ int64_t operand_chunk_offset(int m, int c, int KS) {
+  return FUSED ? fused_chunk_offset(m, c) : xa_offset(m, 8 * c, KS);
+}
 
 // ---- pieces of the row prologue shared by every kernel that runs it -------
 // A row lives in registers as v[i][0..7] = elements 8c..8c+7 of chunk
@@ -340,8 +353,8 @@ __device__ __forceinline__ void quant8(const float (&v)[8], float scale, uint32_
 
 // Row m of the activation prologue.  Threads 0..255 do the work; any further
 // threads of the block only take part in the barriers.  With COHERENT the
-// quantised row and a_dq are written with coherent stores (for a consumer in
-// the same launch).
+// quantised row and a_dq are written with coherent stores, the row into the
+// fused decode kernel's own tile layout (for a consumer in the same launch).
 template <bool NORM, bool QUANT, bool COHERENT, int CPT>
 __device__ void act_row(const ActArgs& p, int m, int tid) {
   static_assert(CPT >= 1 && CPT <= kActMaxChunks, "chunks per thread");
@@ -363,7 +376,8 @@ __device__ void act_row(const ActArgs& p, int m, int tid) {
   const int nchp = p.KS * 16;  // chunks up to the 128-column padding
   if (m >= p.M) {              // padding row of the last 32-row block
     if (QUANT && active) {
-      for (int c = tid; c < nchp; c += kActThreads) store8<COHERENT>(p.xa + xa_offset(m, 8 * c, p.KS), 0u, 0u);
+      for (int c = tid; c < nchp; c += kActThreads)
+        store8<COHERENT>(p.xa + operand_chunk_offset<COHERENT>(m, c, p.KS), 0u, 0u);
       if (tid == 0) {
         if (COHERENT)
           st_coherent(p.a_dq + m, 0.0f);
@@ -442,12 +456,13 @@ __device__ void act_row(const ActArgs& p, int m, int tid) {
     if (active && c < nch) {
       uint32_t lo, hi;
       quant8(v[i], scale, lo, hi, rs);
-      store_chunk<COHERENT>(p.xa, m, c, p.KS, lo, hi);
+      store8<COHERENT>(p.xa + operand_chunk_offset<COHERENT>(m, c, p.KS), lo, hi);
       if (p.xq_rm) *reinterpret_cast<uint2*>(p.xq_rm + (int64_t)m * p.K + 8 * c) = make_uint2(lo, hi);
     }
   }
   if (active)
-    for (int c = nch + tid; c < nchp; c += kActThreads) store8<COHERENT>(p.xa + xa_offset(m, 8 * c, p.KS), 0u, 0u);
+    for (int c = nch + tid; c < nchp; c += kActThreads)
+      store8<COHERENT>(p.xa + operand_chunk_offset<COHERENT>(m, c, p.KS), 0u, 0u);
 
   if (!p.rowsum) return;  // the GEMM derives row sums from its operand
 #pragma unroll

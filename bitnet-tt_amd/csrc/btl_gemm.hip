@@ -229,7 +229,10 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
       const int sb = base + (i < cnt ? i : cnt - 1);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int off = ((sb * 4 + q) * 64 + lane) * 16;
+        // lane l: row l & 31, k-group l >> 5 (the fused kernel's own tile
+        // holds a row's 32 bytes of a step together, fused_chunk_offset)
+        const int off = FUSED ? (sb * 4 + q) * 1024 + (lane & 31) * 32 + (lane >> 5) * 16
+                              : ((sb * 4 + q) * 64 + lane) * 16;
         // plain loads in both kernels: the tile is written once per launch
         // (by this launch's activation blocks, before their ready flags) and
         // caches start clean at every kernel boundary, so each XCD's L2
@@ -340,8 +343,9 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
 // v_mfma_i32_16x16x64_i8, two MFMAs (columns 0-15 and 16-31) per tile and
 // 64 k.  A 32-row MFMA would spend half its cycles on the other half's rows.
 //  * A: lane l takes row 16h + (l & 15), k-group l >> 4 of a 64-k step
-//    straight from the MFMA-order tile: k-group G of step p is 32-k step
-//    2p + (G >> 1), half G & 1, i.e. tile lane 16h + (l & 15) + 32 (G & 1).
+//    straight from the fused kernel's tile: k-group G of step p is 32-k step
+//    2p + (G >> 1), half G & 1, i.e. the 16 bytes at 32 row + 16 (G & 1) of
+//    that step's block (fused_chunk_offset).
 //  * B: the device layout gives lane l column l & 31, half l >> 5 of each
 //    32-k step.  A 32-lane swap and then a 16-lane swap of the packed words
 //    of steps 2p and 2p+1 give, in 16-lane rows r of (step, lanes),
@@ -429,7 +433,7 @@ __device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs
   // holding sum_k q[r][k].
   const v4i ones = (v4i){0x01010101, 0x01010101, 0x01010101, 0x01010101};
   v4i acc_rs = (v4i){0, 0, 0, 0};
-  const int a_lane = 16 * h + (lane & 15) + 32 * ((lane >> 4) & 1);
+  const int a_off = (16 * h + (lane & 15)) * 32 + ((lane >> 4) & 1) * 16;  // row, k-group in a step's block
   const int a_step = lane >> 5;
   for (int base = wb; base < we; base += NSB) {
     const int cnt = (we - base) < NSB ? (we - base) : NSB;
@@ -442,7 +446,7 @@ __device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs
     for (int i = 0; i < NSB; ++i) {
       const int sb = base + (i < cnt ? i : cnt - 1);
 #pragma unroll
-      for (int pp = 0; pp < 2; ++pp) a[i][pp] = ld128(p.xa + ((sb * 4 + 2 * pp + a_step) * 64 + a_lane) * 16);
+      for (int pp = 0; pp < 2; ++pp) a[i][pp] = ld128(p.xa + (sb * 4 + 2 * pp + a_step) * 1024 + a_off);
     }
 #pragma unroll
     for (int i = 0; i < NSB; ++i) {
