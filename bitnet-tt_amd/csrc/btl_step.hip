@@ -40,7 +40,9 @@
 // Hand-offs (every one crosses XCDs; a coherent hop costs ~0.45 us each way):
 //   row -> GEMM: the row's int8 operand bytes with device-coherent 8-byte
 //     stores, then, without waiting for their acknowledgement, the row's flag
-//     (two tagged words: the row's sum of quantised values and a/127).  A
+//     (one tagged word: a/127; the units sum the operand bytes they read for
+//     the weight codes' offset themselves, so the row stage ends with no
+//     reduction of its own).  A
 //     GEMM unit polls the flags of its 16 (or 32) rows, then reads its operand
 //     tile with L1-bypassing loads and checks it: between two uses every row
 //     overwrites its slice of a tile with the sentinel byte 0x80, which no
@@ -100,6 +102,7 @@ enum { S_QKV = 0, S_O = 1, S_GU = 2, S_DN = 3, kStepOps = 4 };
 // 16-row half's bytes (every unit of that half, 16-row or 32-row, has then
 // read them).  Every row stage starts with a wait for all of the row's
 // earlier memory operations (microseconds old by then, so it costs nothing),
+// and the stage's barriers put every thread's wait before thread 0's flag,
 // so a clear is performed before the row publishes anything later, and the
 // next flag of tile j of every row of the same half causally follows it
 // (through that half's units of the BitLinears in between, which wait for
@@ -214,8 +217,8 @@ __host__ __device__ __forceinline__ int64_t tile_chunk_offset(int m, int c) {
 __device__ __forceinline__ int8_t* tile_of(const StepArgs& p, int l, int j) {
   return reinterpret_cast<int8_t*>(layer_base(p, l) + p.off_xa[j]);
 }
-// Row m's flag of (l, j), on its own 128-byte line: word 0 = tag << 32 | the
-// row's sum of its quantised values, word 1 = tag << 32 | the bits of a/127.
+// Row m's flag of (l, j), on its own 128-byte line: one word, tag << 32 | the
+// bits of a/127.
 __device__ __forceinline__ uint64_t* flag_of(const StepArgs& p, int l, int j, int m) {
   return reinterpret_cast<uint64_t*>(layer_base(p, l) + p.off_flag) + (j * 32 + m) * 16;
 }
@@ -383,15 +386,15 @@ __device__ __forceinline__ void pairs_to_floats(const uint32_t (&pr)[C][4], floa
 }
 
 // RMSNorm with gain g, absmax int8 quantisation into the tile of (l, j), then
-// the row's flag (row sum and a/127), issued right behind the operand stores
-// with no wait for their acknowledgement (a GEMM unit checks the bytes it
+// the row's flag (a/127), issued right behind the operand stores with no
+// wait for their acknowledgement (a GEMM unit checks the bytes it
 // reads against the sentinel).  Rows m >= M publish zeros.  The same row code
 // as btl_bitlinear_fused.  K is a multiple of 128 (checked on the host), so
 // the row's chunks fill its slice of the tile.
 template <int C>
 __device__ void publish_row(const StepArgs& p, int l, int j, int m, int K, int KS, float (&v)[C][8],
-                            const float (&g)[C][8], uint32_t want, float* s_sum, float* s_max, int* s_rs) {
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+                            const float (&g)[C][8], uint32_t want, float* s_sum, float* s_max) {
+  const int tid = threadIdx.x;
   const int nch = K >> 3;
   int8_t* xa = tile_of(p, l, j);
   float adq = 0.0f;
@@ -409,13 +412,7 @@ __device__ void publish_row(const StepArgs& p, int l, int j, int m, int K, int K
     for (int i = 0; i < C; ++i)
       if (tid + kActThreads * i < nch) quant8(v[i], scale, qlo[i], qhi[i], rs);
   }
-  rs += (int)xor_partner_u<32>((uint32_t)rs);
-  rs += (int)xor_partner_u<16>((uint32_t)rs);
-  rs += (int)xor_partner_u<8>((uint32_t)rs);
-  rs += (int)xor_partner_u<4>((uint32_t)rs);
-  rs += (int)xor_partner_u<2>((uint32_t)rs);
-  rs += (int)xor_partner_u<1>((uint32_t)rs);
-  if (lane == 0) s_rs[wv] = rs;
+  (void)rs;  // the GEMM units sum the operand bytes they read
   // The operand bytes go out last: nothing after them in this stage reuses
   // their registers or waits on the vector-memory counter.
 #pragma unroll
@@ -423,15 +420,14 @@ __device__ void publish_row(const StepArgs& p, int l, int j, int m, int K, int K
     const int c = tid + kActThreads * i;
     if (c < nch) st_coherent(reinterpret_cast<uint64_t*>(xa + tile_chunk_offset(m, c)), (uint64_t)qlo[i] | ((uint64_t)qhi[i] << 32));
   }
-  lds_barrier();
-  if (tid == 0) {
-    int32_t tot = 0;
-#pragma unroll
-    for (int w = 0; w < kActWaves; ++w) tot += s_rs[w];
-    uint64_t* f = flag_of(p, l, j, m);
-    st_coherent(f, ((uint64_t)want << 32) | (uint32_t)tot);
-    st_coherent(f + 1, ((uint64_t)want << 32) | __float_as_uint(adq));
-  }
+  // Thread 0 sets the flag right behind its own operand stores, with no
+  // barrier for the other waves' (a barrier there measured 1 % slower per
+  // step): a unit that reads a piece before it lands sees the sentinel.  The
+  // reductions' barriers above already order the tile clear that follows
+  // after the threads that polled the row's words; a row past the batch
+  // skips them, so it takes a barrier here instead.
+  if (m >= p.M) lds_barrier();
+  if (tid == 0) st_coherent(flag_of(p, l, j, m), ((uint64_t)want << 32) | __float_as_uint(adq));
 }
 
 // Row m's share of a tile back to the sentinel, in whole 128-byte lines (a
@@ -477,8 +473,7 @@ __device__ __forceinline__ void residual_add(uint32_t (&hid)[4], const uint32_t 
 // this thread (the last tile clear among them), publish, then clear the
 // previous BitLinear's tile slice, whose readers are all done.
 template <int CF, bool ATT>
-__device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t E, float* s_sum, float* s_max,
-                         int* s_rs) {
+__device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t E, float* s_sum, float* s_max) {
   constexpr int CH = 1;
   const int tid = threadIdx.x;
   const bool live = m < p.M;
@@ -503,7 +498,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       float v[CH][8];
       pairs_to_floats<CH>(hid, v);
       STEP_TRACE(l, 0);
-      publish_row<CH>(p, l, S_QKV, m, p.H, p.KSH, v, g_qkv, step_tag(E, l, S_QKV), s_sum, s_max, s_rs);
+      publish_row<CH>(p, l, S_QKV, m, p.H, p.KSH, v, g_qkv, step_tag(E, l, S_QKV), s_sum, s_max);
       STEP_TRACE(l, 1);
       if (l > 0) clear_tile_share<CF>(tile_of(p, l - 1, S_DN), m, p.KSF);
     }
@@ -543,7 +538,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       }
       float v[CH][8];
       pairs_to_floats<CH>(pr, v);
-      publish_row<CH>(p, l, S_O, m, p.H, p.KSH, v, g, step_tag(E, l, S_O), s_sum, s_max, s_rs);
+      publish_row<CH>(p, l, S_O, m, p.H, p.KSH, v, g, step_tag(E, l, S_O), s_sum, s_max);
       STEP_TRACE(l, 3);
       clear_tile_share<CH>(tile_of(p, l, S_QKV), m, p.KSH);
     }
@@ -558,7 +553,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       residual_add(hid[0], pr[0], live);
       float v[CH][8];
       pairs_to_floats<CH>(hid, v);
-      publish_row<CH>(p, l, S_GU, m, p.H, p.KSH, v, g, step_tag(E, l, S_GU), s_sum, s_max, s_rs);
+      publish_row<CH>(p, l, S_GU, m, p.H, p.KSH, v, g, step_tag(E, l, S_GU), s_sum, s_max);
       STEP_TRACE(l, 5);
       clear_tile_share<CH>(tile_of(p, l, S_O), m, p.KSH);
     }
@@ -572,7 +567,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       STEP_TRACE(l, 6);
       float v[CF][8];
       pairs_to_floats<CF>(pr, v);
-      publish_row<CF>(p, l, S_DN, m, p.F, p.KSF, v, g, step_tag(E, l, S_DN), s_sum, s_max, s_rs);
+      publish_row<CF>(p, l, S_DN, m, p.F, p.KSF, v, g, step_tag(E, l, S_DN), s_sum, s_max);
       STEP_TRACE(l, 7);
       clear_tile_share<CH>(tile_of(p, l, S_GU), m, p.KSH);
     }
@@ -677,28 +672,22 @@ __device__ __forceinline__ void load_unit_weights(const StepArgs& p, const StepO
   }
 }
 
-// Poll wave: wait for the flags of rows [r0, r0 + n) of (l, j), lanes 0..31
-// reading word 0 and lanes 32..63 word 1 of row r0 + (lane & 31); the row
-// sums they carry go to s_rsum[0 .. n), a/127 to s_adq[0 .. n).
-__device__ void wait_flags(const StepArgs& p, int l, int j, int r0, int n, uint32_t want, int* s_rsum, float* s_adq,
+// Poll wave: wait for the flags of rows [r0, r0 + n) of (l, j), n <= 32, lane
+// r reading row r0 + r; the a/127 they carry go to s_adq[0 .. n).
+__device__ void wait_flags(const StepArgs& p, int l, int j, int r0, int n, uint32_t want, float* s_adq,
                            WaitState& ws) {
-  const int lane = threadIdx.x & 63, r = lane & 31, word = lane >> 5;
+  const int r = threadIdx.x & 63;
   const bool act = r < n;
   unsigned k = 0;
   uint64_t f = 0;
   while (!ws.dead) {
-    if (act) f = ld_coherent(flag_of(p, l, j, r0 + r) + word);
+    if (act) f = ld_coherent(flag_of(p, l, j, r0 + r));
     const bool ok = !act || (uint32_t)(f >> 32) == want;
     if (__all(ok)) break;
     if (should_stop(p, ++k, ws, WAIT_FLAGS, want)) break;
     __builtin_amdgcn_s_sleep(BTL_STEP_POLL_SLEEP);
   }
-  if (act) {
-    if (word == 0)
-      s_rsum[r] = (int32_t)(uint32_t)f;
-    else
-      s_adq[r] = __uint_as_float((uint32_t)f);
-  }
+  if (act) s_adq[r] = __uint_as_float((uint32_t)f);
 }
 
 // Running minimum of the 16-bit lanes of the operand dwords read (v_pk_min_i16);
@@ -716,24 +705,10 @@ __device__ __forceinline__ uint32_t slot_min(uint32_t mn, const v4i& a) {
 __device__ __forceinline__ bool slot_stale(uint32_t mn) {
   return (int)(short)(mn & 0xffffu) <= kTileSentinelMax16 || (int)(short)(mn >> 16) <= kTileSentinelMax16;
 }
-// Rare path of an operand read that found the sentinel: polls the two 8-byte
-// pieces of one 16-byte slot (dwords 0 and 2, 4-byte loads that bypass the L1)
-// until neither is the sentinel, or the error word is set, or the wait runs
-// out (which sets it).  The slot is then read again in full.
-__device__ __forceinline__ void wait_tile_piece(const StepArgs& p, __amdgpu_buffer_rsrc_t xa, int off, unsigned& n,
-                                                WaitState& ws, uint32_t want) {
-  while (!ws.dead) {
-    const uint32_t d0 = __builtin_amdgcn_raw_buffer_load_b32(xa, off, 0, 16);
-    const uint32_t d2 = __builtin_amdgcn_raw_buffer_load_b32(xa, off + 8, 0, 16);
-    if (!slot_stale(pk_min_i16(d0, d2))) break;
-    if (++n > p.spin_limit) set_error_word(p, WAIT_TILE, want);
-    if (n > p.spin_limit || ld_coherent(p.error) != 0u) {
-      ws.dead = true;
-      break;
-    }
-    __builtin_amdgcn_s_sleep(BTL_STEP_POLL_SLEEP);
-  }
-}
+// Rare path of an operand read that found the sentinel: every operand of the
+// wave is read again, all in one round, with the weights (issued first), and
+// the MFMAs redone, until no piece holds the sentinel or the wait runs out
+// (which sets the error word).  One round usually finds every piece landed.
 // One BitLinear J of layer l on GEMM workgroup gi: wait for the operand
 // tile's rows, MFMA against the weights held in w, reduce the waves in LDS,
 // epilogue (tagged bf16 pairs), then issue the next BitLinear's weights into wn.
@@ -772,13 +747,12 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
   const int cnt = we - wb;
   const uint32_t want = step_tag(E, l, J);
   int32_t* red = lds;                                // reductions
-  int32_t* s_rsum = lds + kStepWaves * 2 * 16 * 64;  // [32] row sums from the flags
-  float* s_adq = reinterpret_cast<float*>(s_rsum + 32);  // [32] a/127 from the flags
+  float* s_adq = reinterpret_cast<float*>(lds + kStepWaves * 2 * 16 * 64);  // [32] a/127 from the flags
   constexpr int NR = OpShape<J, A>::HALF ? 16 : 32;  // rows of the unit
   // A 16-row unit's weight words are regrouped for its MFMA before the flags
   // are awaited (they were loaded during the previous hand-off).
   if constexpr (OpShape<J, A>::HALF) regroup_half_weights<TPW, NSW>(w);
-  if (wv == kStepPollWave) wait_flags(p, l, J, 16 * h, NR, want, s_rsum, s_adq, ws);
+  if (wv == kStepPollWave) wait_flags(p, l, J, 16 * h, NR, want, s_adq, ws);
   lds_barrier();  // the rows' flags are in (no wait for loads in flight)
   STEP_TRACE(l, 8 + 2 * J);
   const __amdgpu_buffer_rsrc_t xa = tile_rsrc(tile_of(p, l, J), 32 * op_ks(p, J) * 128);
@@ -801,8 +775,13 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     const int a_voff = (lane >> 5) * 1024 + (16 * h + (lane & 15)) * 32 + ((lane >> 4) & 1) * 16;
     // Operand loads, then the MFMAs as the data arrives, each operand's
     // 16-bit lanes folded into a running minimum on the way.  A piece that
-    // still held the sentinel had not landed: then (rarely) the wave waits for
-    // its pieces, reads them and its weights again, and redoes the MFMAs.
+    // still held the sentinel had not landed: then (rarely) the wave reads its
+    // operands and weights again and redoes the MFMAs, until all have landed.
+    // One more MFMA per operand, against all-ones bytes, gives the wave's
+    // share of each row's sum of quantised values in every column of
+    // acc_rs (the weight codes are value + 1); the body waits on its 2-bit
+    // unpack on the VALU more than on the MFMAs, so this one runs in their
+    // shadow.
     v4i a[NSW][2];
     // Every wave issues NSW superblocks of loads (one past its range reads the
     // tile's first 16 bytes in every lane, one line), so all waves count the
@@ -817,10 +796,12 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
         __builtin_amdgcn_sched_barrier(0);  // superblocks in order: the first MFMAs wait for the first loads
       }
     };
-    v4i acc[TPW][2];
+    v4i acc[TPW][2], acc_rs;
+    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
     auto mfma = [&](const v4i (&ww)[kStepWSlots]) {
 #pragma unroll
       for (int t = 0; t < TPW; ++t) acc[t][0] = acc[t][1] = (v4i){0, 0, 0, 0};
+      acc_rs = (v4i){0, 0, 0, 0};
       uint32_t mn = 0x7fff7fffu;
 #pragma unroll
       for (int i = 0; i < NSW; ++i)
@@ -828,6 +809,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
 #pragma unroll
           for (int pp = 0; pp < 2; ++pp) {
             mn = slot_min(mn, a[i][pp]);
+            acc_rs = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][pp], ones, acc_rs, 0, 0, 0);
 #pragma unroll
             for (int t = 0; t < TPW; ++t) {
               const v4i& g = ww[t * NSW + i];
@@ -841,33 +823,32 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     };
     load();
     if (__any(slot_stale(mfma(w))) || ws.reread) {
-      unsigned tries = 0;
-      for (int i = 0; i < cnt; ++i)
-        for (int pp = 0; pp < 2; ++pp)
-          wait_tile_piece(p, xa, a_voff + ((wb + i) * 4 + 2 * pp) * 1024, tries, ws, want);
-      load();
       v4i wr[kStepWSlots];
       load_unit_weights<J, NSW, A>(p, sops, l, gi, wr);
+      load();
       regroup_half_weights<TPW, NSW>(wr);
-      (void)mfma(wr);
+      unsigned tries = 0;
+      while (!ws.dead && __any(slot_stale(mfma(wr))) && !should_stop(p, ++tries, ws, WAIT_TILE, want)) {
+        __builtin_amdgcn_s_sleep(BTL_STEP_POLL_SLEEP);
+        load();
+      }
     }
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        red[((wv * TPW + t) * 8 + q) * 64 + lane] = acc[t][0][q];
-        red[((wv * TPW + t) * 8 + 4 + q) * 64 + lane] = acc[t][1][q];
+        red[((wv * TPW + t) * 8 + q) * 64 + lane] = acc[t][0][q] - acc_rs[q];
+        red[((wv * TPW + t) * 8 + 4 + q) * 64 + lane] = acc[t][1][q] - acc_rs[q];
       }
     lds_barrier();
     const int reg = 4 * (ec >> 4) + (er & 3), src = 16 * (er >> 2) + (ec & 15);
     int32_t sum[TPW];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      sum[t] = -s_rsum[er];
+      sum[t] = 0;
 #pragma unroll
       for (int v2 = 0; v2 < kStepWaves; ++v2) sum[t] += red[((v2 * TPW + t) * 8 + reg) * 64 + src];
     }
-    lds_barrier();  // LDS free for the next BitLinear
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       const int n = unit_tile<J>(p, tile0, t) * 32 + ec;
@@ -878,6 +859,10 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
         if (J == S_QKV && row < p.M) *reinterpret_cast<uint32_t*>(p.qkv_out + (int64_t)row * p.NQKV + n) = pair;
       }
     }
+    // LDS free for the next BitLinear; the barrier after the stores keeps
+    // them ahead of every wave's next weight loads (1 % faster per step than
+    // the stores after it)
+    lds_barrier();
   } else {
     // ---- all 32 rows on v_mfma_i32_32x32x32_i8 ----
     const int jc = lane & 31;
@@ -885,15 +870,13 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     const float sc0 = op_seg_scale(op, tile0 * 32 + jc);
     const float sc1 = TPW == 1 ? sc0 : op_seg_scale(op, unit_tile<J>(p, tile0, 1) * 32 + jc);
     float ad_r[2];
-    int32_t rs_r[2];
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      const int i = acc_row(wv + kStepWaves * rr, lane);
-      ad_r[rr] = s_adq[i];
-      rs_r[rr] = s_rsum[i];
-    }
+    for (int rr = 0; rr < 2; ++rr) ad_r[rr] = s_adq[acc_row(wv + kStepWaves * rr, lane)];
     // Operand loads, MFMAs with the sentinel fold, and the rare re-read, as
-    // in the 16-row body.  Lane l: row l & 31, k-group l >> 5.
+    // in the 16-row body, and the row sums from an MFMA against all-ones
+    // bytes as there (v_dot4 on the operand bytes instead, on the VALU that
+    // the unpack already keeps busy, measured 1 % slower per step).  Lane l:
+    // row l & 31, k-group l >> 5.
     const int a_voff = (lane & 31) * 32 + (lane >> 5) * 16;
     v4i a[NSW][4];
     auto load = [&]() {  // NSW superblocks in every wave, as in the 16-row body
@@ -905,10 +888,12 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
         __builtin_amdgcn_sched_barrier(0);
       }
     };
-    v16i acc[TPW];
+    v16i acc[TPW], acc_rs;
+    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
     auto mfma = [&](const v4i (&ww)[kStepWSlots]) {
 #pragma unroll
       for (int t = 0; t < TPW; ++t) acc[t] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+      acc_rs = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
       uint32_t mn = 0x7fff7fffu;
 #pragma unroll
       for (int i = 0; i < NSW; ++i)
@@ -916,6 +901,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             mn = slot_min(mn, a[i][q]);
+            acc_rs = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][q], ones, acc_rs, 0, 0, 0);
 #pragma unroll
             for (int t = 0; t < TPW; ++t)
               acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][q], unpack_b((uint32_t)ww[t * NSW + i][q]), acc[t],
@@ -925,18 +911,19 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     };
     load();
     if (__any(slot_stale(mfma(w))) || ws.reread) {
-      unsigned tries = 0;
-      for (int i = 0; i < cnt; ++i)
-        for (int q = 0; q < 4; ++q) wait_tile_piece(p, xa, a_voff + ((wb + i) * 4 + q) * 1024, tries, ws, want);
-      load();
       v4i wr[kStepWSlots];
       load_unit_weights<J, NSW, A>(p, sops, l, gi, wr);
-      (void)mfma(wr);
+      load();
+      unsigned tries = 0;
+      while (!ws.dead && __any(slot_stale(mfma(wr))) && !should_stop(p, ++tries, ws, WAIT_TILE, want)) {
+        __builtin_amdgcn_s_sleep(BTL_STEP_POLL_SLEEP);
+        load();
+      }
     }
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) red[((wv * TPW + t) * 16 + r) * 64 + lane] = acc[t][r];
+      for (int r = 0; r < 16; ++r) red[((wv * TPW + t) * 16 + r) * 64 + lane] = acc[t][r] - acc_rs[r];
     lds_barrier();
     // thread (wv, lane) finishes rows acc_row(wv + 8 rr, lane), column lane & 31, of every tile
     int32_t v[TPW][2];
@@ -945,16 +932,12 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
       const int r = wv + kStepWaves * rr;
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
-        int32_t sum = -rs_r[rr];
+        int32_t sum = 0;
 #pragma unroll
         for (int v2 = 0; v2 < kStepWaves; ++v2) sum += red[((v2 * TPW + t) * 16 + r) * 64 + lane];
         v[t][rr] = sum;
       }
     }
-    // LDS free for the next BitLinear.  The barrier also keeps every wave's
-    // output stores ahead of any wave's loads of the next weights in the CU's
-    // memory pipeline (two reduction areas without it measured 1 % slower).
-    lds_barrier();
     // Every load of this BitLinear has been consumed; settling the counter
     // here, before the first store, keeps the compiler from placing a wait
     // (for the stores' acknowledgements too) between the two rows' stores.
@@ -986,6 +969,11 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
         }
       }
     }
+    // LDS free for the next BitLinear.  The barrier also keeps every wave's
+    // output stores ahead of any wave's loads of the next weights in the CU's
+    // memory pipeline (two reduction areas without it measured 1 % slower;
+    // the barrier before the stores instead of after them, 0.2 %).
+    lds_barrier();
   }
   STEP_TRACE(l, 9 + 2 * J);
   // The next BitLinear's weights, issued after this one's last wait: its
@@ -1113,14 +1101,15 @@ __device__ void step_gemm(const StepArgs& p, const StepOp* sops, int gi, uint32_
 
 template <int CF, int NQ, int NDN, bool ATT>
 __global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
-  // GEMM: reductions [8][2][16][64] int32 + 32 row sums; rows: 24 words.  The op table
+  // GEMM: reductions [8][2][16][64] int32 and 32 a/127; rows: 16 words.  The op table
   // (up to 16 KiB) is copied into LDS above them, so reading a weight address or a
   // scale is an LDS read, never a vector memory load waited for with the weight
   // stream.  96 KiB in all: more than half of a CU's LDS, so no CU ever holds two
   // workgroups of the launch.
   __shared__ __attribute__((aligned(16))) int32_t lds[24576];
   constexpr int kTableInts = kStepMaxLayers * kStepOps * (int)sizeof(StepOp) / 4;
-  static_assert(kStepWaves * 2 * 16 * 64 + 64 + kTableInts <= 24576, "LDS layout");
+  static_assert(kStepWaves * 2 * 16 * 64 + 32 + kTableInts <= 24576 && kStepWaves * 2 * 16 * 64 + 32 <= kStepIdxInt,
+                "LDS layout");
   static_assert(sizeof(AttnSmem) <= (24576 - kTableInts) * 4, "the attention body's LDS below the op table");
   static_assert(kStepIdxInt * 4 >= (int)sizeof(AttnSmem) && kStepIdxInt + 2 <= 24576 - kTableInts,
                 "the unit index and zero words between the attention's LDS and the op table");
@@ -1136,7 +1125,7 @@ __global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
   const uint32_t E = p.epoch[b] + 1u;  // this launch (written by the previous launch of the step)
   if (b < kStepRows) {
     float* f = reinterpret_cast<float*>(lds);
-    step_row<CF, ATT>(p, sops, b, E, f, f + kActWaves, reinterpret_cast<int*>(lds) + 2 * kActWaves);
+    step_row<CF, ATT>(p, sops, b, E, f, f + kActWaves);
   } else {
     step_gemm<NQ, NDN, ATT>(p, sops, b - kStepRows, E, lds);
   }
@@ -1167,17 +1156,14 @@ __device__ void floor_row(const StepArgs& p, int m, uint32_t E) {
                             reinterpret_cast<uint32_t(&)[1][4]>(pr), ws);
       }
       __syncthreads();
-      if (threadIdx.x == 0) {
-        st_coherent(flag_of(p, l, j, m), (uint64_t)step_tag(E, l, j) << 32);
-        st_coherent(flag_of(p, l, j, m) + 1, (uint64_t)step_tag(E, l, j) << 32);
-      }
+      if (threadIdx.x == 0) st_coherent(flag_of(p, l, j, m), (uint64_t)step_tag(E, l, j) << 32);
     }
   uint32_t pr[1][4];  // the last down projection's words end the row's step
   wait_row_words<1>(p, out_of(p, p.L - 1, S_DN) + (int64_t)m * (p.H >> 1), p.H, step_tag(E, p.L - 1, S_DN), pr, ws);
 }
 
 template <int J>
-__device__ __forceinline__ void floor_gemm_op(const StepArgs& p, int l, int gi, uint32_t E, int32_t* s_rsum, float* s_adq,
+__device__ __forceinline__ void floor_gemm_op(const StepArgs& p, int l, int gi, uint32_t E, float* s_adq,
                                               WaitState& ws) {
   if (gi >= op_units<J>(p)) return;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -1185,7 +1171,7 @@ __device__ __forceinline__ void floor_gemm_op(const StepArgs& p, int l, int gi, 
   unit_of<J>(p, gi, tile0, h);
   const uint32_t want = step_tag(E, l, J);
   constexpr int NR = OpShape<J>::HALF ? 16 : 32;
-  if (wv == kStepPollWave) wait_flags(p, l, J, 16 * h, NR, want, s_rsum, s_adq, ws);
+  if (wv == kStepPollWave) wait_flags(p, l, J, 16 * h, NR, want, s_adq, ws);
   lds_barrier();
   uint64_t* outw = out_of(p, l, J);
   const int n_out = J == S_QKV ? p.NQKV : J == S_GU ? p.F : p.H;
@@ -1208,7 +1194,6 @@ __device__ __forceinline__ void floor_gemm_op(const StepArgs& p, int l, int gi, 
 
 template <int CF>
 __global__ __launch_bounds__(512) void k_decode_step_floor(StepArgs p) {
-  __shared__ int32_t s_rsum[32];
   __shared__ float s_adq[32];
   const int b = blockIdx.x;
   const uint32_t E = p.epoch[b] + 1u;
@@ -1217,10 +1202,10 @@ __global__ __launch_bounds__(512) void k_decode_step_floor(StepArgs p) {
   } else {
     WaitState ws{false};
     for (int l = 0; l < p.L; ++l) {
-      floor_gemm_op<S_QKV>(p, l, b - kStepRows, E, s_rsum, s_adq, ws);
-      floor_gemm_op<S_O>(p, l, b - kStepRows, E, s_rsum, s_adq, ws);
-      floor_gemm_op<S_GU>(p, l, b - kStepRows, E, s_rsum, s_adq, ws);
-      floor_gemm_op<S_DN>(p, l, b - kStepRows, E, s_rsum, s_adq, ws);
+      floor_gemm_op<S_QKV>(p, l, b - kStepRows, E, s_adq, ws);
+      floor_gemm_op<S_O>(p, l, b - kStepRows, E, s_adq, ws);
+      floor_gemm_op<S_GU>(p, l, b - kStepRows, E, s_adq, ws);
+      floor_gemm_op<S_DN>(p, l, b - kStepRows, E, s_adq, ws);
     }
   }
   if (threadIdx.x == 0) p.epoch[b] = E;
