@@ -219,6 +219,9 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
     for (int rr = 0; rr < RR; ++rr) ad_pre[rr] = ld_coherent(p.a_dq + acc_row(wv + WAVES * rr, lane));
   }
 
+  // Row sums from v_dot4 on the A bytes (an MFMA against an all-ones operand
+  // instead measured 0.7 us slower per gate||up launch: this body's MFMAs
+  // set its pace).
   int32_t rs_lane = 0;  // sum of this lane's A bytes (row lane & 31, half lane >> 5)
   for (int base = wb; base < we; base += NSB) {
     const int cnt = (we - base) < NSB ? (we - base) : NSB;
@@ -250,10 +253,7 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
             const uint32_t d = (uint32_t)b[t][i][q];
             acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][q], unpack_b(d), acc[t], 0, 0, 0);
           }
-          rs_lane = __builtin_amdgcn_sdot4(a[i][q].x, 0x01010101, rs_lane, false);
-          rs_lane = __builtin_amdgcn_sdot4(a[i][q].y, 0x01010101, rs_lane, false);
-          rs_lane = __builtin_amdgcn_sdot4(a[i][q].z, 0x01010101, rs_lane, false);
-          rs_lane = __builtin_amdgcn_sdot4(a[i][q].w, 0x01010101, rs_lane, false);
+          rs_lane = bytes_sum(a[i][q], rs_lane);
         }
       }
     }
@@ -358,7 +358,6 @@ __device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs
   static_assert(EPI == EPI_SCALE ? (TPW == 1 || TPW == 2) : TPW == 2, "tiles per workgroup");
   static_assert(WAVES * 64 == 512, "one output element per thread and tile");
   __shared__ int32_t red[WAVES][TPW][8][64];
-  __shared__ int32_t red_rs[WAVES][16];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   // The two halves of a group are 8 workgroups apart, so that round-robin
   // dispatch puts them on one XCD and its L2 fetches the group's weights
@@ -465,25 +464,19 @@ __device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs
       }
     }
   }
-  if ((lane & 15) == 0)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) red_rs[wv][4 * (lane >> 4) + j] = acc_rs[j];
 #pragma unroll
   for (int t = 0; t < TPW; ++t)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      red[wv][t][j][lane] = acc[t][0][j];
-      red[wv][t][4 + j][lane] = acc[t][1][j];
+      red[wv][t][j][lane] = acc[t][0][j] - acc_rs[j];
+      red[wv][t][4 + j][lane] = acc[t][1][j] - acc_rs[j];
     }
   __syncthreads();
   const int reg = 4 * (ec >> 4) + (er & 3), src = 16 * (er >> 2) + (ec & 15);
-  int32_t rs = 0;
-#pragma unroll
-  for (int w = 0; w < WAVES; ++w) rs += red_rs[w][er];
   int32_t v[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
-    int32_t sum = -rs;
+    int32_t sum = 0;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) sum += red[w][t][reg][src];
     v[t] = sum;

@@ -194,7 +194,6 @@ struct StepArgs {
 // produces.  A 16-bit lane of an operand dword holding quantised bytes is
 // >= -127 * 256 = -32512; one of a cleared 8-byte piece is 0x8080 = -32640.
 constexpr uint32_t kTileSentinel = 0x80808080u;
-constexpr int kTileSentinelMax16 = -32513;  // a 16-bit lane at or below this is the sentinel
 
 __device__ __forceinline__ uint32_t step_tag(uint32_t E, int l, int j) { return (E << 8) | (uint32_t)(l * 4 + j); }
 
@@ -690,25 +689,36 @@ __device__ void wait_flags(const StepArgs& p, int l, int j, int r0, int n, uint3
   if (act) s_adq[r] = __uint_as_float((uint32_t)f);
 }
 
-// Running minimum of the 16-bit lanes of the operand dwords read (v_pk_min_i16);
-// a lane at or below kTileSentinelMax16 means a piece still held the sentinel.
-typedef short s16x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pk_min_i16(uint32_t a, uint32_t b) {
-  return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(s16x2_t, a),
-                                                                __builtin_bit_cast(s16x2_t, b)));
-}
-// Dwords 0 and 2 of a 16-byte operand slot each lie in one 8-byte piece,
-// written (data or sentinel) by one 8-byte store.
+// Running minimum of the operand dwords read, as signed 32-bit integers (one
+// v_min3_i32 per 16-byte slot).  Dwords 0 and 2 of a slot each lie in one
+// 8-byte piece, written (data or sentinel) by one 8-byte store.  A data
+// dword's top byte is a quantised value, at least -127, so the dword is at
+// least 0x81000000 as an integer; the sentinel dword 0x80808080 is below it.
 __device__ __forceinline__ uint32_t slot_min(uint32_t mn, const v4i& a) {
-  return pk_min_i16(pk_min_i16(mn, (uint32_t)a.x), (uint32_t)a.z);
+  return (uint32_t)min(min((int)mn, a.x), a.z);
 }
-__device__ __forceinline__ bool slot_stale(uint32_t mn) {
-  return (int)(short)(mn & 0xffffu) <= kTileSentinelMax16 || (int)(short)(mn >> 16) <= kTileSentinelMax16;
+__device__ __forceinline__ bool slot_stale(uint32_t mn) { return (int)mn < (int)0x81000000u; }
+// Rare path of an operand read that found the sentinel: polls the two 8-byte
+// pieces of one 16-byte slot (dwords 0 and 2, 4-byte loads that bypass the L1)
+// until neither is the sentinel, or the error word is set, or the wait runs
+// out (which sets it).  The slot is then read again in full.  (Reading every
+// operand again in one round instead, until none is the sentinel, keeps more
+// registers live across the loop: the instance with the decode attention then
+// spills, 914 against 873 us per step.)
+__device__ __forceinline__ void wait_tile_piece(const StepArgs& p, __amdgpu_buffer_rsrc_t xa, int off, unsigned& n,
+                                                WaitState& ws, uint32_t want) {
+  while (!ws.dead) {
+    const uint32_t d0 = __builtin_amdgcn_raw_buffer_load_b32(xa, off, 0, 16);
+    const uint32_t d2 = __builtin_amdgcn_raw_buffer_load_b32(xa, off + 8, 0, 16);
+    if (!slot_stale((uint32_t)min((int)d0, (int)d2))) break;
+    if (++n > p.spin_limit) set_error_word(p, WAIT_TILE, want);
+    if (n > p.spin_limit || ld_coherent(p.error) != 0u) {
+      ws.dead = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(BTL_STEP_POLL_SLEEP);
+  }
 }
-// Rare path of an operand read that found the sentinel: every operand of the
-// wave is read again, all in one round, with the weights (issued first), and
-// the MFMAs redone, until no piece holds the sentinel or the wait runs out
-// (which sets the error word).  One round usually finds every piece landed.
 // One BitLinear J of layer l on GEMM workgroup gi: wait for the operand
 // tile's rows, MFMA against the weights held in w, reduce the waves in LDS,
 // epilogue (tagged bf16 pairs), then issue the next BitLinear's weights into wn.
@@ -775,8 +785,8 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     const int a_voff = (lane >> 5) * 1024 + (16 * h + (lane & 15)) * 32 + ((lane >> 4) & 1) * 16;
     // Operand loads, then the MFMAs as the data arrives, each operand's
     // 16-bit lanes folded into a running minimum on the way.  A piece that
-    // still held the sentinel had not landed: then (rarely) the wave reads its
-    // operands and weights again and redoes the MFMAs, until all have landed.
+    // still held the sentinel had not landed: then (rarely) the wave waits for
+    // its pieces, reads them and its weights again, and redoes the MFMAs.
     // One more MFMA per operand, against all-ones bytes, gives the wave's
     // share of each row's sum of quantised values in every column of
     // acc_rs (the weight codes are value + 1); the body waits on its 2-bit
@@ -802,7 +812,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
 #pragma unroll
       for (int t = 0; t < TPW; ++t) acc[t][0] = acc[t][1] = (v4i){0, 0, 0, 0};
       acc_rs = (v4i){0, 0, 0, 0};
-      uint32_t mn = 0x7fff7fffu;
+      uint32_t mn = 0x7fffffffu;
 #pragma unroll
       for (int i = 0; i < NSW; ++i)
         if (i < cnt)
@@ -823,15 +833,15 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     };
     load();
     if (__any(slot_stale(mfma(w))) || ws.reread) {
+      unsigned tries = 0;
+      for (int i = 0; i < cnt; ++i)
+        for (int pp = 0; pp < 2; ++pp)
+          wait_tile_piece(p, xa, a_voff + ((wb + i) * 4 + 2 * pp) * 1024, tries, ws, want);
+      load();
       v4i wr[kStepWSlots];
       load_unit_weights<J, NSW, A>(p, sops, l, gi, wr);
-      load();
       regroup_half_weights<TPW, NSW>(wr);
-      unsigned tries = 0;
-      while (!ws.dead && __any(slot_stale(mfma(wr))) && !should_stop(p, ++tries, ws, WAIT_TILE, want)) {
-        __builtin_amdgcn_s_sleep(BTL_STEP_POLL_SLEEP);
-        load();
-      }
+      (void)mfma(wr);
     }
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
@@ -894,7 +904,7 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
 #pragma unroll
       for (int t = 0; t < TPW; ++t) acc[t] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
       acc_rs = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-      uint32_t mn = 0x7fff7fffu;
+      uint32_t mn = 0x7fffffffu;
 #pragma unroll
       for (int i = 0; i < NSW; ++i)
         if (i < cnt)
@@ -911,14 +921,13 @@ __device__ void step_gemm_op(const StepArgs& p, const StepOp* sops, int l, int g
     };
     load();
     if (__any(slot_stale(mfma(w))) || ws.reread) {
+      unsigned tries = 0;
+      for (int i = 0; i < cnt; ++i)
+        for (int q = 0; q < 4; ++q) wait_tile_piece(p, xa, a_voff + ((wb + i) * 4 + q) * 1024, tries, ws, want);
+      load();
       v4i wr[kStepWSlots];
       load_unit_weights<J, NSW, A>(p, sops, l, gi, wr);
-      load();
-      unsigned tries = 0;
-      while (!ws.dead && __any(slot_stale(mfma(wr))) && !should_stop(p, ++tries, ws, WAIT_TILE, want)) {
-        __builtin_amdgcn_s_sleep(BTL_STEP_POLL_SLEEP);
-        load();
-      }
+      (void)mfma(wr);
     }
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
