@@ -284,7 +284,8 @@ def test_persistent_full_step_matches_step_full_2b(orc):
     user at position 511 of a 512 context), the one-launch step with
     attention against step_full, bit for bit; then graph replays of the
     one-launch step from the same state give the same bits again (three
-    compared in full, 100 more on the hidden state)."""
+    compared in full, 100 more on the hidden state), and once more with every
+    GEMM unit forced onto the sentinel check's re-read path."""
     from bitnet_tt.config import BitNet2B4TConfig
     from bitnet_tt.decode import BitLinearDecodeStep
 
@@ -325,3 +326,22 @@ def test_persistent_full_step_matches_step_full_2b(orc):
             bad.append(rep)
     step.check()
     assert not bad, f"replays {bad[:10]} differ"
+    # Every GEMM unit on the sentinel check's rare path (it waits for its
+    # operand pieces, reads them and its weights again and redoes its MFMAs),
+    # forced through the step workspace's test word: the attention instance's
+    # own register allocation of that path gives the same bits.
+    key = next(k for k in N._workspaces if k[0] == "step" and k[2] == s.cuda_stream)
+    ws = N._workspaces[key]
+    off = int(N.lib().btl_decode_step_error_offset()) + 64
+    ws[off:off + 4] = torch.tensor([1, 0, 0, 0], dtype=torch.uint8, device=ws.device)
+    try:
+        _restore(step, state)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            step.step_persistent_full()
+        s.synchronize()
+        step.check()
+        _compare(_outputs(step), ref, "persistent full step, every unit on the re-read path")
+    finally:
+        ws[off:off + 4] = 0
+        torch.cuda.synchronize()
