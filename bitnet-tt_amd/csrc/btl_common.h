@@ -70,6 +70,7 @@ struct GemmPlan {
   int ngroups;    // decode: workgroups along N
   int splitk;     // decode: workgroups along K
   int mh;         // fused decode: workgroups along M (2: 16 rows each)
+  bool half16;    // fused decode, M <= 16: one 16-row workgroup per column group
   int64_t ws_bytes;
 };
 GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int epilogue, int splitk_req);

@@ -54,6 +54,7 @@ struct GemmArgs {
   int M, KS, NT, N, n_out, Mb;
   int splitk, ngroups;
   int mh;  // fused decode: 1, or 2 workgroups per column group, one per 16-row half
+  int half16;  // fused decode, M <= 16: one workgroup per column group on the 16-row body
   int xa_bytes;
   float seg_scale[BTL_MAX_SEGMENTS];
   int seg_end[BTL_MAX_SEGMENTS];
@@ -337,7 +338,8 @@ __device__ void gemm_decode_wg(const GemmArgs& p, int bid, const FusedSync& fs) 
   }
 }
 
-// GEMM workgroup of a fused row-half launch (mh = 2): rows 16h..16h+15 of
+// GEMM workgroup of a fused row-half launch (mh = 2, or half16 for M <= 16
+// with every workgroup on h = 0): rows 16h..16h+15 of
 // the token tile against TPW column tiles of 32 (scale epilogue: tiles
 // g*TPW ..; relu2: gate tile g and its up tile), on
 // v_mfma_i32_16x16x64_i8, two MFMAs (columns 0-15 and 16-31) per tile and
@@ -364,7 +366,10 @@ __device__ void gemm_decode_half(const GemmArgs& p, int bid, const FusedSync& fs
   // once.  Past the last whole block of 8 groups they pair up r apart.
   const int g8 = p.ngroups & ~7;
   int g, h;
-  if (bid < 2 * g8) {
+  if (p.half16) {  // M <= 16: one workgroup per group, rows 0..15
+    g = bid;
+    h = 0;
+  } else if (bid < 2 * g8) {
     g = ((bid >> 4) << 3) | (bid & 7);
     h = (bid >> 3) & 1;
   } else {
@@ -1349,6 +1354,11 @@ static GemmPlan plan_fused(int64_t M, int64_t K, int64_t N, int epilogue, int sp
     // 9.9 us against 8.95 us for the whole-tile workgroups at 2560 -> 2 x 6912.
     // The 16-row MFMA halves the MFMA time per unpacked weight dword, so the
     // 2-bit unpack on the VALU then sets the pace.
+  } else if (pl.fused && M <= 16 && pl.splitk == 1) {
+    // Every row in the first half: one workgroup per column group runs the
+    // 16-row body on it, so no MFMA or operand fetch is spent on the 16
+    // padding rows of the whole-tile body.
+    pl.half16 = true;
   }
   return pl;
 }
@@ -1470,6 +1480,7 @@ static GemmArgs gemm_args(const int8_t* xa, const float* a_dq, const int32_t* ro
   a.acc_out = acc_out;
   a.splitk = pl.splitk;
   a.mh = pl.mh == 2 ? 2 : 1;
+  a.half16 = pl.half16 ? 1 : 0;
   a.ngroups = pl.ngroups;
   if (pl.splitk > 1) {  // decode split-K, or prefill split-K (per tile)
     a.ws_cnt = reinterpret_cast<uint32_t*>(ws);
@@ -1627,7 +1638,7 @@ static int launch_gemm(const GemmArgs& a, int epilogue, const GemmPlan& pl, hipS
 template <bool NORM, int CPT>
 static int launch_fused_epi(int epilogue, const GemmPlan& pl, int nsb, dim3 grid, hipStream_t s, const GemmArgs& g,
                             const ActArgs& a, const FusedSync& fs) {
-  if (pl.mh == 2) {
+  if (pl.mh == 2 || pl.half16) {
     if (epilogue == BTL_EPI_RELU2_MUL) return launch_fused_nsb<2, EPI_RELU2, NORM, CPT, true>(nsb, grid, s, g, a, fs);
     if (pl.tpw == 2) return launch_fused_nsb<2, EPI_SCALE, NORM, CPT, true>(nsb, grid, s, g, a, fs);
     return launch_fused_nsb<1, EPI_SCALE, NORM, CPT, true>(nsb, grid, s, g, a, fs);

@@ -456,10 +456,14 @@ def test_fused_decode_handshake_clean(orc):
 @pytest.mark.parametrize("m,k,n,epi", [(32, 2560, 2560, "none"), (17, 6912, 2560, "none"), (24, 2560, 640, "none"),
                                         (32, 6912, 96, "none"), (32, 2560, 3840, "qkv"), (17, 2560, 3840, "qkv"),
                                         (32, 2560, 13824, "relu2_mul"), (19, 2560, 13824, "relu2_mul"),
-                                        (32, 2560, 1024, "relu2_mul"), (24, 2560, 1024, "relu2_mul")])
+                                        (32, 2560, 1024, "relu2_mul"), (24, 2560, 1024, "relu2_mul"),
+                                        (16, 2560, 3840, "qkv"), (1, 6912, 2560, "none"), (8, 2560, 13824, "relu2_mul"),
+                                        (13, 2560, 2560, "none"), (16, 6912, 96, "none")])
 def test_fused_row_halves_bit_exact(orc, m, k, n, epi):
-    """Single-launch BitLinear with more than 16 rows.  Two GEMM workgroups
-    take each column group, one per 16-row half, in these cases:
+    """Single-launch BitLinear on the 16-row body.  At M <= 16 one GEMM
+    workgroup per column group takes rows 0..15 (every shape).  With more
+    than 16 rows two take each column group, one per 16-row half, in these
+    cases:
     - the o_proj and down shapes of the 2B model (one column tile a group,
       scale and residual epilogue);
     - fused QKV (two tiles a group, three scale segments);
