@@ -391,7 +391,7 @@ __device__ __forceinline__ void pairs_to_floats(const uint32_t (&pr)[C][4], floa
 // as btl_bitlinear_fused.  K is a multiple of 128 (checked on the host), so
 // the row's chunks fill its slice of the tile.
 template <int C>
-__device__ void publish_row(const StepArgs& p, int l, int j, int m, int K, int KS, float (&v)[C][8],
+__device__ void publish_row(const StepArgs& p, int l, int j, int m, int K, float (&v)[C][8],
                             const float (&g)[C][8], uint32_t want, float* s_sum, float* s_max) {
   const int tid = threadIdx.x;
   const int nch = K >> 3;
@@ -477,7 +477,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
   const int tid = threadIdx.x;
   const bool live = m < p.M;
   const int nh = p.H >> 3, nf = p.F >> 3;
-  WaitState ws{false};
+  WaitState ws{false, false};
   uint32_t hid[CH][4];
   {
     uint4 raw = make_uint4(0u, 0u, 0u, 0u);
@@ -497,7 +497,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       float v[CH][8];
       pairs_to_floats<CH>(hid, v);
       STEP_TRACE(l, 0);
-      publish_row<CH>(p, l, S_QKV, m, p.H, p.KSH, v, g_qkv, step_tag(E, l, S_QKV), s_sum, s_max);
+      publish_row<CH>(p, l, S_QKV, m, p.H, v, g_qkv, step_tag(E, l, S_QKV), s_sum, s_max);
       STEP_TRACE(l, 1);
       if (l > 0) clear_tile_share<CF>(tile_of(p, l - 1, S_DN), m, p.KSF);
     }
@@ -537,7 +537,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       }
       float v[CH][8];
       pairs_to_floats<CH>(pr, v);
-      publish_row<CH>(p, l, S_O, m, p.H, p.KSH, v, g, step_tag(E, l, S_O), s_sum, s_max);
+      publish_row<CH>(p, l, S_O, m, p.H, v, g, step_tag(E, l, S_O), s_sum, s_max);
       STEP_TRACE(l, 3);
       clear_tile_share<CH>(tile_of(p, l, S_QKV), m, p.KSH);
     }
@@ -552,7 +552,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       residual_add(hid[0], pr[0], live);
       float v[CH][8];
       pairs_to_floats<CH>(hid, v);
-      publish_row<CH>(p, l, S_GU, m, p.H, p.KSH, v, g, step_tag(E, l, S_GU), s_sum, s_max);
+      publish_row<CH>(p, l, S_GU, m, p.H, v, g, step_tag(E, l, S_GU), s_sum, s_max);
       STEP_TRACE(l, 5);
       clear_tile_share<CH>(tile_of(p, l, S_O), m, p.KSH);
     }
@@ -566,7 +566,7 @@ __device__ void step_row(const StepArgs& p, const StepOp* sops, int m, uint32_t 
       STEP_TRACE(l, 6);
       float v[CF][8];
       pairs_to_floats<CF>(pr, v);
-      publish_row<CF>(p, l, S_DN, m, p.F, p.KSF, v, g, step_tag(E, l, S_DN), s_sum, s_max);
+      publish_row<CF>(p, l, S_DN, m, p.F, v, g, step_tag(E, l, S_DN), s_sum, s_max);
       STEP_TRACE(l, 7);
       clear_tile_share<CH>(tile_of(p, l, S_GU), m, p.KSH);
     }
@@ -1151,7 +1151,7 @@ __global__ __launch_bounds__(512) void k_decode_step(StepArgs p) {
 // is the latency floor that the chain of 120 dependent hand-off pairs sets.
 template <int CF>
 __device__ void floor_row(const StepArgs& p, int m, uint32_t E) {
-  WaitState ws{false};
+  WaitState ws{false, false};
   for (int l = 0; l < p.L; ++l)
     for (int j = 0; j < kStepOps; ++j) {
       if (l > 0 || j > 0) {  // the words this row stage waits for in the step
@@ -1209,7 +1209,7 @@ __global__ __launch_bounds__(512) void k_decode_step_floor(StepArgs p) {
   if (b < kStepRows) {
     floor_row<CF>(p, b, E);
   } else {
-    WaitState ws{false};
+    WaitState ws{false, false};
     for (int l = 0; l < p.L; ++l) {
       floor_gemm_op<S_QKV>(p, l, b - kStepRows, E, s_adq, ws);
       floor_gemm_op<S_O>(p, l, b - kStepRows, E, s_adq, ws);
